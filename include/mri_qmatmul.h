@@ -1,0 +1,180 @@
+/*
+ * mri_qmatmul.h — C ABI of the MI355X (gfx950) quantized-matmul library.
+ *
+ * Drop-in boundary for mini-rust-inference's quantized matmul hot path
+ * (crate llm-inference-engine, lib llm_engine).  Each entry point names the
+ * reference item it replaces as src/<file>:<line>.  The reference functions
+ * take host slices / Tensor<f32> and return Result<Tensor<f32>, TensorError>;
+ * here every tensor argument is a DEVICE pointer (row-major, contiguous),
+ * outputs are caller-owned device buffers, and work is enqueued on `stream`
+ * (a hipStream_t; NULL = the default stream).  Weights are uploaded once into
+ * opaque device-resident handles, the GPU counterpart of the reference's
+ * long-lived QuantizedMatrix / Q8_0WeightMatrix.
+ *
+ * Errors mirror TensorError (src/tensor/error.rs:7-29): InvalidShape and
+ * ShapeMismatch are returned in the same situations and the same check order
+ * as the reference; mri_last_error() returns the thread-local `reason`.
+ *
+ * Numerics contract: int32 accumulators are bit-exact.  The per-channel INT8
+ * f32 epilogue ((f32)acc * s_a) * s_w and the Q8_0 block-ordered f32 sum are
+ * bit-exact against the reference's evaluation order.  Q4_0 (W4A32) sums in
+ * a different order and is within 1e-5 * max(|ref|, sum|terms|).
+ *
+ * Concurrency: calls are asynchronous on `stream`.  Handles are immutable
+ * after creation and may be shared by calls on any stream.  Internal scratch
+ * (activation quantization) is kept per (device, stream), so concurrent calls
+ * on different streams do not interfere.
+ */
+#ifndef MRI_QMATMUL_H
+#define MRI_QMATMUL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum mri_status {
+    MRI_OK = 0,
+    MRI_ERR_INVALID_SHAPE = 1,    /* TensorError::InvalidShape  */
+    MRI_ERR_SHAPE_MISMATCH = 2,   /* TensorError::ShapeMismatch */
+    MRI_ERR_INVALID_ARGUMENT = 3, /* null pointer / bad handle (no Rust analogue: borrowck) */
+    MRI_ERR_HIP = 4,              /* HIP runtime error (allocation, launch) */
+    MRI_ERR_UNSUPPORTED = 5       /* device is not gfx950 */
+} mri_status;
+
+/* Thread-local message for the last non-OK status on this thread
+ * (TensorError's `reason`, or the HIP error string). */
+const char *mri_last_error(void);
+/* Library version string. */
+const char *mri_version(void);
+
+/* ===================================================================== */
+/* Device-resident weights                                                */
+/* ===================================================================== */
+
+/* QuantizedMatrix, src/quant/int8/per_channel.rs:31-40: data [n_out*k_in]
+ * int8 row-major, scales [n_out] f32.  Host pointers; uploaded and repacked
+ * once into the kernel's tiled layout. */
+typedef struct mri_qmatrix mri_qmatrix;
+mri_status mri_qmatrix_create(const int8_t *data, const float *scales,
+                              size_t n_out, size_t k_in, mri_qmatrix **out);
+/* Same from DEVICE pointers (e.g. the output of mri_quantize_per_channel). */
+mri_status mri_qmatrix_create_device(const int8_t *data_dev,
+                                     const float *scales_dev, size_t n_out,
+                                     size_t k_in, void *stream,
+                                     mri_qmatrix **out);
+/* Reads the weights back in the reference layout (host pointers). */
+mri_status mri_qmatrix_read(const mri_qmatrix *w, int8_t *data, float *scales);
+size_t mri_qmatrix_n_out(const mri_qmatrix *w);
+size_t mri_qmatrix_k_in(const mri_qmatrix *w);
+/* Device bytes held by the handle (tiled quants + scales, with padding). */
+size_t mri_qmatrix_device_bytes(const mri_qmatrix *w);
+void mri_qmatrix_destroy(mri_qmatrix *w);
+
+/* Q8_0WeightMatrix::from_raw_bytes, src/ops/matmul/q8_direct.rs:80-107:
+ * raw GGUF Q8_0 blocks ([f16 d][32 x i8], 34 bytes, block (n,b) at
+ * (n*k_in/32 + b)*34).  InvalidShape when k_in % 32 != 0 or
+ * len != n_out*(k_in/32)*34 (n_out == 0 is accepted).  Host pointer. */
+typedef struct mri_q8_0_matrix mri_q8_0_matrix;
+mri_status mri_q8_0_matrix_from_raw_bytes(const uint8_t *data, size_t len,
+                                          size_t n_out, size_t k_in,
+                                          mri_q8_0_matrix **out);
+/* Same from a DEVICE pointer to the raw blocks (e.g. an uploaded GGUF slice). */
+mri_status mri_q8_0_matrix_from_raw_device(const uint8_t *data_dev,
+                                           size_t len, size_t n_out,
+                                           size_t k_in, void *stream,
+                                           mri_q8_0_matrix **out);
+/* Reads the raw 34-byte blocks back (host pointer, len bytes). */
+mri_status mri_q8_0_matrix_read_raw(const mri_q8_0_matrix *w, uint8_t *data,
+                                    size_t len);
+size_t mri_q8_0_matrix_n_out(const mri_q8_0_matrix *w);
+size_t mri_q8_0_matrix_k_in(const mri_q8_0_matrix *w);
+size_t mri_q8_0_matrix_device_bytes(const mri_q8_0_matrix *w);
+void mri_q8_0_matrix_destroy(mri_q8_0_matrix *w);
+
+/* ===================================================================== */
+/* Quantizers (device pointers)                                          */
+/* ===================================================================== */
+
+/* quantize_symmetric, src/quant/int8/symmetric.rs:42-57: one per-tensor
+ * scale over all `len` values; writes q[len] and scale[0] (device). */
+mri_status mri_quantize_symmetric(const float *x, size_t len, int8_t *q,
+                                  float *scale, void *stream);
+/* quantize_symmetric applied to each row of [m,k] separately (the per-row
+ * use in matmul_q8_0_direct, src/ops/matmul/q8_direct.rs:264). */
+mri_status mri_quantize_symmetric_rows(const float *x, size_t m, size_t k,
+                                       int8_t *q, float *scales, void *stream);
+/* quantize_per_channel, src/quant/int8/per_channel.rs:98-128 (weight prep);
+ * InvalidShape where the reference panics (len != n_out*k_in). */
+mri_status mri_quantize_per_channel(const float *w, size_t len, size_t n_out,
+                                    size_t k_in, int8_t *data, float *scales,
+                                    void *stream);
+
+/* ===================================================================== */
+/* Hot path (device pointers)                                            */
+/* ===================================================================== */
+
+/* dot_i8_avx2, src/ops/matmul/int8_avx2.rs:136-148: *out = sum a[i]*b[i]. */
+mri_status mri_dot_i8(const int8_t *a, const int8_t *b, size_t len,
+                      int32_t *out, void *stream);
+
+/* matmul_int8, src/ops/matmul/int8.rs:61-98 (also matmul_int8_avx2
+ * int8_avx2.rs:174, matmul_int8_neon int8_neon.rs:158, matmul_int8_parallel
+ * parallel.rs:308 — same signature and results):
+ *   out[m,n] = ((f32)sum_k act_q[m,k]*w[n,k] * act_scale) * scales[n].
+ * InvalidShape when act_q_len != m*k_in.  out is [m, n_out] f32;
+ * acc_out (nullable) receives the [m, n_out] int32 accumulators. */
+mri_status mri_matmul_int8(const int8_t *act_q, size_t act_q_len,
+                           float act_scale, const mri_qmatrix *w, size_t m,
+                           float *out, int32_t *acc_out, void *stream);
+
+/* matmul_int8 with one activation scale per row (act_scales: device [m]).
+ * No reference counterpart: the per-row-quantized prefill configuration. */
+mri_status mri_matmul_int8_rows(const int8_t *act_q, size_t act_q_len,
+                                const float *act_scales, const mri_qmatrix *w,
+                                size_t m, float *out, int32_t *acc_out,
+                                void *stream);
+
+/* matmul_int8_from_f32, src/ops/matmul/int8.rs:113-143: `input` is a
+ * contiguous f32 tensor with `ndim` dims (InvalidShape unless ndim == 2);
+ * ShapeMismatch{expected:[m,k_in], got:[m,k]} when dims[1] != k_in; then one
+ * per-tensor quantize_symmetric over the whole [m,k] and matmul_int8.
+ * Optional outputs (nullable, device): act_q_out [m*k], act_scale_out [1],
+ * acc_out [m*n_out]. */
+mri_status mri_matmul_int8_from_f32(const float *input, const size_t *dims,
+                                    size_t ndim, const mri_qmatrix *w,
+                                    float *out, int8_t *act_q_out,
+                                    float *act_scale_out, int32_t *acc_out,
+                                    void *stream);
+
+/* matmul_q8_0_direct, src/ops/matmul/q8_direct.rs:229-289: per-row
+ * quantize_symmetric of `input` [m,k], per-block int32 dots, and
+ *   out[m,n] = sum over b in block order of ((f32)dot[m,n,b]*s_a[m])*d[n,b].
+ * InvalidShape unless ndim == 2; ShapeMismatch when dims[1] != k_in.
+ * Optional outputs (nullable, device): block_dots_out [m, n_out, k_in/32]
+ * int32, act_scales_out [m]. */
+mri_status mri_matmul_q8_0_direct(const float *input, const size_t *dims,
+                                  size_t ndim, const mri_q8_0_matrix *w,
+                                  float *out, int32_t *block_dots_out,
+                                  float *act_scales_out, void *stream);
+
+/* matmul_q4_0_dequant, src/ops/matmul/q4_0.rs:94-181 (W4A32): weight_q4 is
+ * a DEVICE pointer to raw Q4_0 blocks ([f16 d][16 bytes], 18 bytes, element
+ * 2i = low nibble of byte i minus 8, element 2i+1 = high nibble minus 8).
+ * Check order as the reference: ndim != 2 -> InvalidShape; dims[1] != k ->
+ * ShapeMismatch; k % 32 -> InvalidShape; len != n_out*(k/32)*18 ->
+ * InvalidShape.  out is [m, n_out] f32. */
+mri_status mri_matmul_q4_0_dequant(const float *input, const size_t *dims,
+                                   size_t ndim, const uint8_t *weight_q4,
+                                   size_t weight_len, size_t n_out, size_t k,
+                                   float *out, void *stream);
+
+/* Waits for all work enqueued on `stream`. */
+mri_status mri_synchronize(void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,163 @@
+// common.hpp — shared definitions of the gfx950 quantized-matmul library.
+//
+// Device weight layouts (chosen at upload time, not visible through the ABI):
+//
+//  * Per-channel INT8 (QuantizedMatrix, per_channel.rs:31-40) is stored as
+//    "MFMA tiles": the output rows are grouped in tiles of 16 and K in chunks
+//    of 64.  Chunk (T, p) is 1 KiB at byte offset (T * P + p) * 1024 with
+//    P = Kp / 64, Kp = K rounded up to 64.  Inside a chunk, lane l (0..63)
+//    owns 16 bytes at l * 16: row 16*T + (l % 16), k = 64*p + 16*(l / 16) +
+//    [0, 16).  This is exactly the B operand of v_mfma_i32_16x16x64_i8 for
+//    lane l, so one global_load_dwordx4 per lane per chunk feeds one MFMA and
+//    a wave reads 1 KiB contiguous bytes per instruction.  Scales: f32 [Np].
+//
+//  * Q8_0 (Q8_0WeightMatrix, q8_direct.rs:60-69) is split into quants and
+//    scales.  Quants use the same 1 KiB chunks, but lane l's 16 bytes hold
+//    two 8-byte B operands of v_mfma_i32_16x16x32_i8 (one MFMA per 32-element
+//    block): bytes [8h, 8h+8) = quants [8g, 8g+8) of block 2p+h of row
+//    16T + (l % 16), g = l / 16.  Kp = K rounded up to 256.  Scales stay
+//    f16 (2 bytes per block, as in GGUF) in groups of 8 blocks:
+//    [T][Kp/256][16 rows][8 blocks], so one 16-byte load gives a lane the
+//    scales of 8 consecutive blocks of its row.
+//
+//  * Activations quantized by the library are written to a per-(device,
+//    stream) scratch in [M][Kp] int8 rows (zero padded).  For Q8_0 the 64
+//    bytes of each chunk are permuted to match the weight chunk:
+//    element kk of a chunk sits at q8_perm(kk).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "mri_qmatmul.h"
+
+namespace mri {
+
+constexpr int kTileN = 16;        // output rows per MFMA tile
+constexpr int kChunkK = 64;       // K elements per 1 KiB chunk
+constexpr int kQK = 32;           // Q8_0 / Q4_0 block elements
+constexpr int kQ8Bytes = 34;      // raw Q8_0 block bytes
+constexpr int kQ4Bytes = 18;      // raw Q4_0 block bytes
+constexpr int kQ8ScaleGroup = 8;  // blocks per scale group (16 bytes of f16)
+
+inline size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
+
+// Position of element kk (0..63) of a Q8_0 chunk inside the permuted
+// 64-byte activation chunk: [g = 0..3][h = 0..1][8 bytes].
+__host__ __device__ inline int q8_perm(int kk) {
+    return ((kk >> 3) & 3) * 16 + (kk >> 5) * 8 + (kk & 7);
+}
+
+struct QMatrixDev {
+    size_t n_out = 0, k_in = 0;
+    size_t n_tiles = 0;     // ceil(n_out / 16)
+    size_t kp = 0;          // K padded to 64
+    int8_t *tiles = nullptr;  // n_tiles * (kp/64) KiB
+    float *scales = nullptr;  // n_tiles * 16
+    int device = 0;
+};
+
+struct Q8MatrixDev {
+    size_t n_out = 0, k_in = 0;
+    size_t n_blocks = 0;    // k_in / 32
+    size_t n_tiles = 0;
+    size_t kp = 0;          // K padded to 256
+    int8_t *tiles = nullptr;     // n_tiles * (kp/64) KiB
+    uint16_t *scales = nullptr;  // n_tiles * (kp/256) * 16 * 8 f16
+    int device = 0;
+};
+
+// Exact f16 -> f32 decode (v_cvt_f32_f16), the f16_to_f32 of
+// gguf/quantization.rs:416-459 for every finite input.
+__device__ inline float f16_bits_to_f32(unsigned bits) {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)bits);
+}
+
+// ---- error handling ------------------------------------------------------
+mri_status set_error(mri_status st, const std::string &msg);
+mri_status hip_error(hipError_t e, const char *what);
+
+#define MRI_HIP(call)                                               \
+    do {                                                            \
+        hipError_t _e = (call);                                     \
+        if (_e != hipSuccess) return ::mri::hip_error(_e, #call);   \
+    } while (0)
+
+#define MRI_LAUNCHED(what)                                          \
+    do {                                                            \
+        hipError_t _e = hipGetLastError();                          \
+        if (_e != hipSuccess) return ::mri::hip_error(_e, what);    \
+    } while (0)
+
+// ---- per-(device, stream) scratch ----------------------------------------
+// Grow-only device buffer; growth synchronizes `stream` before freeing the
+// old buffer, so work already enqueued on it never sees freed memory.
+mri_status scratch_get(hipStream_t stream, size_t bytes, void **ptr);
+
+// ---- kernel launchers (defined in the .hip files) -------------------------
+// quantize.hip
+mri_status launch_quantize_tensor(const float *x, size_t m, size_t k,
+                                  size_t ld_out, bool q8_perm_layout,
+                                  int8_t *q_pad, int8_t *q_plain,
+                                  float *scale, float *partials,
+                                  hipStream_t s);
+mri_status launch_quantize_rows(const float *x, size_t m, size_t k,
+                                size_t ld_out, bool q8_perm_layout,
+                                int8_t *q_pad, int8_t *q_plain,
+                                float *scales, hipStream_t s);
+mri_status launch_quantize_per_channel(const float *w, size_t n, size_t k,
+                                       int8_t *data, float *scales,
+                                       hipStream_t s);
+mri_status launch_pad_rows(const int8_t *src, size_t m, size_t k, size_t kp,
+                           int8_t *dst, hipStream_t s);
+mri_status launch_dot_i8(const int8_t *a, const int8_t *b, size_t n,
+                         int32_t *out, hipStream_t s);
+size_t quantize_partials_count(size_t n);
+
+// repack.hip
+mri_status launch_repack_int8(const int8_t *data, const float *scales,
+                              QMatrixDev &w, hipStream_t s);
+mri_status launch_repack_q8_0(const uint8_t *raw, Q8MatrixDev &w,
+                              hipStream_t s);
+
+// skinny.hip: M <= 32 rows per launch (larger M loops), one wave per tile.
+// act: [M][kp] int8 (Q8_0: chunk-permuted).  Activation scale of row m is
+// sa_ptr[m * sa_stride] when sa_ptr != nullptr, else sa_value.
+mri_status launch_skinny_int8(const int8_t *act, size_t m, const float *sa_ptr,
+                              int sa_stride, float sa_value,
+                              const QMatrixDev &w, float *out,
+                              int32_t *acc_out, hipStream_t s);
+mri_status launch_skinny_q8_0(const int8_t *act, size_t m,
+                              const float *sa_ptr, const Q8MatrixDev &w,
+                              float *out, int32_t *block_dots,
+                              hipStream_t s);
+// gemv.hip: M <= 4, K split over S waves per 16-row tile, weights streamed
+// through a per-wave ring of loads.  Activations come either as one f32 row
+// x (quantized in the kernel; requires gemv_fusable, M == 1; optional
+// act_q_out [k] and scale_out [1]) or as quantized rows act [m][kp] (Q8_0:
+// chunk-permuted) with their scales.
+bool gemv_int8_supported(bool fused, size_t m, size_t n_tiles, size_t k, size_t kp);
+bool gemv_q8_supported(bool fused, size_t m, size_t n_tiles, size_t k, size_t kp);
+bool gemv_fusable(size_t m, size_t k, const float *x);
+mri_status launch_gemv_int8(const float *x, const int8_t *act, size_t m,
+                            const float *sa_ptr, int sa_stride, float sa_value,
+                            const QMatrixDev &w, float *out, int8_t *act_q_out,
+                            float *scale_out, int32_t *acc_out, hipStream_t s);
+mri_status launch_gemv_q8_0(const float *x, const int8_t *act, size_t m,
+                            const float *sa_rows, const Q8MatrixDev &w, float *out,
+                            int32_t *block_dots, float *scales_out, hipStream_t s);
+
+// gemm.hip: prefill-sized M on MFMA with LDS tiles.
+mri_status launch_gemm_int8(const int8_t *act, size_t m, const float *sa_ptr,
+                            int sa_stride, float sa_value, const QMatrixDev &w,
+                            float *out, int32_t *acc_out, hipStream_t s);
+
+// q4_0.hip
+mri_status launch_q4_0_dequant(const float *x, size_t m, size_t k,
+                               const uint8_t *w, size_t n_out, float *out,
+                               hipStream_t s);
+
+}  // namespace mri

@@ -1,0 +1,232 @@
+// quantize.hip — activation / weight quantizers on gfx950.
+//
+// All of them evaluate the reference's scalar formula exactly
+// (quant/int8/symmetric.rs:42-57, per_channel.rs:98-128):
+//   max_abs = fold(0, f32::max)(|v|)          (fmaxf ignores NaN as f32::max)
+//   scale   = max_abs == 0 ? 1 : max_abs / 127 (correctly rounded divide)
+//   inv     = 1 / scale                         (correctly rounded divide)
+//   q       = clamp(round_half_away(v * inv), -127, 127) as i8, NaN -> 0
+// The library is compiled with -ffp-contract=off and correctly rounded
+// f32 division, so each operation rounds exactly once, as in Rust.
+#include "common.hpp"
+
+namespace mri {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxPartials = 1024;
+
+__device__ inline int8_t round_clamp_i8(float y) {
+    float r = roundf(y);              // ties away from zero, like f32::round
+    if (r != r) return 0;             // `NaN as i8` == 0
+    r = fminf(fmaxf(r, -127.0f), 127.0f);
+    return (int8_t)(int)r;
+}
+
+__device__ inline float scale_of(float max_abs) {
+    return max_abs == 0.0f ? 1.0f : __fdiv_rn(max_abs, 127.0f);
+}
+
+// Block-wide max of non-negative floats (NaN-free inputs are not required:
+// fmaxf drops NaN operands).
+__device__ inline float block_max(float v, float *red) {
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float r = 0.0f;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) r = fmaxf(r, red[w]);
+    __syncthreads();
+    return r;
+}
+
+__global__ __launch_bounds__(kThreads) void k_absmax_partial(
+    const float *__restrict__ x, size_t n, float *__restrict__ partials) {
+    __shared__ float red[kThreads / 64];
+    float m = 0.0f;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if ((reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+        const size_t n4 = n / 4;
+        const float4 *x4 = reinterpret_cast<const float4 *>(x);
+        for (size_t j = i; j < n4; j += stride) {
+            float4 v = x4[j];
+            m = fmaxf(m, fabsf(v.x));
+            m = fmaxf(m, fabsf(v.y));
+            m = fmaxf(m, fabsf(v.z));
+            m = fmaxf(m, fabsf(v.w));
+        }
+        for (size_t j = n4 * 4 + i; j < n; j += stride) m = fmaxf(m, fabsf(x[j]));
+    } else {
+        for (size_t j = i; j < n; j += stride) m = fmaxf(m, fabsf(x[j]));
+    }
+    m = block_max(m, red);
+    if (threadIdx.x == 0) partials[blockIdx.x] = m;
+}
+
+// Quantize [m,k] with the per-tensor scale reduced from `partials`.
+// q_pad: [m][ld] (ld >= k, zero padded; chunk-permuted when perm) or null;
+// q_plain: [m*k] row-major or null.
+__global__ __launch_bounds__(kThreads) void k_quantize_tensor(
+    const float *__restrict__ x, size_t m, size_t k, size_t ld, int perm,
+    const float *__restrict__ partials, int n_partials,
+    int8_t *__restrict__ q_pad, int8_t *__restrict__ q_plain,
+    float *__restrict__ scale_out) {
+    __shared__ float red[kThreads / 64];
+    float mx = 0.0f;
+    for (int i = threadIdx.x; i < n_partials; i += blockDim.x)
+        mx = fmaxf(mx, partials[i]);
+    mx = block_max(mx, red);
+    const float scale = scale_of(mx);
+    const float inv = __fdiv_rn(1.0f, scale);
+    if (blockIdx.x == 0 && threadIdx.x == 0 && scale_out) *scale_out = scale;
+    const size_t total = m * ld;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += stride) {
+        const size_t r = e / ld, kk = e - r * ld;
+        int8_t q = 0;
+        if (kk < k) {
+            q = round_clamp_i8(x[r * k + kk] * inv);
+            if (q_plain) q_plain[r * k + kk] = q;
+        }
+        if (q_pad) {
+            size_t pos = kk;
+            if (perm) pos = (kk & ~(size_t)63) + q8_perm((int)(kk & 63));
+            q_pad[r * ld + pos] = q;
+        }
+    }
+}
+
+// One block per row: quantize_symmetric of each row separately.
+__global__ __launch_bounds__(kThreads) void k_quantize_rows(
+    const float *__restrict__ x, size_t k, size_t ld, int perm,
+    int8_t *__restrict__ q_pad, int8_t *__restrict__ q_plain,
+    float *__restrict__ scales) {
+    __shared__ float red[kThreads / 64];
+    const size_t r = blockIdx.x;
+    const float *row = x + r * k;
+    float mx = 0.0f;
+    for (size_t i = threadIdx.x; i < k; i += blockDim.x)
+        mx = fmaxf(mx, fabsf(row[i]));
+    mx = block_max(mx, red);
+    const float scale = scale_of(mx);
+    const float inv = __fdiv_rn(1.0f, scale);
+    if (threadIdx.x == 0 && scales) scales[r] = scale;
+    for (size_t kk = threadIdx.x; kk < ld; kk += blockDim.x) {
+        int8_t q = 0;
+        if (kk < k) {
+            q = round_clamp_i8(row[kk] * inv);
+            if (q_plain) q_plain[r * k + kk] = q;
+        }
+        if (q_pad) {
+            size_t pos = kk;
+            if (perm) pos = (kk & ~(size_t)63) + q8_perm((int)(kk & 63));
+            q_pad[r * ld + pos] = q;
+        }
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void k_pad_rows(
+    const int8_t *__restrict__ src, size_t m, size_t k, size_t kp,
+    int8_t *__restrict__ dst) {
+    const size_t total = m * kp;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += stride) {
+        const size_t r = e / kp, kk = e - r * kp;
+        dst[e] = kk < k ? src[r * k + kk] : (int8_t)0;
+    }
+}
+
+// Single-block int32 dot (wrapping arithmetic, as Rust release i32 adds).
+__global__ __launch_bounds__(kThreads) void k_dot_i8(
+    const int8_t *__restrict__ a, const int8_t *__restrict__ b, size_t n,
+    int32_t *__restrict__ out) {
+    __shared__ uint32_t red[kThreads / 64];
+    uint32_t s = 0;
+    for (size_t i = threadIdx.x; i < n; i += blockDim.x)
+        s += (uint32_t)((int32_t)a[i] * (int32_t)b[i]);
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t t = 0;
+        for (int w = 0; w < kThreads / 64; ++w) t += red[w];
+        *out = (int32_t)t;
+    }
+}
+
+inline int grid_for(size_t n, int per_thread = 1) {
+    size_t g = (n + (size_t)kThreads * per_thread - 1) / ((size_t)kThreads * per_thread);
+    if (g < 1) g = 1;
+    if (g > 4096) g = 4096;
+    return (int)g;
+}
+
+}  // namespace
+
+size_t quantize_partials_count(size_t n) {
+    size_t g = (n + (size_t)kThreads * 16 - 1) / ((size_t)kThreads * 16);
+    if (g < 1) g = 1;
+    if (g > (size_t)kMaxPartials) g = kMaxPartials;
+    return g;
+}
+
+mri_status launch_quantize_tensor(const float *x, size_t m, size_t k,
+                                  size_t ld_out, bool q8_perm_layout,
+                                  int8_t *q_pad, int8_t *q_plain,
+                                  float *scale, float *partials,
+                                  hipStream_t s) {
+    const size_t n = m * k;
+    const int g = (int)quantize_partials_count(n);
+    hipLaunchKernelGGL(k_absmax_partial, dim3(g), dim3(kThreads), 0, s, x, n,
+                       partials);
+    MRI_LAUNCHED("k_absmax_partial");
+    hipLaunchKernelGGL(k_quantize_tensor, dim3(grid_for(m * (q_pad ? ld_out : k), 4)),
+                       dim3(kThreads), 0, s, x, m, k, q_pad ? ld_out : k,
+                       q8_perm_layout ? 1 : 0, partials, g, q_pad, q_plain,
+                       scale);
+    MRI_LAUNCHED("k_quantize_tensor");
+    return MRI_OK;
+}
+
+mri_status launch_quantize_rows(const float *x, size_t m, size_t k,
+                                size_t ld_out, bool q8_perm_layout,
+                                int8_t *q_pad, int8_t *q_plain,
+                                float *scales, hipStream_t s) {
+    if (m == 0) return MRI_OK;
+    hipLaunchKernelGGL(k_quantize_rows, dim3((unsigned)m), dim3(kThreads), 0, s,
+                       x, k, q_pad ? ld_out : k, q8_perm_layout ? 1 : 0, q_pad,
+                       q_plain, scales);
+    MRI_LAUNCHED("k_quantize_rows");
+    return MRI_OK;
+}
+
+mri_status launch_quantize_per_channel(const float *w, size_t n, size_t k,
+                                       int8_t *data, float *scales,
+                                       hipStream_t s) {
+    if (n == 0) return MRI_OK;
+    hipLaunchKernelGGL(k_quantize_rows, dim3((unsigned)n), dim3(kThreads), 0, s,
+                       w, k, k, 0, data, (int8_t *)nullptr, scales);
+    MRI_LAUNCHED("k_quantize_rows(per_channel)");
+    return MRI_OK;
+}
+
+mri_status launch_pad_rows(const int8_t *src, size_t m, size_t k, size_t kp,
+                           int8_t *dst, hipStream_t s) {
+    if (m * kp == 0) return MRI_OK;
+    hipLaunchKernelGGL(k_pad_rows, dim3(grid_for(m * kp, 4)), dim3(kThreads), 0,
+                       s, src, m, k, kp, dst);
+    MRI_LAUNCHED("k_pad_rows");
+    return MRI_OK;
+}
+
+mri_status launch_dot_i8(const int8_t *a, const int8_t *b, size_t n,
+                         int32_t *out, hipStream_t s) {
+    hipLaunchKernelGGL(k_dot_i8, dim3(1), dim3(kThreads), 0, s, a, b, n, out);
+    MRI_LAUNCHED("k_dot_i8");
+    return MRI_OK;
+}
+
+}  // namespace mri

@@ -1,0 +1,136 @@
+// repack.hip — one-time weight upload transforms into the MFMA tile layouts
+// described in common.hpp.  Run once per weight handle, off the hot path.
+#include "common.hpp"
+
+namespace mri {
+namespace {
+
+constexpr int kThreads = 256;
+
+// One thread per 16-byte lane piece of the per-channel INT8 tiles.
+__global__ __launch_bounds__(kThreads) void k_repack_int8(
+    const int8_t *__restrict__ data, size_t n, size_t k, size_t n_tiles,
+    size_t P, int8_t *__restrict__ tiles) {
+    const size_t total = n_tiles * P * 64;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += stride) {
+        const size_t lane = e & 63, tp = e >> 6;
+        const size_t T = tp / P, p = tp - T * P;
+        const size_t row = T * kTileN + (lane & 15);
+        const size_t k0 = p * kChunkK + (lane >> 4) * 16;
+        int8_t v[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+            v[j] = (row < n && k0 + j < k) ? data[row * k + k0 + j] : (int8_t)0;
+        int8_t *dst = tiles + e * 16;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) dst[j] = v[j];
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void k_pad_scales(
+    const float *__restrict__ scales, size_t n, size_t np,
+    float *__restrict__ out) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < np) out[i] = i < n ? scales[i] : 0.0f;
+}
+
+// One thread per 16-byte lane piece of the Q8_0 quant tiles.
+__global__ __launch_bounds__(kThreads) void k_repack_q8_quants(
+    const uint8_t *__restrict__ raw, size_t n, size_t nb, size_t n_tiles,
+    size_t P, int8_t *__restrict__ tiles) {
+    const size_t total = n_tiles * P * 64;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += stride) {
+        const size_t lane = e & 63, tp = e >> 6;
+        const size_t T = tp / P, p = tp - T * P;
+        const size_t row = T * kTileN + (lane & 15);
+        const size_t g = lane >> 4;
+        int8_t *dst = tiles + e * 16;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const size_t b = 2 * p + h;
+            const bool ok = row < n && b < nb;
+            const uint8_t *src = raw + (row * nb + b) * kQ8Bytes + 2 + g * 8;
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                dst[h * 8 + j] = ok ? (int8_t)src[j] : (int8_t)0;
+        }
+    }
+}
+
+// One thread per (tile, group of 8 blocks, row): 8 f16 scales.
+__global__ __launch_bounds__(kThreads) void k_repack_q8_scales(
+    const uint8_t *__restrict__ raw, size_t n, size_t nb, size_t n_tiles,
+    size_t Q, uint16_t *__restrict__ scales) {
+    const size_t total = n_tiles * Q * kTileN;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += stride) {
+        const size_t r = e & 15, tq = e >> 4;
+        const size_t T = tq / Q, q = tq - T * Q;
+        const size_t row = T * kTileN + r;
+        uint16_t *dst = scales + e * kQ8ScaleGroup;
+#pragma unroll
+        for (int j = 0; j < kQ8ScaleGroup; ++j) {
+            const size_t b = q * kQ8ScaleGroup + j;
+            uint16_t d = 0;
+            if (row < n && b < nb) {
+                const uint8_t *src = raw + (row * nb + b) * kQ8Bytes;
+                d = (uint16_t)(src[0] | (src[1] << 8));
+            }
+            dst[j] = d;
+        }
+    }
+}
+
+inline int grid_for(size_t n) {
+    size_t g = (n + kThreads - 1) / kThreads;
+    if (g < 1) g = 1;
+    if (g > 8192) g = 8192;
+    return (int)g;
+}
+
+}  // namespace
+
+mri_status launch_repack_int8(const int8_t *data, const float *scales,
+                              QMatrixDev &w, hipStream_t s) {
+    const size_t P = w.kp / kChunkK;
+    const size_t pieces = w.n_tiles * P * 64;
+    if (pieces) {
+        hipLaunchKernelGGL(k_repack_int8, dim3(grid_for(pieces)), dim3(kThreads),
+                           0, s, data, w.n_out, w.k_in, w.n_tiles, P, w.tiles);
+        MRI_LAUNCHED("k_repack_int8");
+    }
+    const size_t np = w.n_tiles * kTileN;
+    if (np) {
+        hipLaunchKernelGGL(k_pad_scales, dim3(grid_for(np)), dim3(kThreads), 0, s,
+                           scales, w.n_out, np, w.scales);
+        MRI_LAUNCHED("k_pad_scales");
+    }
+    return MRI_OK;
+}
+
+mri_status launch_repack_q8_0(const uint8_t *raw, Q8MatrixDev &w,
+                              hipStream_t s) {
+    const size_t P = w.kp / kChunkK;
+    const size_t Q = w.kp / (kQK * kQ8ScaleGroup);
+    const size_t pieces = w.n_tiles * P * 64;
+    if (pieces) {
+        hipLaunchKernelGGL(k_repack_q8_quants, dim3(grid_for(pieces)),
+                           dim3(kThreads), 0, s, raw, w.n_out, w.n_blocks,
+                           w.n_tiles, P, w.tiles);
+        MRI_LAUNCHED("k_repack_q8_quants");
+    }
+    const size_t sc = w.n_tiles * Q * kTileN;
+    if (sc) {
+        hipLaunchKernelGGL(k_repack_q8_scales, dim3(grid_for(sc)), dim3(kThreads),
+                           0, s, raw, w.n_out, w.n_blocks, w.n_tiles, Q, w.scales);
+        MRI_LAUNCHED("k_repack_q8_scales");
+    }
+    return MRI_OK;
+}
+
+}  // namespace mri

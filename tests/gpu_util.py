@@ -1,0 +1,71 @@
+"""Helpers for GPU tests: numpy <-> torch device tensors, seeded data."""
+import numpy as np
+
+F32 = np.float32
+
+
+def torch():
+    import torch as _t
+    assert _t.cuda.is_available(), "GPU tests need a visible MI355X"
+    return _t
+
+
+def dev(a):
+    t = torch()
+    return t.from_numpy(np.ascontiguousarray(a)).to("cuda")
+
+
+def empty(shape, dtype):
+    t = torch()
+    return t.empty(shape, dtype=dtype, device="cuda")
+
+
+def host(t):
+    torch().cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def bits(a):
+    return np.asarray(a, F32).view(np.uint32)
+
+
+def assert_bits_equal(got, exp, what=""):
+    got = np.asarray(got, F32)
+    exp = np.asarray(exp, F32)
+    assert got.shape == exp.shape, (what, got.shape, exp.shape)
+    g, e = bits(got), bits(exp)
+    bad = np.flatnonzero(g.ravel() != e.ravel())
+    if bad.size:
+        i = bad[0]
+        raise AssertionError(
+            f"{what}: {bad.size} of {g.size} f32 values differ bitwise; first at "
+            f"{np.unravel_index(i, got.shape)}: got {got.ravel()[i]!r} "
+            f"expected {exp.ravel()[i]!r}")
+
+
+def synth_q8_0(rng, n, k, with_min=False):
+    """Q8_0 raw blocks: quants uniform in [-127,127] (optionally some -128),
+    f16 scales ~U(0.001, 0.01)."""
+    import closed_form as CF
+    q = rng.integers(-127, 128, (n, k)).astype(np.int8)
+    if with_min:
+        q[rng.random((n, k)) < 0.02] = -128
+    d = rng.uniform(0.001, 0.01, (n, k // 32)).astype(np.float16).view(np.uint16)
+    return CF.q8_0_pack(d, q)
+
+
+def synth_q4_0(rng, n, k):
+    raw = np.empty((n, k // 32, 18), np.uint8)
+    raw[:, :, 2:] = rng.integers(0, 256, (n, k // 32, 16))
+    d = rng.uniform(0.001, 0.05, (n, k // 32)).astype(np.float16).view(np.uint16)
+    raw[:, :, 0] = d & 0xFF
+    raw[:, :, 1] = d >> 8
+    return raw.ravel()
+
+
+def synth_int8_weights(rng, n, k):
+    """Per-channel weights as the reference builds them: N(0, 0.02) f32
+    quantized per row (quantize_per_channel), via the oracle."""
+    import oracle_lib as O
+    w = (rng.standard_normal((n, k)) * 0.02).astype(F32)
+    return O.quantize_per_channel(w, n, k)

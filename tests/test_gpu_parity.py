@@ -1,0 +1,320 @@
+"""GPU parity: the HIP kernels through the C ABI vs the CPU oracle.
+
+Integer results (quantized activations, int32 accumulators, block dots) and
+the per-channel / Q8_0 f32 outputs must be bit-identical; Q4_0 (W4A32)
+outputs are within 1e-5 * max(|ref|, sum_k |x_k w_k|).
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import closed_form as CF
+import oracle_lib as O
+from gpu_util import (F32, assert_bits_equal, bits, dev, empty, host, synth_int8_weights,
+                      synth_q4_0, synth_q8_0, torch)
+
+pytestmark = pytest.mark.gpu
+
+
+def mri():
+    import mri_qmatmul
+    return mri_qmatmul
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+# ---- quantizers ----------------------------------------------------------------
+
+@pytest.mark.parametrize("n,scale,seed", [(4096, 1.0, 0), (1, 3.0, 1), (4097, 1e-3, 2),
+                                          (11008 * 3 + 5, 50.0, 3)])
+def test_quantize_symmetric(n, scale, seed):
+    say(f"quantize_symmetric n={n}")
+    t = torch()
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal(n) * scale).astype(F32)
+    q, s = O.quantize_symmetric(x)
+    xd = dev(x)
+    qd = empty(n, t.int8)
+    sd = empty(1, t.float32)
+    mri().quantize_symmetric(xd, qd, sd)
+    assert host(sd)[0] == s
+    assert np.array_equal(host(qd), q)
+
+
+def test_quantize_ties_and_specials():
+    t = torch()
+    x = np.array([127.0, 0.5, -0.5, 1.5, -1.5, 2.5, -62.5, 126.5, np.nan, -0.0], F32)
+    q, s = O.quantize_symmetric(x)
+    qd, sd = empty(x.size, t.int8), empty(1, t.float32)
+    mri().quantize_symmetric(dev(x), qd, sd)
+    assert host(sd)[0] == s and np.array_equal(host(qd), q)
+    z = np.zeros(100, F32)                               # all-zero -> scale 1
+    qd, sd = empty(100, t.int8), empty(1, t.float32)
+    mri().quantize_symmetric(dev(z), qd, sd)
+    assert host(sd)[0] == 1.0 and not host(qd).any()
+
+
+def test_quantize_rows_and_per_channel():
+    t = torch()
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((9, 333)).astype(F32)
+    x[4] = 0.0
+    q0, s0 = CF.quantize_rows(x)
+    qd, sd = empty((9, 333), t.int8), empty(9, t.float32)
+    mri().quantize_symmetric_rows(dev(x), qd, sd)
+    assert np.array_equal(host(qd), q0) and np.array_equal(bits(host(sd)), bits(s0))
+    w = (rng.standard_normal((37, 96)) * 0.02).astype(F32)
+    d0, ws0 = O.quantize_per_channel(w, 37, 96)
+    dd, sd = empty((37, 96), t.int8), empty(37, t.float32)
+    mri().quantize_per_channel(dev(w), 37, 96, dd, sd)
+    assert np.array_equal(host(dd), d0) and np.array_equal(bits(host(sd)), bits(ws0))
+
+
+def test_dot_i8_kats():  # int8_avx2.rs:219-297 through the GPU
+    t = torch()
+    cases = [([1, 2, 3], [4, 5, 6], 32), ([127] * 64, [1] * 64, 8128),
+             ([1, -1] * 32, [2] * 64, 0), ([-3] * 32, [-5] * 32, 480),
+             ([127] * 4096, [1] * 4096, 127 * 4096)]
+    for a, b, want in cases:
+        o = empty(1, t.int32)
+        mri().dot_i8(dev(np.array(a, np.int8)), dev(np.array(b, np.int8)), o)
+        assert host(o)[0] == want
+
+
+# ---- weights round trip ----------------------------------------------------------
+
+@pytest.mark.parametrize("n,k", [(1, 32), (17, 96), (64, 4096), (33, 100)])
+def test_qmatrix_roundtrip(n, k):
+    rng = np.random.default_rng(n * 1000 + k)
+    d = rng.integers(-127, 128, (n, k)).astype(np.int8)
+    s = rng.uniform(1e-4, 1e-3, n).astype(F32)
+    w = mri().QMatrix.from_host(d, s)
+    d2, s2 = w.read()
+    assert np.array_equal(d, d2) and np.array_equal(s, s2)
+
+
+@pytest.mark.parametrize("n,k", [(1, 32), (17, 96), (64, 4096), (3, 11008)])
+def test_q8_matrix_roundtrip(n, k):
+    raw = synth_q8_0(np.random.default_rng(k), n, k, with_min=True)
+    w = mri().Q8Matrix.from_raw_bytes(raw, n, k)
+    assert np.array_equal(w.read_raw(), raw)
+
+
+# ---- per-channel INT8 ------------------------------------------------------------
+
+INT8_SHAPES = [
+    # (m, n, k)
+    (1, 16, 64), (1, 11008 // 8, 4096), (1, 37, 96), (2, 50, 128), (3, 16, 4096),
+    (4, 64, 1024), (5, 48, 320), (16, 64, 4096), (17, 33, 64), (32, 96, 4096),
+    (33, 40, 256), (64, 128, 512), (128, 64, 1024),
+]
+
+
+@pytest.mark.parametrize("m,n,k", INT8_SHAPES)
+def test_matmul_int8_bit_exact(m, n, k):
+    say(f"matmul_int8 m={m} n={n} k={k}")
+    t = torch()
+    rng = np.random.default_rng(m * 7 + n * 13 + k)
+    wq, ws = synth_int8_weights(rng, n, k)
+    aq = rng.integers(-127, 128, (m, k)).astype(np.int8)
+    sa = F32(0.0173)
+    out0, acc0 = O.matmul_int8(aq, sa, wq, ws, m, want_acc=True)
+    assert np.array_equal(acc0.astype(np.int64), CF.int_matmul(aq, wq))
+    w = mri().QMatrix.from_host(wq, ws)
+    out = empty((m, n), t.float32)
+    acc = empty((m, n), t.int32)
+    mri().matmul_int8(dev(aq), sa, w, m, out, acc)
+    assert np.array_equal(host(acc), acc0)
+    assert_bits_equal(host(out), out0, "matmul_int8 out")
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 64, 4096), (7, 40, 256), (48, 32, 128)])
+def test_matmul_int8_rows_bit_exact(m, n, k):
+    t = torch()
+    rng = np.random.default_rng(m + n + k)
+    wq, ws = synth_int8_weights(rng, n, k)
+    aq = rng.integers(-127, 128, (m, k)).astype(np.int8)
+    sas = rng.uniform(1e-3, 1e-1, m).astype(F32)
+    out0, acc0 = O.matmul_int8_rows(aq, sas, wq, ws, m, want_acc=True)
+    w = mri().QMatrix.from_host(wq, ws)
+    out, acc = empty((m, n), t.float32), empty((m, n), t.int32)
+    mri().matmul_int8_rows(dev(aq), dev(sas), w, m, out, acc)
+    assert np.array_equal(host(acc), acc0)
+    assert_bits_equal(host(out), out0, "matmul_int8_rows out")
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 11008, 4096), (4, 64, 4096), (32, 128, 4096),
+                                   (3, 20, 96), (200, 48, 256)])
+def test_matmul_int8_from_f32_bit_exact(m, n, k):
+    say(f"matmul_int8_from_f32 m={m} n={n} k={k}")
+    t = torch()
+    rng = np.random.default_rng(m * 3 + n + k)
+    wq, ws = synth_int8_weights(rng, n, k)
+    x = rng.standard_normal((m, k)).astype(F32)
+    out0, aq0, sa0, acc0 = O.matmul_int8_from_f32(x, wq, ws)
+    w = mri().QMatrix.from_host(wq, ws)
+    out, acc = empty((m, n), t.float32), empty((m, n), t.int32)
+    aq, sa = empty((m, k), t.int8), empty(1, t.float32)
+    mri().matmul_int8_from_f32(dev(x), w, out, aq, sa, acc)
+    assert host(sa)[0] == sa0
+    assert np.array_equal(host(aq), aq0)
+    assert np.array_equal(host(acc), acc0)
+    assert_bits_equal(host(out), out0, "matmul_int8_from_f32 out")
+
+
+# ---- Q8_0 --------------------------------------------------------------------------
+
+Q8_SHAPES = [
+    (1, 16, 32), (1, 4096 // 4, 4096), (1, 50, 96), (1, 64, 11008), (2, 33, 256),
+    (4, 48, 4096), (8, 16, 512), (16, 40, 1024), (17, 20, 64), (32, 64, 4096),
+    (40, 24, 128),
+]
+
+
+@pytest.mark.parametrize("m,n,k", Q8_SHAPES)
+def test_matmul_q8_0_direct_bit_exact(m, n, k):
+    say(f"matmul_q8_0_direct m={m} n={n} k={k}")
+    t = torch()
+    rng = np.random.default_rng(m * 11 + n + k)
+    raw = synth_q8_0(rng, n, k, with_min=True)
+    x = rng.standard_normal((m, k)).astype(F32)
+    out0, bd0, sa0 = O.matmul_q8_0_direct(x, raw, n, k, want_block_dots=True)
+    w = mri().Q8Matrix.from_raw_bytes(raw, n, k)
+    out = empty((m, n), t.float32)
+    bd = empty((m, n, k // 32), t.int32)
+    sa = empty(m, t.float32)
+    mri().matmul_q8_0_direct(dev(x), w, out, bd, sa)
+    assert np.array_equal(bits(host(sa)), bits(sa0))
+    assert np.array_equal(host(bd), bd0)
+    assert_bits_equal(host(out), out0, "q8_0 out")
+    out2 = empty((m, n), t.float32)        # without the debug outputs
+    mri().matmul_q8_0_direct(dev(x), w, out2)
+    assert_bits_equal(host(out2), out0, "q8_0 out (no debug outputs)")
+
+
+def test_q8_0_reference_encoder_weights():
+    """Weights built by create_q8_0_block (dequant.rs:389-421), as
+    Q8_0WeightMatrix::from_f32_tensor does."""
+    t = torch()
+    rng = np.random.default_rng(3)
+    wf = (rng.standard_normal((24, 256)) * 0.05).astype(F32)
+    raw = O.quantize_q8_0(wf)
+    x = rng.standard_normal((3, 256)).astype(F32)
+    out0 = O.matmul_q8_0_direct(x, raw, 24, 256)
+    w = mri().Q8Matrix.from_raw_bytes(raw, 24, 256)
+    out = empty((3, 24), t.float32)
+    mri().matmul_q8_0_direct(dev(x), w, out)
+    assert_bits_equal(host(out), out0, "q8_0 encoder weights")
+
+
+# ---- Q4_0 ----------------------------------------------------------------------------
+
+@pytest.mark.parametrize("m,n,k", [(1, 16, 32), (1, 300, 4096), (3, 20, 96),
+                                   (2, 64, 11008), (5, 7, 64)])
+def test_matmul_q4_0_dequant_tolerance(m, n, k):
+    say(f"matmul_q4_0 m={m} n={n} k={k}")
+    t = torch()
+    rng = np.random.default_rng(m + n * 3 + k)
+    raw = synth_q4_0(rng, n, k)
+    x = rng.standard_normal((m, k)).astype(F32)
+    out0 = O.matmul_q4_0_dequant(x, raw, n, k)
+    out = empty((m, n), t.float32)
+    mri().matmul_q4_0_dequant(dev(x), dev(raw), n, k, out)
+    got = host(out)
+    scale = np.maximum(np.abs(out0), CF.q4_0_terms_abs_sum(x, raw, n, k))
+    err = np.abs(got.astype(np.float64) - out0)
+    assert np.all(err <= 1e-5 * scale), float(np.max(err / scale))
+
+
+# ---- error behaviour (TensorError kinds and order) ------------------------------------
+
+def test_errors():
+    t = torch()
+    M = mri()
+    wq = np.zeros((2, 32), np.int8)
+    w = M.QMatrix.from_host(wq, np.ones(2, F32))
+    out = empty((4, 4), t.float32)
+    x = dev(np.ones((2, 4, 8), F32))
+    with pytest.raises(M.MriError) as e:                 # int8.rs:292-301
+        M.matmul_int8_from_f32(x, w, out)
+    assert e.value.kind == "InvalidShape"
+    w64 = M.QMatrix.from_host(np.zeros((1, 64), np.int8), np.ones(1, F32))
+    with pytest.raises(M.MriError) as e:                 # int8.rs:303-318
+        M.matmul_int8_from_f32(dev(np.ones((1, 32), F32)), w64, out)
+    assert e.value.kind == "ShapeMismatch"
+    with pytest.raises(M.MriError) as e:                 # int8.rs:320-329
+        M.matmul_int8(dev(np.zeros(10, np.int8)), 1.0, w, 1, out)
+    assert e.value.kind == "InvalidShape"
+    with pytest.raises(M.MriError) as e:                 # q8_direct.rs:321-331
+        M.Q8Matrix.from_raw_bytes(np.zeros(34, np.uint8), 1, 31)
+    assert e.value.kind == "InvalidShape"
+    with pytest.raises(M.MriError):
+        M.Q8Matrix.from_raw_bytes(np.zeros(33, np.uint8), 1, 32)
+    M.Q8Matrix.from_raw_bytes(np.zeros(0, np.uint8), 0, 32)   # zero n_out accepted
+    q8 = M.Q8Matrix.from_raw_bytes(np.zeros(68, np.uint8), 2, 32)
+    with pytest.raises(M.MriError) as e:
+        M.matmul_q8_0_direct(x, q8, out)
+    assert e.value.kind == "InvalidShape"
+    q8b = M.Q8Matrix.from_raw_bytes(np.zeros(2 * 2 * 34, np.uint8), 2, 64)
+    with pytest.raises(M.MriError) as e:
+        M.matmul_q8_0_direct(dev(np.ones((1, 32), F32)), q8b, out)
+    assert e.value.kind == "ShapeMismatch"
+    dummy = dev(np.zeros(18, np.uint8))                  # q4_0.rs:307-347 order
+    with pytest.raises(M.MriError) as e:
+        M.matmul_q4_0_dequant(x, dummy, 1, 32, out)
+    assert e.value.kind == "InvalidShape"
+    with pytest.raises(M.MriError) as e:
+        M.matmul_q4_0_dequant(dev(np.ones((1, 33), F32)), dummy, 1, 33, out)
+    assert e.value.kind == "InvalidShape"
+    with pytest.raises(M.MriError) as e:
+        M.matmul_q4_0_dequant(dev(np.ones((1, 32), F32)), dummy, 1, 64, out)
+    assert e.value.kind == "ShapeMismatch"
+    with pytest.raises(M.MriError) as e:
+        M.matmul_q4_0_dequant(dev(np.ones((1, 32), F32)), dev(np.zeros(20, np.uint8)),
+                              1, 32, out)
+    assert e.value.kind == "InvalidShape"
+    with pytest.raises(M.MriError) as e:
+        M.quantize_per_channel(dev(np.zeros(5, F32)), 2, 3, empty(6, t.int8),
+                               empty(2, t.float32))
+    assert e.value.kind == "InvalidShape"
+
+
+def test_zero_sizes():
+    t = torch()
+    M = mri()
+    w = M.QMatrix.from_host(np.zeros((0, 32), np.int8), np.zeros(0, F32))
+    out = empty(1, t.float32)
+    M.matmul_int8_from_f32(dev(np.ones((2, 32), F32)), w, out)
+    w2 = M.QMatrix.from_host(np.ones((3, 32), np.int8), np.ones(3, F32))
+    M.matmul_int8(dev(np.zeros(0, np.int8)), 1.0, w2, 0, out)
+    M.synchronize()
+
+
+@pytest.mark.parametrize("m", [1, 3])
+def test_unfused_path_matches(m):
+    """x at a 4-byte (not 16-byte) aligned address takes the two-kernel path
+    (quantize kernel + GEMV); both paths must agree bit-for-bit."""
+    t = torch()
+    rng = np.random.default_rng(21 + m)
+    n, k = 48, 4096
+    raw = synth_q8_0(rng, n, k)
+    wq, ws = synth_int8_weights(rng, n, k)
+    x = rng.standard_normal((m, k)).astype(F32)
+    buf = dev(np.concatenate([np.zeros(1, F32), x.ravel()]))
+    xu = buf[1:].view(m, k)                       # misaligned by 4 bytes
+    assert xu.data_ptr() % 16 != 0
+    out0 = O.matmul_q8_0_direct(x, raw, n, k)
+    w8 = mri().Q8Matrix.from_raw_bytes(raw, n, k)
+    out = empty((m, n), t.float32)
+    mri().matmul_q8_0_direct(xu, w8, out)
+    assert_bits_equal(host(out), out0, "q8_0 unfused")
+    ref, aq0, sa0, acc0 = O.matmul_int8_from_f32(x, wq, ws)
+    wi = mri().QMatrix.from_host(wq, ws)
+    out2, aq, sa = empty((m, n), t.float32), empty((m, k), t.int8), empty(1, t.float32)
+    mri().matmul_int8_from_f32(xu, wi, out2, aq, sa)
+    assert host(sa)[0] == sa0 and np.array_equal(host(aq), aq0)
+    assert_bits_equal(host(out2), ref, "int8 unfused")
