@@ -258,7 +258,7 @@ mri_status mri_qmatrix_read(const mri_qmatrix *w, int8_t *data, float *scales) {
         for (size_t k = 0; k < d.k_in; ++k) {
             const size_t p = k / kChunkK, g = (k % kChunkK) / 16, j = k % 16;
             const size_t lane = g * 16 + r;
-            if (data) data[n * d.k_in + k] = tiles[((T * P + p) * 64 + lane) * 16 + j];
+            if (data) data[n * d.k_in + k] = tiles[((p * d.n_tiles + T) * 64 + lane) * 16 + j];
         }
         if (scales) scales[n] = sc[n];
     }
@@ -365,14 +365,14 @@ mri_status mri_q8_0_matrix_read_raw(const mri_q8_0_matrix *w, uint8_t *data, siz
         const size_t T = n / kTileN, r = n % kTileN;
         for (size_t b = 0; b < d.n_blocks; ++b) {
             uint8_t *blk = data + (n * d.n_blocks + b) * kQ8Bytes;
-            const uint16_t dv = sc[((T * Q + b / 8) * kTileN + r) * 8 + b % 8];
+            const uint16_t dv = sc[((b / 8 * d.n_tiles + T) * kTileN + r) * 8 + b % 8];
             blk[0] = (uint8_t)(dv & 0xFF);
             blk[1] = (uint8_t)(dv >> 8);
             const size_t p = b / 2, h = b % 2;
             for (size_t g = 0; g < 4; ++g)
                 for (size_t j = 0; j < 8; ++j)
                     blk[2 + g * 8 + j] =
-                        (uint8_t)tiles[((T * P + p) * 64 + g * 16 + r) * 16 + h * 8 + j];
+                        (uint8_t)tiles[((p * d.n_tiles + T) * 64 + g * 16 + r) * 16 + h * 8 + j];
         }
     }
     return MRI_OK;
@@ -511,7 +511,7 @@ mri_status mri_matmul_int8_from_f32(const float *input, const size_t *dims, size
     mri_status st = current_device(&dev);
     if (st) return st;
     auto s = static_cast<hipStream_t>(stream);
-    if (d.n_out > 0 && gemv_fusable(m, k, input) &&
+    if (d.n_out > 0 && gemv_fusable(m, k, input) && aligned(act_q_out, 4) &&
         gemv_int8_supported(true, m, d.n_tiles, k, d.kp))
         return launch_gemv_int8(input, nullptr, m, nullptr, 0, 0.0f, d, out, act_q_out,
                                 act_scale_out, acc_out, s);

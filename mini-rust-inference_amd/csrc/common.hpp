@@ -3,22 +3,26 @@
 // Device weight layouts (chosen at upload time, not visible through the ABI):
 //
 //  * Per-channel INT8 (QuantizedMatrix, per_channel.rs:31-40) is stored as
-//    "MFMA tiles": the output rows are grouped in tiles of 16 and K in chunks
-//    of 64.  Chunk (T, p) is 1 KiB at byte offset (T * P + p) * 1024 with
-//    P = Kp / 64, Kp = K rounded up to 64.  Inside a chunk, lane l (0..63)
-//    owns 16 bytes at l * 16: row 16*T + (l % 16), k = 64*p + 16*(l / 16) +
-//    [0, 16).  This is exactly the B operand of v_mfma_i32_16x16x64_i8 for
-//    lane l, so one global_load_dwordx4 per lane per chunk feeds one MFMA and
-//    a wave reads 1 KiB contiguous bytes per instruction.  Scales: f32 [Np].
+//    "MFMA chunks": the output rows are grouped in tiles of 16 and K in
+//    slabs of 64.  Chunk (p, T) (slab p, tile T) is 1 KiB; chunks are stored
+//    slab-major, at byte offset (p * n_tiles + T) * 1024, so a sweep over K
+//    by the waves of all tiles reads one contiguous, moving window.  Inside
+//    a chunk, lane l (0..63) owns 16 bytes at l * 16: row 16*T + (l % 16),
+//    k = 64*p + 16*(l / 16) + [0, 16).  This is the B operand of
+//    v_mfma_i32_16x16x64_i8 for lane l (the A operand uses the same k
+//    assignment), so one global_load_dwordx4 per lane per chunk feeds one
+//    MFMA and a wave reads 1 KiB contiguous bytes per instruction.
+//    Scales: f32 [n_tiles * 16] (zero padded).
 //
 //  * Q8_0 (Q8_0WeightMatrix, q8_direct.rs:60-69) is split into quants and
-//    scales.  Quants use the same 1 KiB chunks, but lane l's 16 bytes hold
-//    two 8-byte B operands of v_mfma_i32_16x16x32_i8 (one MFMA per 32-element
-//    block): bytes [8h, 8h+8) = quants [8g, 8g+8) of block 2p+h of row
-//    16T + (l % 16), g = l / 16.  Kp = K rounded up to 256.  Scales stay
-//    f16 (2 bytes per block, as in GGUF) in groups of 8 blocks:
-//    [T][Kp/256][16 rows][8 blocks], so one 16-byte load gives a lane the
-//    scales of 8 consecutive blocks of its row.
+//    scales.  Quants use the same slab-major 1 KiB chunks, but lane l's 16
+//    bytes hold two 8-byte B operands of v_mfma_i32_16x16x32_i8 (one MFMA
+//    per 32-element block): bytes [8h, 8h+8) = quants [8g, 8g+8) of block
+//    2p+h of row 16T + (l % 16), g = l / 16.  Kp = K rounded up to 256.
+//    Scales stay f16 (2 bytes per block, as in GGUF) in groups of 8 blocks
+//    (4 chunks), also slab-major: group (q, T) row r at 16-byte index
+//    (q * n_tiles + T) * 16 + r holds the scales of blocks 8q .. 8q+7, so
+//    one 16-byte load gives a lane the scales of 4 consecutive chunks.
 //
 //  * Activations quantized by the library are written to a per-(device,
 //    stream) scratch in [M][Kp] int8 rows (zero padded).  For Q8_0 the 64

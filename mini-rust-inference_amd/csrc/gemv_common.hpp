@@ -1,0 +1,175 @@
+// gemv_common.hpp — shared pieces of the decode GEMV kernels (M <= 4) of
+// gemv_int8.hip and gemv_q8.hip: a single sweep over the slab-major weight
+// stream with a ring of loads in flight per wave.
+//
+// Work decomposition: a workgroup holds TPW tiles of 16 output channels with
+// S waves each; a tile's K chunks are split over its S waves as evenly as
+// possible (Q8_0: in whole scale groups of 4 chunks).  Because the weights
+// are stored slab-major (chunk (p, T) at (p * n_tiles + T) KiB), the waves
+// of all tiles that run together read one contiguous window of the matrix
+// that moves through memory, which is the access pattern HBM serves best.
+//
+// Ring: each wave keeps D chunk loads in flight.  Slot s holds the chunks
+// i == s (mod D) of its segment; the loop body is unrolled by D, so every
+// slot is a fixed register range, and after chunk i is consumed the load of
+// chunk i + D is issued into the same slot.  The loop contains no other
+// global memory instruction (the Q8_0 scale loads ride the same ring, one
+// 16-byte load per 4 chunks), so the wait before each MFMA leaves D - 1
+// loads outstanding.  Optional int32 debug outputs are compiled into a
+// separate kernel instance so that the timed kernel has no stores in the
+// loop.
+//
+//  * Fused prologue (one f32 row, the decode case): the S waves split the
+//    activation read, reduce max|x| through LDS, quantize (symmetric.rs:42-57;
+//    per row and per tensor coincide for one row) and write the int8 row to
+//    LDS in the weight chunk order.  The activation loads are issued before
+//    the ring's first D weight loads, so the prologue overlaps the weight
+//    stream.  Other calls copy pre-quantized rows to LDS instead.
+#pragma once
+
+#include <cstdlib>
+#include <type_traits>
+#include <utility>
+
+#include "common.hpp"
+
+namespace mri {
+namespace gemv {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+constexpr int kMaxM = 4;
+constexpr size_t kMaxLds = 64 * 1024;
+
+inline size_t ceil_div(size_t a, size_t b) { return (a + b - 1) / b; }
+
+__device__ inline long lo8(const v4i &v) {
+    return (long)(((unsigned long)(unsigned)v.y << 32) | (unsigned)v.x);
+}
+__device__ inline long hi8(const v4i &v) {
+    return (long)(((unsigned long)(unsigned)v.w << 32) | (unsigned)v.z);
+}
+
+__device__ inline float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+__device__ inline int round_clamp_i8(float y) {
+    float r = roundf(y);              // ties away from zero, like f32::round
+    if (r != r) return 0;             // `NaN as i8` == 0
+    r = fminf(fmaxf(r, -127.0f), 127.0f);
+    return (int)r;
+}
+
+// Calls f(std::integral_constant<int, I>) for I = 0 .. N-1 (compile-time
+// ring slot indices).
+template <typename F, int... I>
+__device__ inline void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ inline void static_for(F &&f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// Even split of `units` over `parts`: part w gets [lo, hi).
+__host__ __device__ inline int split_lo(int units, int parts, int w) {
+    return (int)((long)units * w / parts);
+}
+
+// Activation source of a launch: f32 rows quantized in the kernel (x != 0)
+// or int8 rows of pitch kp already quantized (act != 0).
+struct ActIn {
+    const float *x;      // [1][K] f32, 16-byte aligned, K % 4 == 0
+    const int8_t *act;   // [M][kp] int8 (Q8_0: chunk-permuted), 16-byte aligned
+    int K;
+    int8_t *act_q_out;   // optional plain [K] int8 (INT8 fused path)
+    float *scale_out;    // optional [1] (fused path)
+};
+
+// Each thread stages XR 16-byte pieces of the activations in registers:
+// piece e of thread t is element t + S*64*e (index clamped, use guarded).
+// The loads are unconditional so that no wait count depends on a branch.
+template <int S, int XR>
+__device__ inline void stage_load(const v4i *src, int n16, v4i (&xr)[XR]) {
+#pragma unroll
+    for (int e = 0; e < XR; ++e) xr[e] = src[min((int)threadIdx.x + S * kWave * e, n16 - 1)];
+}
+
+// The activation prologue runs in two parts around the priming of the
+// weight ring.  act_begin consumes the staged registers (the per-wave
+// max|x| of an f32 row, or the copy of int8 rows into LDS), so the wave
+// waits for its activation loads BEFORE it issues any weight load: the
+// small activation read then does not queue behind megabytes of weight
+// requests in HBM.  act_end (after the ring is primed) finishes the
+// quantization: block max through LDS, quantize_symmetric
+// (symmetric.rs:42-57; per row and per tensor coincide for one row) of the
+// row held in xr into LDS (chunk-permuted when perm).
+template <int S, int XR, bool FUSED>
+__device__ inline void act_begin(const ActIn &in, int n16, const v4i (&xr)[XR], int8_t *s_act,
+                                 float *red) {
+    const int t = threadIdx.x;
+    if constexpr (FUSED) {
+        const int K4 = in.K / 4;
+        float mx = 0.0f;
+#pragma unroll
+        for (int e = 0; e < XR; ++e) {
+            if (t + S * kWave * e < K4) {
+                const float4 v = __builtin_bit_cast(float4, xr[e]);
+                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+            }
+        }
+        mx = wave_max(mx);
+        if ((t & 63) == 0) red[t >> 6] = mx;
+    } else {
+        v4i *dst = reinterpret_cast<v4i *>(s_act);
+#pragma unroll
+        for (int e = 0; e < XR; ++e) {
+            const int i = t + S * kWave * e;
+            if (i < n16) dst[i] = xr[e];
+        }
+    }
+    // keep the weight loads that follow behind the uses above
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int S, int XR, bool FUSED>
+__device__ inline void act_end(const ActIn &in, bool perm, const v4i (&xr)[XR], int8_t *s_act,
+                               const float *red, float &scale, bool writer) {
+    __syncthreads();
+    if constexpr (FUSED) {
+        const int t = threadIdx.x;
+        const int K4 = in.K / 4;
+        float mx = 0.0f;
+#pragma unroll
+        for (int s = 0; s < S; ++s) mx = fmaxf(mx, red[s]);
+        scale = mx == 0.0f ? 1.0f : __fdiv_rn(mx, 127.0f);
+        const float inv = __fdiv_rn(1.0f, scale);
+#pragma unroll
+        for (int e = 0; e < XR; ++e) {
+            const int j = t + S * kWave * e;
+            if (j < K4) {
+                const float4 v = __builtin_bit_cast(float4, xr[e]);
+                const int q0 = round_clamp_i8(v.x * inv);
+                const int q1 = round_clamp_i8(v.y * inv);
+                const int q2 = round_clamp_i8(v.z * inv);
+                const int q3 = round_clamp_i8(v.w * inv);
+                const int kk = 4 * j;
+                const int pos = perm ? (kk & ~63) + q8_perm(kk & 63) : kk;
+                const int packed =
+                    (q0 & 255) | ((q1 & 255) << 8) | ((q2 & 255) << 16) | (q3 << 24);
+                *reinterpret_cast<int *>(s_act + pos) = packed;
+                if (writer && in.act_q_out)
+                    *reinterpret_cast<int *>(in.act_q_out + kk) = packed;
+            }
+        }
+        if (writer && t == 0 && in.scale_out) in.scale_out[0] = scale;
+        __syncthreads();
+    }
+}
+
+}  // namespace gemv
+}  // namespace mri

@@ -1,0 +1,199 @@
+// gemv_int8.hip — per-channel INT8 decode GEMV (M <= 4): matmul_int8 /
+// matmul_int8_from_f32 (int8.rs:61-143) on the slab-major MFMA chunks.
+//
+// v_mfma_i32_16x16x64_i8 accumulates exact int32 sums over the wave's K
+// segment; with S > 1 the S partial accumulators are added through LDS and
+// wave 0 of the tile applies ((f32)acc * s_a) * s_w (int8.rs:93).  Each wave
+// keeps D chunk loads in flight in a ring of registers.
+#include "gemv_common.hpp"
+
+namespace mri {
+using namespace gemv;
+namespace {
+
+// ---------------------------------------------------------------------------
+// Per-channel INT8.
+// ---------------------------------------------------------------------------
+template <int NI, int S, int TPW, int D, int XR, bool FUSED>
+__global__ __launch_bounds__(S * TPW * kWave) void k_gemv_int8(
+    ActIn in, int M, int kp, const float *__restrict__ sa_ptr, int sa_stride,
+    float sa_value, const v4i *__restrict__ tiles, const float *__restrict__ wscales,
+    int N, int n_tiles, int P, float *__restrict__ out, int32_t *__restrict__ acc_out) {
+    constexpr int NW = S * TPW;
+    extern __shared__ v4i s_lds[];
+    // wave index as a scalar: segment bounds and loop guards stay uniform, so
+    // no MFMA ever sits under a partial EXEC mask.
+    const int wl = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int tw_ = wl / S;                   // tile of the wave within the WG
+    const int w = wl - tw_ * S;               // segment of the wave
+    const int T = blockIdx.x * TPW + tw_;
+    const bool tile_ok = T < n_tiles;
+    const int Tc = tile_ok ? T : n_tiles - 1;
+    const int l = threadIdx.x & 63;
+    const int r = l & 15, g = l >> 4;
+    const int c0 = split_lo(P, S, w), c1 = tile_ok ? split_lo(P, S, w + 1) : c0;
+    const int nc = c1 - c0;
+    const int last = max(c1 - 1, 0);
+    const size_t pitch = (size_t)n_tiles * kWave;  // v4i per slab of chunks
+    const v4i *wp = tiles + (size_t)Tc * kWave + l;
+
+    // LDS: [act M*kp][red NW floats][partials TPW x (S-1) x 64 v4i]
+    int8_t *s_act = reinterpret_cast<int8_t *>(s_lds);
+    float *red = reinterpret_cast<float *>(s_act + (size_t)M * kp);
+    v4i *part = reinterpret_cast<v4i *>(red + 4 * NW) + (size_t)tw_ * (S - 1) * kWave;
+
+    const bool aval = r < M;
+    const v4i *ap = reinterpret_cast<const v4i *>(s_act + (size_t)(aval ? r : 0) * kp) + g;
+    const v4i zero = {0, 0, 0, 0};
+    v4i acc = zero;
+    v4i wr[D];
+
+    v4i xr[XR];
+    const int n16 = FUSED ? in.K / 4 : M * kp / 16;
+    stage_load<NW, XR>(FUSED ? reinterpret_cast<const v4i *>(in.x)
+                             : reinterpret_cast<const v4i *>(in.act),
+                       n16, xr);
+    act_begin<NW, XR, FUSED>(in, n16, xr, s_act, red);
+#pragma unroll
+    for (int s = 0; s < D; ++s)
+        wr[s] = __builtin_nontemporal_load(wp + (size_t)min(c0 + s, last) * pitch);
+    act_end<NW, XR, FUSED>(in, false, xr, s_act, red, sa_value, blockIdx.x == 0);
+    if constexpr (FUSED) sa_ptr = nullptr;
+
+    auto mfma = [&](int s, int i) __attribute__((always_inline)) {
+        const v4i a = aval ? ap[(size_t)(c0 + i) * 4] : zero;
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, wr[s], acc, 0, 0, 0);
+    };
+    // full laps with refills: chunk i is consumed from slot i % D, then the
+    // slot is reloaded with chunk i + D, which exists (i + D < laps * D <= nc)
+    const int laps = nc / D;
+    for (int lap = 0; lap + 1 < laps; ++lap) {
+#pragma unroll
+        for (int s = 0; s < D; ++s) {
+            const int i = lap * D + s;
+            mfma(s, i);
+            wr[s] = __builtin_nontemporal_load(wp + (size_t)(c0 + i + D) * pitch);
+        }
+    }
+    // last full lap: refill only the slots of the remaining nc % D chunks
+    const int rem = nc - laps * D;
+    if (laps > 0) {
+#pragma unroll
+        for (int s = 0; s < D; ++s) {
+            const int i = (laps - 1) * D + s;
+            mfma(s, i);
+            if (s < rem)
+                wr[s] = __builtin_nontemporal_load(wp + (size_t)(c0 + i + D) * pitch);
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < D; ++s)
+        if (s < rem) mfma(s, laps * D + s);
+
+    // exact int32 reduction over the S segments
+    if constexpr (S > 1) {
+        if (w > 0) part[(w - 1) * kWave + l] = acc;
+        __syncthreads();
+        if (w > 0) return;
+#pragma unroll
+        for (int s = 1; s < S; ++s) acc += part[(s - 1) * kWave + l];
+    }
+
+    const int n = T * 16 + r;
+    if (!tile_ok || n >= N || g != 0) return;
+    const float sw = wscales[n];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        if (i < M) {
+            const float sa = sa_ptr ? sa_ptr[(size_t)i * sa_stride] : sa_value;
+            float v = (float)acc[i] * sa;
+            v = v * sw;
+            out[(size_t)i * N + n] = v;
+            if (acc_out) acc_out[(size_t)i * N + n] = acc[i];
+        }
+    }
+}
+
+
+struct CfgI8 {
+    int s = 0, tpw = 1, d = 4, xr = 0;  // s == 0: unsupported
+};
+
+size_t lds_i8(int s, int tpw, size_t m, size_t kp) {
+    return m * kp + (size_t)s * tpw * 16 + (size_t)tpw * (s - 1) * kWave * 16;
+}
+
+// Configuration by the number of 16-row tiles (measured on MI355X): about
+// 2000-2800 waves and 4-16 MB of weight loads in flight over the whole GPU.
+// Many tiles: one wave per tile, 8 tiles per workgroup; otherwise the K
+// split keeps enough waves.  The activation staging must fit XR pieces per
+// thread (4, 8 or 12 of 16 bytes).
+CfgI8 pick_i8(bool fused, size_t n_tiles, size_t m, size_t k, size_t kp) {
+    CfgI8 c;
+    if (n_tiles >= 1024) { c.s = 1; c.tpw = 8; c.d = 8; }
+    else if (n_tiles >= 512) { c.s = 4; c.d = 4; }
+    else if (kp <= 4096) { c.s = 4; c.d = 8; }
+    else { c.s = 8; c.d = 8; }
+    const size_t threads = (size_t)c.s * c.tpw * kWave;
+    const size_t nx = ceil_div(fused ? k / 4 : m * kp / 16, threads);
+    c.xr = nx <= 4 ? 4 : nx <= 8 ? 8 : nx <= 12 ? 12 : 0;
+    if (c.xr == 0 || lds_i8(c.s, c.tpw, m, kp) > kMaxLds) c.s = 0;
+    return c;
+}
+
+template <int NI, int S, int TPW, int D, int XR, bool FUSED>
+void launch_i8(ActIn in, size_t m, const float *sa_ptr, int sa_stride, float sa_value,
+               const QMatrixDev &w, float *out, int32_t *acc_out, hipStream_t st) {
+    hipLaunchKernelGGL((k_gemv_int8<NI, S, TPW, D, XR, FUSED>),
+                       dim3((unsigned)ceil_div(w.n_tiles, TPW)), dim3(S * TPW * kWave),
+                       lds_i8(S, TPW, m, w.kp), st, in, (int)m, (int)w.kp, sa_ptr, sa_stride,
+                       sa_value, reinterpret_cast<const v4i *>(w.tiles), w.scales,
+                       (int)w.n_out, (int)w.n_tiles, (int)(w.kp / kChunkK), out, acc_out);
+}
+
+template <int NI, bool FUSED>
+void dispatch_i8(CfgI8 c, ActIn in, size_t m, const float *sa_ptr, int sa_stride,
+                 float sa_value, const QMatrixDev &w, float *out, int32_t *acc_out,
+                 hipStream_t st) {
+#define MRI_I8(S_, TPW_, D_, XR_)                                                          \
+    if (c.s == S_ && c.tpw == TPW_ && c.d == D_ && c.xr == XR_)                            \
+        return launch_i8<NI, S_, TPW_, D_, XR_, FUSED>(in, m, sa_ptr, sa_stride, sa_value, \
+                                                       w, out, acc_out, st);
+    MRI_I8(1, 8, 8, 4) MRI_I8(1, 8, 8, 8) MRI_I8(1, 8, 8, 12)
+    MRI_I8(4, 1, 4, 4) MRI_I8(4, 1, 4, 8) MRI_I8(4, 1, 4, 12)
+    MRI_I8(4, 1, 8, 4) MRI_I8(4, 1, 8, 8) MRI_I8(4, 1, 8, 12)
+    MRI_I8(8, 1, 8, 4) MRI_I8(8, 1, 8, 8) MRI_I8(8, 1, 8, 12)
+#undef MRI_I8
+}
+
+}  // namespace
+
+bool gemv_int8_supported(bool fused, size_t m, size_t n_tiles, size_t k, size_t kp) {
+    return m >= 1 && m <= (size_t)kMaxM && pick_i8(fused, n_tiles, m, k, kp).s > 0;
+}
+
+bool gemv_fusable(size_t m, size_t k, const float *x) {
+    return m == 1 && k % 4 == 0 && x &&
+           (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+}
+
+mri_status launch_gemv_int8(const float *x, const int8_t *act, size_t m,
+                            const float *sa_ptr, int sa_stride, float sa_value,
+                            const QMatrixDev &w, float *out, int8_t *act_q_out,
+                            float *scale_out, int32_t *acc_out, hipStream_t st) {
+    if (w.n_tiles == 0 || m == 0) return MRI_OK;
+    const CfgI8 c = pick_i8(x != nullptr, w.n_tiles, m, w.k_in, w.kp);
+    if (c.s == 0) return set_error(MRI_ERR_INVALID_ARGUMENT, "gemv: shape not supported");
+    const ActIn in{x, act, (int)w.k_in, act_q_out, scale_out};
+    if (x) {
+        dispatch_i8<1, true>(c, in, m, nullptr, 0, 0.0f, w, out, acc_out, st);
+    } else {
+        if (m == 1) dispatch_i8<1, false>(c, in, m, sa_ptr, sa_stride, sa_value, w, out, acc_out, st);
+        else if (m == 2) dispatch_i8<2, false>(c, in, m, sa_ptr, sa_stride, sa_value, w, out, acc_out, st);
+        else dispatch_i8<4, false>(c, in, m, sa_ptr, sa_stride, sa_value, w, out, acc_out, st);
+    }
+    MRI_LAUNCHED("k_gemv_int8");
+    return MRI_OK;
+}
+
+}  // namespace mri

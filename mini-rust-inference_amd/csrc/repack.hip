@@ -1,5 +1,5 @@
-// repack.hip — one-time weight upload transforms into the MFMA tile layouts
-// described in common.hpp.  Run once per weight handle, off the hot path.
+// repack.hip — one-time weight upload transforms into the slab-major MFMA
+// chunk layouts described in common.hpp.  Run once per weight handle, off the hot path.
 #include "common.hpp"
 
 namespace mri {
@@ -15,8 +15,8 @@ __global__ __launch_bounds__(kThreads) void k_repack_int8(
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
          e += stride) {
-        const size_t lane = e & 63, tp = e >> 6;
-        const size_t T = tp / P, p = tp - T * P;
+        const size_t lane = e & 63, pt = e >> 6;
+        const size_t p = pt / n_tiles, T = pt - p * n_tiles;
         const size_t row = T * kTileN + (lane & 15);
         const size_t k0 = p * kChunkK + (lane >> 4) * 16;
         int8_t v[16];
@@ -44,8 +44,8 @@ __global__ __launch_bounds__(kThreads) void k_repack_q8_quants(
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
          e += stride) {
-        const size_t lane = e & 63, tp = e >> 6;
-        const size_t T = tp / P, p = tp - T * P;
+        const size_t lane = e & 63, pt = e >> 6;
+        const size_t p = pt / n_tiles, T = pt - p * n_tiles;
         const size_t row = T * kTileN + (lane & 15);
         const size_t g = lane >> 4;
         int8_t *dst = tiles + e * 16;
@@ -69,8 +69,8 @@ __global__ __launch_bounds__(kThreads) void k_repack_q8_scales(
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
          e += stride) {
-        const size_t r = e & 15, tq = e >> 4;
-        const size_t T = tq / Q, q = tq - T * Q;
+        const size_t r = e & 15, qt = e >> 4;
+        const size_t q = qt / n_tiles, T = qt - q * n_tiles;
         const size_t row = T * kTileN + r;
         uint16_t *dst = scales + e * kQ8ScaleGroup;
 #pragma unroll

@@ -50,7 +50,8 @@ __global__ __launch_bounds__(kWave) void k_skinny_int8(
     const int T = blockIdx.x;
     const int l = threadIdx.x;
     const int r = l & 15, g = l >> 4;
-    const v4i *wp = tiles + (size_t)T * P * kWave + l;
+    const size_t pitch = (size_t)gridDim.x * kWave;  // slab-major chunks
+    const v4i *wp = tiles + (size_t)T * kWave + l;
     const v4i *ap[MT];
     bool aval[MT];
 #pragma unroll
@@ -73,7 +74,7 @@ __global__ __launch_bounds__(kWave) void k_skinny_int8(
     auto load_w = [&](int buf, int p0) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < U; ++u)
-            wb[buf][u] = __builtin_nontemporal_load(wp + (size_t)min(p0 + u, P - 1) * kWave);
+            wb[buf][u] = __builtin_nontemporal_load(wp + (size_t)min(p0 + u, P - 1) * pitch);
     };
     auto load_a = [&](int buf, int p0) __attribute__((always_inline)) {
 #pragma unroll
@@ -159,8 +160,10 @@ __global__ __launch_bounds__(kWave) void k_skinny_q8_0(
     const int l = threadIdx.x;
     const int r = l & 15, g = l >> 4;
     const int Pe = (nb + 1) / 2;  // chunks holding real blocks
-    const v4i *wp = tiles + (size_t)T * P * kWave + l;
-    const v4i *sp = qscales + (size_t)T * Q * 16 + r;
+    const size_t pitch = (size_t)gridDim.x * kWave;   // slab-major chunks
+    const size_t spitch = (size_t)gridDim.x * 16;     // slab-major scale groups
+    const v4i *wp = tiles + (size_t)T * kWave + l;
+    const v4i *sp = qscales + (size_t)T * 16 + r;
     const v4i *ap[MT];
     bool aval[MT];
 #pragma unroll
@@ -186,8 +189,8 @@ __global__ __launch_bounds__(kWave) void k_skinny_q8_0(
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int p = min(p0 + u, Pe - 1);
-            wb[buf][u] = __builtin_nontemporal_load(wp + (size_t)p * kWave);
-            if ((u & 3) == 0) sb[buf][u / 4] = sp[(size_t)(p / 4) * 16];
+            wb[buf][u] = __builtin_nontemporal_load(wp + (size_t)p * pitch);
+            if ((u & 3) == 0) sb[buf][u / 4] = sp[(size_t)(p / 4) * spitch];
         }
     };
     auto load_a = [&](int buf, int p0) __attribute__((always_inline)) {

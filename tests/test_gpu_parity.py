@@ -109,6 +109,7 @@ def test_q8_matrix_roundtrip(n, k):
 INT8_SHAPES = [
     # (m, n, k)
     (1, 16, 64), (1, 11008 // 8, 4096), (1, 37, 96), (2, 50, 128), (3, 16, 4096),
+    (1, 16400, 8192), (1, 300, 11008), (2, 4096, 4096),
     (4, 64, 1024), (5, 48, 320), (16, 64, 4096), (17, 33, 64), (32, 96, 4096),
     (33, 40, 256), (64, 128, 512), (128, 64, 1024),
 ]
@@ -170,6 +171,7 @@ def test_matmul_int8_from_f32_bit_exact(m, n, k):
 
 Q8_SHAPES = [
     (1, 16, 32), (1, 4096 // 4, 4096), (1, 50, 96), (1, 64, 11008), (2, 33, 256),
+    (1, 16400, 8192), (1, 4096, 11008), (3, 2000, 4096), (1, 32000, 4096),
     (4, 48, 4096), (8, 16, 512), (16, 40, 1024), (17, 20, 64), (32, 64, 4096),
     (40, 24, 128),
 ]
