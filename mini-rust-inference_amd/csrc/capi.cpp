@@ -124,6 +124,8 @@ static mri_status run_int8(const int8_t *act, size_t m, const float *sa_ptr,
     if (gemv_int8_supported(false, m, w.n_tiles, w.k_in, w.kp))
         return launch_gemv_int8(nullptr, act, m, sa_ptr, sa_stride, sa_value, w, out,
                                 nullptr, nullptr, acc_out, s);
+    if (m >= kGemmMinRows)
+        return launch_gemm_int8(act, m, sa_ptr, sa_stride, sa_value, w, out, acc_out, s);
     return launch_skinny_int8(act, m, sa_ptr, sa_stride, sa_value, w, out, acc_out, s);
 }
 

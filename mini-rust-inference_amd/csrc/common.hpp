@@ -154,7 +154,8 @@ mri_status launch_gemv_q8_0(const float *x, const int8_t *act, size_t m,
                             const float *sa_rows, const Q8MatrixDev &w, float *out,
                             int32_t *block_dots, float *scales_out, hipStream_t s);
 
-// gemm.hip: prefill-sized M on MFMA with LDS tiles.
+// gemm.hip: prefill-sized M on MFMA with LDS tiles; act rows [m][kp].
+constexpr size_t kGemmMinRows = 64;
 mri_status launch_gemm_int8(const int8_t *act, size_t m, const float *sa_ptr,
                             int sa_stride, float sa_value, const QMatrixDev &w,
                             float *out, int32_t *acc_out, hipStream_t s);

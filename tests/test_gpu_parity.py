@@ -133,7 +133,30 @@ def test_matmul_int8_bit_exact(m, n, k):
     assert_bits_equal(host(out), out0, "matmul_int8 out")
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 64, 4096), (7, 40, 256), (48, 32, 128)])
+@pytest.mark.parametrize("m,n,k", [(512, 11008, 4096), (300, 200, 1024), (2048, 512, 4096),
+                                   (64, 4096, 11008), (128, 4096, 4096)])
+def test_matmul_int8_prefill_closed_form(m, n, k):
+    """Prefill-sized matmul_int8 (int8.rs:61-98) at full shapes: the int32
+    accumulators against an exact float64 matmul (|sum| <= 127^2 * K < 2^53)
+    and the f32 outputs against the two-multiply epilogue in float32."""
+    say(f"matmul_int8 prefill m={m} n={n} k={k}")
+    t = torch()
+    rng = np.random.default_rng(m + 3 * n + 7 * k)
+    wq = rng.integers(-127, 128, (n, k)).astype(np.int8)
+    ws = rng.uniform(1e-4, 1e-3, n).astype(F32)
+    aq = rng.integers(-127, 128, (m, k)).astype(np.int8)
+    sa = F32(0.0173)
+    acc0 = (aq.astype(np.float64) @ wq.astype(np.float64).T).astype(np.int32)
+    out0 = (acc0.astype(F32) * sa) * ws[None, :]
+    w = mri().QMatrix.from_host(wq, ws)
+    out = empty((m, n), t.float32)
+    acc = empty((m, n), t.int32)
+    mri().matmul_int8(dev(aq), sa, w, m, out, acc)
+    assert np.array_equal(host(acc), acc0)
+    assert_bits_equal(host(out), out0, "matmul_int8 prefill out")
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 64, 4096), (7, 40, 256), (48, 32, 128), (260, 96, 512)])
 def test_matmul_int8_rows_bit_exact(m, n, k):
     t = torch()
     rng = np.random.default_rng(m + n + k)
