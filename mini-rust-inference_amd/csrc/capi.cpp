@@ -124,8 +124,6 @@ static mri_status run_int8(const int8_t *act, size_t m, const float *sa_ptr,
     if (gemv_int8_supported(false, m, w.n_tiles, w.k_in, w.kp))
         return launch_gemv_int8(nullptr, act, m, sa_ptr, sa_stride, sa_value, w, out,
                                 nullptr, nullptr, acc_out, s);
-    if (m >= kGemmMinRows)
-        return launch_gemm_int8(act, m, sa_ptr, sa_stride, sa_value, w, out, acc_out, s);
     return launch_skinny_int8(act, m, sa_ptr, sa_stride, sa_value, w, out, acc_out, s);
 }
 
@@ -471,6 +469,16 @@ static mri_status matmul_int8_common(const char *fn, const int8_t *act_q, size_t
     mri_status st = current_device(&dev);
     if (st) return st;
     auto s = static_cast<hipStream_t>(stream);
+    if (m >= kGemmMinRows) {
+        // prefill: repack the rows into the GEMM fragment layout
+        void *base = nullptr;
+        st = scratch_get(s, gemm_pack_bytes(m, d.kp), &base);
+        if (st) return st;
+        auto *packed = static_cast<int8_t *>(base);
+        st = launch_pack_gemm(act_q, m, k, k, d.kp, packed, s);
+        if (st) return st;
+        return launch_gemm_int8(packed, m, sa_ptr, sa_stride, sa_value, d, out, acc_out, s);
+    }
     const int8_t *act = nullptr;
     st = prepare_act(act_q, m, d, s, &act);
     if (st) return st;
@@ -517,8 +525,9 @@ mri_status mri_matmul_int8_from_f32(const float *input, const size_t *dims, size
         gemv_int8_supported(true, m, d.n_tiles, k, d.kp))
         return launch_gemv_int8(input, nullptr, m, nullptr, 0, 0.0f, d, out, act_q_out,
                                 act_scale_out, acc_out, s);
+    const bool gemm = m >= kGemmMinRows;
     Carver cv;
-    const size_t o_act = cv.take(m * d.kp);
+    const size_t o_act = cv.take(gemm ? gemm_pack_bytes(m, d.kp) : m * d.kp);
     const size_t o_part = cv.take(1024 * sizeof(float));
     const size_t o_scale = cv.take(sizeof(float));
     void *base = nullptr;
@@ -527,8 +536,15 @@ mri_status mri_matmul_int8_from_f32(const float *input, const size_t *dims, size
     auto *b = static_cast<uint8_t *>(base);
     int8_t *act = reinterpret_cast<int8_t *>(b + o_act);
     float *scale = act_scale_out ? act_scale_out : reinterpret_cast<float *>(b + o_scale);
-    st = launch_quantize_tensor(input, m, k, d.kp, false, act, act_q_out, scale,
-                                reinterpret_cast<float *>(b + o_part), s);
+    auto *partials = reinterpret_cast<float *>(b + o_part);
+    if (gemm) {
+        // prefill: quantize straight into the GEMM fragment layout
+        st = launch_quantize_pack(input, m, k, d.kp, act, act_q_out, scale, partials, s);
+        if (st) return st;
+        if (d.n_out == 0) return MRI_OK;
+        return launch_gemm_int8(act, m, scale, 0, 0.0f, d, out, acc_out, s);
+    }
+    st = launch_quantize_tensor(input, m, k, d.kp, false, act, act_q_out, scale, partials, s);
     if (st) return st;
     if (m * d.n_out == 0) return MRI_OK;
     return run_int8(act, m, scale, 0, 0.0f, d, out, acc_out, s);

@@ -28,6 +28,13 @@
 //    stream) scratch in [M][Kp] int8 rows (zero padded).  For Q8_0 the 64
 //    bytes of each chunk are permuted to match the weight chunk:
 //    element kk of a chunk sits at q8_perm(kk).
+//
+//  * Activations of the prefill GEMM (M >= kGemmMinRows) are packed into
+//    its MFMA fragment layout: row group g = m / 32, K step p = k / 64,
+//    half h = (k % 64) / 32; fragment (p, g, h) is 1 KiB at byte offset
+//    ((p * MG + g) * 2 + h) * 1024 with MG = ceil(M / 32); inside it lane
+//    l = m % 32 + 32 * ((k % 32) / 16) owns 16 bytes at l * 16 (element
+//    k % 16 at byte l * 16 + k % 16).  Rows past M are zero.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -117,6 +124,13 @@ mri_status launch_quantize_per_channel(const float *w, size_t n, size_t k,
                                        hipStream_t s);
 mri_status launch_pad_rows(const int8_t *src, size_t m, size_t k, size_t kp,
                            int8_t *dst, hipStream_t s);
+// quantize_symmetric (per tensor) of [m,k] into the packed GEMM layout.
+mri_status launch_quantize_pack(const float *x, size_t m, size_t k, size_t kp,
+                                int8_t *packed, int8_t *q_plain, float *scale,
+                                float *partials, hipStream_t s);
+// int8 rows [m][ld] (k valid) into the packed GEMM layout.
+mri_status launch_pack_gemm(const int8_t *src, size_t m, size_t k, size_t ld, size_t kp,
+                            int8_t *packed, hipStream_t s);
 mri_status launch_dot_i8(const int8_t *a, const int8_t *b, size_t n,
                          int32_t *out, hipStream_t s);
 size_t quantize_partials_count(size_t n);
@@ -154,9 +168,17 @@ mri_status launch_gemv_q8_0(const float *x, const int8_t *act, size_t m,
                             const float *sa_rows, const Q8MatrixDev &w, float *out,
                             int32_t *block_dots, float *scales_out, hipStream_t s);
 
-// gemm.hip: prefill-sized M on MFMA with LDS tiles; act rows [m][kp].
+// gemm.hip: prefill-sized M on MFMA with LDS tiles, packed activations.
 constexpr size_t kGemmMinRows = 64;
-mri_status launch_gemm_int8(const int8_t *act, size_t m, const float *sa_ptr,
+inline size_t gemm_row_groups(size_t m) { return (m + 31) / 32; }
+inline size_t gemm_pack_bytes(size_t m, size_t kp) { return gemm_row_groups(m) * 32 * kp; }
+// Byte offset of element (m, k) in the packed layout.
+__host__ __device__ inline size_t gemm_pack_offset(size_t m, size_t k, size_t mg) {
+    const size_t p = k >> 6, kk = k & 63, h = kk >> 5;
+    const size_t lane = (m & 31) + 32 * ((kk & 31) >> 4);
+    return (((p * mg + (m >> 5)) * 2 + h) * 64 + lane) * 16 + (kk & 15);
+}
+mri_status launch_gemm_int8(const int8_t *act_packed, size_t m, const float *sa_ptr,
                             int sa_stride, float sa_value, const QMatrixDev &w,
                             float *out, int32_t *acc_out, hipStream_t s);
 

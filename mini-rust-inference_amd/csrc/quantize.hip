@@ -157,6 +157,66 @@ __global__ __launch_bounds__(kThreads) void k_dot_i8(
     }
 }
 
+// Piece e (16 bytes) of the packed GEMM activation layout (common.hpp):
+// returns its row and first k.
+__device__ inline void pack_piece(size_t e, size_t mg, size_t *row, size_t *k0) {
+    const size_t lane = e & 63, t = e >> 6;
+    const size_t h = t & 1, t2 = t >> 1;
+    const size_t g = t2 % mg, p = t2 / mg;
+    *row = 32 * g + (lane & 31);
+    *k0 = 64 * p + 32 * h + 16 * (lane >> 5);
+}
+
+// quantize_symmetric with the per-tensor scale reduced from `partials`,
+// written straight into the packed GEMM layout (zero padded to mg*32 rows
+// and kp columns); q_plain (optional) receives the [m*k] row-major values.
+__global__ __launch_bounds__(kThreads) void k_quantize_pack(
+    const float *__restrict__ x, size_t m, size_t k, size_t mg, size_t kp,
+    const float *__restrict__ partials, int n_partials, int8_t *__restrict__ packed,
+    int8_t *__restrict__ q_plain, float *__restrict__ scale_out) {
+    __shared__ float red[kThreads / 64];
+    float mx = 0.0f;
+    for (int i = threadIdx.x; i < n_partials; i += blockDim.x)
+        mx = fmaxf(mx, partials[i]);
+    mx = block_max(mx, red);
+    const float scale = scale_of(mx);
+    const float inv = __fdiv_rn(1.0f, scale);
+    if (blockIdx.x == 0 && threadIdx.x == 0 && scale_out) *scale_out = scale;
+    const size_t pieces = mg * 32 * kp / 16;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < pieces; e += stride) {
+        size_t r, k0;
+        pack_piece(e, mg, &r, &k0);
+        int8_t q[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const size_t kk = k0 + j;
+            q[j] = (r < m && kk < k) ? round_clamp_i8(x[r * k + kk] * inv) : (int8_t)0;
+            if (q_plain && r < m && kk < k) q_plain[r * k + kk] = q[j];
+        }
+        *reinterpret_cast<int4 *>(packed + e * 16) = *reinterpret_cast<const int4 *>(q);
+    }
+}
+
+// Row-major int8 rows [m][ld] (k valid columns) into the packed GEMM layout.
+__global__ __launch_bounds__(kThreads) void k_pack_gemm(
+    const int8_t *__restrict__ src, size_t m, size_t k, size_t ld, size_t mg, size_t kp,
+    int8_t *__restrict__ packed) {
+    const size_t pieces = mg * 32 * kp / 16;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < pieces; e += stride) {
+        size_t r, k0;
+        pack_piece(e, mg, &r, &k0);
+        int8_t q[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const size_t kk = k0 + j;
+            q[j] = (r < m && kk < k) ? src[r * ld + kk] : (int8_t)0;
+        }
+        *reinterpret_cast<int4 *>(packed + e * 16) = *reinterpret_cast<const int4 *>(q);
+    }
+}
+
 inline int grid_for(size_t n, int per_thread = 1) {
     size_t g = (n + (size_t)kThreads * per_thread - 1) / ((size_t)kThreads * per_thread);
     if (g < 1) g = 1;
@@ -188,6 +248,29 @@ mri_status launch_quantize_tensor(const float *x, size_t m, size_t k,
                        q8_perm_layout ? 1 : 0, partials, g, q_pad, q_plain,
                        scale);
     MRI_LAUNCHED("k_quantize_tensor");
+    return MRI_OK;
+}
+
+mri_status launch_quantize_pack(const float *x, size_t m, size_t k, size_t kp,
+                                int8_t *packed, int8_t *q_plain, float *scale,
+                                float *partials, hipStream_t s) {
+    const size_t n = m * k;
+    const int g = (int)quantize_partials_count(n);
+    hipLaunchKernelGGL(k_absmax_partial, dim3(g), dim3(kThreads), 0, s, x, n, partials);
+    MRI_LAUNCHED("k_absmax_partial");
+    const size_t mg = gemm_row_groups(m);
+    hipLaunchKernelGGL(k_quantize_pack, dim3(grid_for(mg * 32 * kp / 16)), dim3(kThreads), 0,
+                       s, x, m, k, mg, kp, partials, g, packed, q_plain, scale);
+    MRI_LAUNCHED("k_quantize_pack");
+    return MRI_OK;
+}
+
+mri_status launch_pack_gemm(const int8_t *src, size_t m, size_t k, size_t ld, size_t kp,
+                            int8_t *packed, hipStream_t s) {
+    const size_t mg = gemm_row_groups(m);
+    hipLaunchKernelGGL(k_pack_gemm, dim3(grid_for(mg * 32 * kp / 16)), dim3(kThreads), 0, s,
+                       src, m, k, ld, mg, kp, packed);
+    MRI_LAUNCHED("k_pack_gemm");
     return MRI_OK;
 }
 

@@ -172,7 +172,8 @@ def test_matmul_int8_rows_bit_exact(m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 11008, 4096), (4, 64, 4096), (32, 128, 4096),
-                                   (3, 20, 96), (200, 48, 256)])
+                                   (3, 20, 96), (200, 48, 256), (300, 512, 4096),
+                                   (64, 100, 96)])
 def test_matmul_int8_from_f32_bit_exact(m, n, k):
     say(f"matmul_int8_from_f32 m={m} n={n} k={k}")
     t = torch()
