@@ -2,23 +2,30 @@
 """Benchmark of the quantized-matmul hot path on one MI355X.
 
 Headline workload (one "step" = one call of the hot path):
-  Q8_0 decode GEMV, x [1, 4096] f32  x  W [11008, 4096] Q8_0 (matmul_q8_0_direct),
-  synthetic data: quants ~U[-127,127], f16 block scales ~U(0.001, 0.01),
-  x ~ N(0, 1).  Eight device copies of the weights (384 MB > the 256 MB
-  Infinity Cache) are used in rotation so the weight stream comes from HBM.
+  Q8_0 decode GEMV, x [1, 4096] f32 x W [11008, 4096] Q8_0 (matmul_q8_0_direct),
+  synthetic data: quants ~U[-127, 127], f16 block scales ~U(0.001, 0.01),
+  x ~ N(0, 1).  Enough device copies of the weights (>= 384 MB, more than
+  the 256 MB Infinity Cache) are used in rotation so that the weight stream
+  comes from HBM.  The output of the first call is checked bit-for-bit
+  against the oracle before timing.
 
-value  = algorithmic bytes per call / mean call time (GB/s), with
-         algorithmic bytes = Q8_0 weight bytes (34 B per 32 weights)
-         + 4*K (x) + 4*N (out).
-roofline.achieved = the same bytes / mean duration of the GEMV kernel, timed
-         with HIP events on the stream the kernel runs on.
+value = algorithmic bytes per call / mean call time (GB/s), with
+        algorithmic bytes = Q8_0 weight bytes (34 B per 32 weights)
+        + 4*K (x) + 4*N (out).  The call is one kernel, so this is also
+        roofline.achieved: bytes / mean kernel time over the timed region,
+        from HIP events on the stream the kernel runs on.
 cpu_baseline = the oracle's restatement of the reference's only Q8_0 path
-         (scalar, single-threaded matmul_q8_0_direct) on the same shape.
+        (scalar, single-threaded matmul_q8_0_direct) on the same shape.
 
-Also reported (secondary fields): the Q8_0 sweep over the Llama-7B
-projection shapes, skinny M in {4,8,16,32}, the per-channel INT8 decode GEMV
-and the M=512 INT8 prefill GEMM in TOPS, plus the reference's rayon+AVX2
-matmul_int8_parallel restatement on the INT8 decode shape.
+Secondary fields (same timing method): the Q8_0 sweep over the Llama-7B
+projection shapes (M = 1), the skinny Q8_0 decode M in {4, 8, 16, 32}, the
+per-channel INT8 decode GEMV (matmul_int8_from_f32, M = 1), the INT8
+prefill GEMM over M in {128, 512, 2048} x N in {4096, 11008} on per-row
+quantized activations (matmul_int8 with per-row scales) and end to end from
+f32, the Q4_0 W4A32 decode GEMV, and the reference's rayon+AVX2
+matmul_int8_parallel restatement on the INT8 decode shape (one core, as
+the reference: one row) and on a bounded row sample of the prefill shape
+(all cores).
 """
 import argparse
 import json
@@ -31,91 +38,150 @@ sys.path.insert(0, os.path.join(ROOT, "mini-rust-inference_amd"))
 sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
-INT8_PEAK_TOPS = 5000.0    # MI355X dense int8 MFMA (5.0 POPS)
-MALL_BYTES = 256 << 20
+INT8_PEAK_TOPS = 5000.0    # MI355X dense int8 MFMA (5.0 POP/s)
+MALL_BYTES = 256 << 20     # Infinity Cache
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_q8_0_decode_1x4096x11008.json")
 
 
 def q8_bytes(m, n, k):
     return n * (k // 32) * 34 + 4 * m * k + 4 * m * n
 
 
+def q4_bytes(m, n, k):
+    return n * (k // 32) * 18 + 4 * m * k + 4 * m * n
+
+
 def int8_bytes(m, n, k):
+    """Per-channel INT8 decode: int8 weights + f32 scales + f32 x + f32 out."""
     return n * k + 4 * n + 4 * m * k + 4 * m * n
-
-
-def make_q8_raw(rng, n, k):
-    import numpy as np
-    q = rng.integers(-127, 128, (n, k), dtype=np.int8)
-    d = rng.uniform(0.001, 0.01, (n, k // 32)).astype(np.float16).view(np.uint16)
-    blk = np.empty((n, k // 32, 34), np.uint8)
-    blk[:, :, 0] = (d & 0xFF).astype(np.uint8)
-    blk[:, :, 1] = (d >> 8).astype(np.uint8)
-    blk[:, :, 2:] = q.reshape(n, k // 32, 32).view(np.uint8)
-    return blk.ravel()
 
 
 def copies_for(nbytes):
     return max(2, min(16, -(-(MALL_BYTES * 3 // 2) // nbytes)))
 
 
-def time_calls(torch, fn, steps, warmup, n_rot):
-    for i in range(warmup):
-        fn(i % n_rot)
-    torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for i in range(steps):
-        fn(i % n_rot)
-    end.record()
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps  # ms per call
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
 
 
-def bench_q8(torch, M, rng, m, n, k, steps, warmup, check=False):
-    import numpy as np
-    raw = make_q8_raw(rng, n, k)
-    nrot = copies_for(len(raw))
-    ws = [M.Q8Matrix.from_raw_bytes(raw, n, k) for _ in range(nrot)]
-    x = torch.randn(m, k, device="cuda")
-    out = torch.empty(m, n, device="cuda")
+class Timer:
+    """HIP events on torch's current stream, which is the stream every
+    entry point below enqueues on."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def per_call_ms(self, fn, steps, warmup, n_rot):
+        t = self.torch
+        for i in range(warmup):
+            fn(i % n_rot)
+        t.cuda.synchronize()
+        e0 = t.cuda.Event(enable_timing=True)
+        e1 = t.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(steps):
+            fn(i % n_rot)
+        e1.record()
+        t.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+
+def q8_raw_device(torch, n, k, seed):
+    """Raw Q8_0 blocks on the device: quants ~U[-127,127], f16 d ~U(0.001,0.01)."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    nb = k // 32
+    q = torch.randint(-127, 128, (n, nb, 32), dtype=torch.int8, device="cuda", generator=g)
+    d = (torch.rand((n, nb), device="cuda", generator=g) * 0.009 + 0.001).half()
+    raw = torch.empty((n, nb, 34), dtype=torch.uint8, device="cuda")
+    raw[:, :, 0:2] = d.view(torch.uint8).view(n, nb, 2)
+    raw[:, :, 2:] = q.view(torch.uint8)
+    return raw.view(-1)
+
+
+def q4_raw_device(torch, n, k, seed):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    nb = k // 32
+    nib = torch.randint(0, 256, (n, nb, 16), dtype=torch.uint8, device="cuda", generator=g)
+    d = (torch.rand((n, nb), device="cuda", generator=g) * 0.049 + 0.001).half()
+    raw = torch.empty((n, nb, 18), dtype=torch.uint8, device="cuda")
+    raw[:, :, 0:2] = d.view(torch.uint8).view(n, nb, 2)
+    raw[:, :, 2:] = nib
+    return raw.view(-1)
+
+
+def int8_weights_device(torch, M, n, k, seed):
+    """Per-channel INT8 weights as the reference builds them: f32 ~N(0, 0.02)
+    quantized per output row (quantize_per_channel) -- on the device."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    wf = torch.randn((n, k), device="cuda", generator=g) * 0.02
+    data = torch.empty((n, k), dtype=torch.int8, device="cuda")
+    scales = torch.empty(n, dtype=torch.float32, device="cuda")
+    M.quantize_per_channel(wf, n, k, data, scales)
+    return data, scales
+
+
+def bench_q8(torch, M, T, m, n, k, steps, warmup, check=False, seed=1):
+    raw = q8_raw_device(torch, n, k, seed)
+    nrot = copies_for(raw.numel())
+    ws = [M.Q8Matrix.from_raw_device(raw, n, k) for _ in range(nrot)]
+    g = torch.Generator(device="cuda").manual_seed(seed + 100)
+    x = torch.randn((m, k), device="cuda", generator=g)
+    out = torch.empty((m, n), device="cuda")
     if check:
+        import numpy as np
         import oracle_lib as O
         M.matmul_q8_0_direct(x, ws[0], out)
-        ref = O.matmul_q8_0_direct(x.cpu().numpy(), raw, n, k)
-        got = out.cpu().numpy()
-        if not np.array_equal(got.view(np.uint32), ref.view(np.uint32)):
+        ref = O.matmul_q8_0_direct(x.cpu().numpy(), raw.cpu().numpy(), n, k)
+        if not np.array_equal(out.cpu().numpy().view(np.uint32), ref.view(np.uint32)):
             raise SystemExit("bench: Q8_0 output differs from the oracle")
-    ms = time_calls(torch, lambda i: M.matmul_q8_0_direct(x, ws[i], out), steps, warmup,
-                    nrot)
-    return ms, raw, x
+    ms = T.per_call_ms(lambda i: M.matmul_q8_0_direct(x, ws[i], out), steps, warmup, nrot)
+    return ms, raw, x, nrot
 
 
-def bench_int8(torch, M, rng, m, n, k, steps, warmup, from_f32=True):
-    import numpy as np
-    wq = rng.integers(-127, 128, (n, k), dtype=np.int8)
-    sc = rng.uniform(1e-4, 1e-3, n).astype(np.float32)
+def bench_q4(torch, M, T, m, n, k, steps, warmup, seed=3):
+    raws = [q4_raw_device(torch, n, k, seed + i) for i in range(copies_for(n * k // 32 * 18))]
+    x = torch.randn((m, k), device="cuda")
+    out = torch.empty((m, n), device="cuda")
+    return T.per_call_ms(lambda i: M.matmul_q4_0_dequant(x, raws[i], n, k, out), steps, warmup,
+                         len(raws))
+
+
+def bench_int8_decode(torch, M, T, n, k, steps, warmup, seed=5):
+    data, scales = int8_weights_device(torch, M, n, k, seed)
     nrot = copies_for(n * k)
-    ws = [M.QMatrix.from_host(wq, sc) for _ in range(nrot)]
-    out = torch.empty(m, n, device="cuda")
-    if from_f32:
-        x = torch.randn(m, k, device="cuda")
-        fn = lambda i: M.matmul_int8_from_f32(x, ws[i], out)
-    else:
-        aq = torch.randint(-127, 128, (m, k), dtype=torch.int8, device="cuda")
-        fn = lambda i: M.matmul_int8(aq, 0.0123, ws[i], m, out)
-    ms = time_calls(torch, fn, steps, warmup, nrot)
-    return ms, wq, sc
+    ws = [M.QMatrix.from_device(data, scales) for _ in range(nrot)]
+    x = torch.randn((1, k), device="cuda")
+    out = torch.empty((1, n), device="cuda")
+    ms = T.per_call_ms(lambda i: M.matmul_int8_from_f32(x, ws[i], out), steps, warmup, nrot)
+    return ms, data, scales
 
 
-def cpu_baseline_q8(raw, x_np, n, k, budget_s):
+def bench_int8_prefill(torch, M, T, m, n, k, steps, warmup, seed=7):
+    """Per-channel INT8 weights, per-row quantized activations (matmul_int8
+    with one scale per row): returns (ms per call of the rows entry point,
+    ms per call end to end from f32 with per-tensor quantization)."""
+    data, scales = int8_weights_device(torch, M, n, k, seed)
+    nrot = copies_for(n * k)
+    ws = [M.QMatrix.from_device(data, scales) for _ in range(nrot)]
+    x = torch.randn((m, k), device="cuda")
+    aq = torch.empty((m, k), dtype=torch.int8, device="cuda")
+    sa = torch.empty(m, dtype=torch.float32, device="cuda")
+    M.quantize_symmetric_rows(x, aq, sa)
+    out = torch.empty((m, n), device="cuda")
+    ms_rows = T.per_call_ms(lambda i: M.matmul_int8_rows(aq, sa, ws[i], m, out), steps, warmup,
+                            nrot)
+    ms_f32 = T.per_call_ms(lambda i: M.matmul_int8_from_f32(x, ws[i], out), steps, warmup, nrot)
+    return ms_rows, ms_f32
+
+
+def cpu_q8_direct(raw_np, x_np, n, k, budget_s):
     """Scalar single-thread matmul_q8_0_direct (the reference's only Q8_0
-    path) timed on this host; returns (GB/s, reps, seconds)."""
+    path) on the full decode shape; returns (GB/s, calls, seconds)."""
     import oracle_lib as O
-    O.matmul_q8_0_direct(x_np, raw, n, k)                 # warm
+    O.matmul_q8_0_direct(x_np, raw_np, n, k)                 # warm
     reps, t0 = 0, time.perf_counter()
     while True:
-        O.matmul_q8_0_direct(x_np, raw, n, k)
+        O.matmul_q8_0_direct(x_np, raw_np, n, k)
         reps += 1
         el = time.perf_counter() - t0
         if el >= budget_s:
@@ -123,18 +189,18 @@ def cpu_baseline_q8(raw, x_np, n, k, budget_s):
     return q8_bytes(1, n, k) * reps / el / 1e9, reps, el
 
 
-def cpu_int8_parallel(wq, sc, k, n, budget_s):
-    """rayon+AVX2 matmul_int8_parallel restatement at M=1 (one row -> one
-    core, as in the reference)."""
+def cpu_int8_parallel(wq, sc, m, k, n, budget_s):
+    """rayon+AVX2 matmul_int8_parallel restatement: one task per output row
+    on a pool of all online CPUs.  Returns (ms per call, cores used, calls)."""
     import numpy as np
     import oracle_lib as O
     rng = np.random.default_rng(5)
-    aq = rng.integers(-127, 128, (1, k), dtype=np.int8)
-    out = np.empty((1, n), np.float32)
-    O.matmul_int8_parallel(aq, 0.01, wq, sc, 1, out=out)
+    aq = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    out = np.empty((m, n), np.float32)
+    O.matmul_int8_parallel(aq, 0.01, wq, sc, m, out=out)
     reps, used, t0 = 0, 0, time.perf_counter()
     while True:
-        _, used = O.matmul_int8_parallel(aq, 0.01, wq, sc, 1, out=out)
+        _, used = O.matmul_int8_parallel(aq, 0.01, wq, sc, m, out=out)
         reps += 1
         el = time.perf_counter() - t0
         if el >= budget_s:
@@ -152,6 +218,16 @@ def cpu_model():
     return "unknown"
 
 
+def load_traffic():
+    """HBM bytes per launch of the headline kernel, from the rocprofv3 --pmc
+    FETCH_SIZE / WRITE_SIZE runs recorded under profiles/ (null if absent)."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -160,12 +236,14 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 256 MiB device copy, 20 times (the reference "
+                         "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "the path shards over output rows without cross-GPU arithmetic, so "
-              "N-GPU throughput is N x the one-GPU value plus an all-gather.",
-              file=sys.stderr)
+              "the path shards over output rows without cross-GPU arithmetic, so the "
+              "N-GPU figure is not measured here.", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
@@ -174,12 +252,21 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
-    rng = np.random.default_rng(2026)
-    log = lambda *a: print(*a, file=sys.stderr, flush=True)
+    T = Timer(torch)
+
+    if args.copy_calibration:
+        src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")   # 256 MiB
+        dst = torch.empty_like(src)
+        for _ in range(20):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": src.numel() * 4, "copy_bytes_written":
+                          dst.numel() * 4, "launches": 20}), flush=True)
+        return
 
     # ---- headline: Q8_0 decode GEMV [1,4096] x [4096,11008] ------------------
     m, n, k = 1, 11008, 4096
-    ms, raw, x = bench_q8(torch, M, rng, m, n, k, args.steps, args.warmup, check=True)
+    ms, raw, x, nrot = bench_q8(torch, M, T, m, n, k, args.steps, args.warmup, check=True)
     nbytes = q8_bytes(m, n, k)
     value = nbytes / (ms * 1e-3) / 1e9
     log(f"q8_0 decode [1,{k}]x[{k},{n}]: {ms*1e3:.2f} us/call, {value:.0f} GB/s")
@@ -189,49 +276,80 @@ def main():
         steps2 = max(20, args.steps // 2)
         sweep = {}
         for (kk, nn) in [(4096, 4096), (11008, 4096), (4096, 32000)]:
-            ms2, _, _ = bench_q8(torch, M, rng, 1, nn, kk, steps2, args.warmup)
+            ms2, _, _, _ = bench_q8(torch, M, T, 1, nn, kk, steps2, args.warmup)
             gbs = q8_bytes(1, nn, kk) / (ms2 * 1e-3) / 1e9
-            sweep[f"{kk}x{nn}"] = {"us": round(ms2 * 1e3, 2), "GB_s": round(gbs, 1)}
+            sweep[f"{kk}x{nn}"] = {"us": round(ms2 * 1e3, 2), "GB_s": round(gbs, 1),
+                                  "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
             log(f"q8_0 M=1 {kk}->{nn}: {ms2*1e3:.2f} us {gbs:.0f} GB/s")
-        sweep["4096x11008"] = {"us": round(ms * 1e3, 2), "GB_s": round(value, 1)}
+        sweep["4096x11008"] = {"us": round(ms * 1e3, 2), "GB_s": round(value, 1),
+                               "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4)}
         secondary["q8_0_m1_sweep"] = sweep
+
         skinny = {}
         for mm in (4, 8, 16, 32):
-            ms2, _, _ = bench_q8(torch, M, rng, mm, 11008, 4096, steps2, args.warmup)
+            ms2, _, _, _ = bench_q8(torch, M, T, mm, 11008, 4096, steps2, args.warmup)
             gbs = q8_bytes(mm, 11008, 4096) / (ms2 * 1e-3) / 1e9
             skinny[str(mm)] = {"us": round(ms2 * 1e3, 2), "GB_s": round(gbs, 1)}
             log(f"q8_0 M={mm}: {ms2*1e3:.2f} us {gbs:.0f} GB/s")
         secondary["q8_0_skinny_4096x11008"] = skinny
-        ms_i8, wq, sc = bench_int8(torch, M, rng, 1, 11008, 4096, steps2, args.warmup)
+
+        ms_i8, wq_d, sc_d = bench_int8_decode(torch, M, T, 11008, 4096, steps2, args.warmup)
+        gbs = int8_bytes(1, 11008, 4096) / (ms_i8 * 1e-3) / 1e9
         secondary["int8_decode_1x4096x11008"] = {
-            "us": round(ms_i8 * 1e3, 2),
-            "GB_s": round(int8_bytes(1, 11008, 4096) / (ms_i8 * 1e-3) / 1e9, 1)}
-        log(f"int8 decode: {ms_i8*1e3:.2f} us")
-        ms_p, _, _ = bench_int8(torch, M, rng, 512, 11008, 4096, max(10, steps2 // 4),
-                                max(3, args.warmup // 4))
-        tops = 2 * 512 * 11008 * 4096 / (ms_p * 1e-3) / 1e12
-        secondary["int8_prefill_512x4096x11008"] = {
-            "us": round(ms_p * 1e3, 2), "TOPS": round(tops, 1),
-            "frac_of_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
-        log(f"int8 prefill M=512: {ms_p*1e3:.1f} us {tops:.0f} TOPS")
+            "us": round(ms_i8 * 1e3, 2), "GB_s": round(gbs, 1),
+            "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+        log(f"int8 decode: {ms_i8*1e3:.2f} us {gbs:.0f} GB/s")
+
+        prefill = {}
+        for mm in (128, 512, 2048):
+            for nn in (4096, 11008):
+                st = max(5, steps2 // (4 if mm < 2048 else 10))
+                ms_r, ms_f = bench_int8_prefill(torch, M, T, mm, nn, 4096, st, 3)
+                tops = 2 * mm * nn * 4096 / (ms_r * 1e-3) / 1e12
+                tops_f = 2 * mm * nn * 4096 / (ms_f * 1e-3) / 1e12
+                prefill[f"{mm}x4096x{nn}"] = {
+                    "us": round(ms_r * 1e3, 2), "TOPS": round(tops, 1),
+                    "frac_of_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                    "us_from_f32": round(ms_f * 1e3, 2), "TOPS_from_f32": round(tops_f, 1)}
+                log(f"int8 prefill M={mm} N={nn}: {ms_r*1e3:.1f} us {tops:.0f} TOPS "
+                    f"(from f32 {ms_f*1e3:.1f} us)")
+        secondary["int8_prefill_gemm"] = prefill
+
+        ms_q4 = bench_q4(torch, M, T, 1, 11008, 4096, steps2, args.warmup)
+        gbs = q4_bytes(1, 11008, 4096) / (ms_q4 * 1e-3) / 1e9
+        secondary["q4_0_decode_1x4096x11008"] = {
+            "us": round(ms_q4 * 1e3, 2), "GB_s": round(gbs, 1),
+            "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+        log(f"q4_0 decode: {ms_q4*1e3:.2f} us {gbs:.0f} GB/s")
+
         if not args.no_cpu:
-            ms_cpu, used, reps = cpu_int8_parallel(wq, sc, 4096, 11008, 3.0)
+            wq, sc = wq_d.cpu().numpy(), sc_d.cpu().numpy()
+            ms_cpu, used, reps = cpu_int8_parallel(wq, sc, 1, 4096, 11008, 3.0)
             secondary["cpu_int8_parallel_1x4096x11008"] = {
                 "ms": round(ms_cpu, 3), "cores_used": used,
-                "cores_available": os.cpu_count(), "reps": reps}
+                "cores_available": os.cpu_count(), "reps": reps,
+                "GB_s": round(int8_bytes(1, 11008, 4096) / (ms_cpu * 1e-3) / 1e9, 2)}
             log(f"cpu matmul_int8_parallel M=1: {ms_cpu:.3f} ms (cores used {used})")
+            rows = 64   # bounded sample of the M = 512 prefill: 64 rows
+            ms_cpu, used, reps = cpu_int8_parallel(wq, sc, rows, 4096, 11008, 4.0)
+            secondary["cpu_int8_parallel_prefill_sample"] = {
+                "rows": rows, "n": 11008, "k": 4096, "ms": round(ms_cpu, 2),
+                "TOPS": round(2 * rows * 11008 * 4096 / (ms_cpu * 1e-3) / 1e12, 4),
+                "cores_used": used, "cores_available": os.cpu_count(), "reps": reps}
+            log(f"cpu matmul_int8_parallel M={rows}: {ms_cpu:.1f} ms (cores used {used})")
 
     cpu = None
     if not args.no_cpu:
-        gbs_cpu, reps, el = cpu_baseline_q8(raw, x.cpu().numpy(), n, k, args.cpu_seconds)
+        gbs_cpu, reps, el = cpu_q8_direct(raw.cpu().numpy(), x.cpu().numpy(), n, k,
+                                          args.cpu_seconds)
         cpu = {"value": round(gbs_cpu, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-               "sample": f"oracle matmul_q8_0_direct (scalar, 1 thread) on "
-                         f"[1,{k}]x[{k},{n}], {reps} calls in {el:.1f} s on "
-                         f"{cpu_model()} ({os.cpu_count()} CPUs visible)"}
+               "sample": f"oracle matmul_q8_0_direct (scalar, 1 thread, the reference's "
+                         f"only Q8_0 path) on [1,{k}]x[{k},{n}]: {reps} calls in {el:.1f} s "
+                         f"on {cpu_model()} ({os.cpu_count()} CPUs visible)"}
         log(f"cpu q8_0 direct: {gbs_cpu:.3f} GB/s ({reps} reps)")
 
     line = {
-        "metric": "Q8_0 decode GEMV HBM GB/s (% peak) + us/token; INT8 prefill GEMM TOPS",
+        "metric": "Q8_0 decode GEMV HBM GB/s (% peak) + \u00b5s/token; INT8 prefill GEMM TOPS",
         "value": round(value, 1),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -246,11 +364,11 @@ def main():
         "dtype": "int8xint8->int32, f32 scale",
         "data": "synthetic",
         "config": {"workload": "Q8_0 decode GEMV [1,4096]x[4096,11008] (matmul_q8_0_direct)",
-                   "m": m, "k": k, "n": n, "weight_copies_rotated": copies_for(len(raw)),
+                   "m": m, "k": k, "n": n, "weight_copies_rotated": nrot,
                    "algorithmic_bytes_per_call": nbytes},
         "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(value / HBM_PEAK_GBS, 4),
-                     "traffic": None},
+                     "traffic": load_traffic()},
         "cpu_baseline": cpu,
     }
     line.update(secondary)
