@@ -17,15 +17,25 @@ namespace {
 // many lane groups hold results.
 //
 // A workgroup holds TPW tiles of S waves each; its waves share the
-// activation staging.  Wave w of a tile sweeps one K segment in laps of one
-// scale group (4 chunks = 8 blocks): the MFMAs of the lap's chunks, each
-// followed by the refill of its ring slot with the chunk RL laps ahead,
-// then the eight terms t_b = ((f32)dot_b * s_a) * d_b (q8_direct.rs:281),
-// folded in block order (w == 0) or stored to LDS (w > 0), then the refill
-// of the lap's scale slot.  With S > 1, after a barrier wave 0 of the tile
-// continues its fold over the later segments in block order; either way the
-// f32 result is bit-identical to the sequential reference.
+// activation staging.  A tile's K is swept in laps of one scale group
+// (4 chunks = 8 blocks) dealt out round-robin: in round R wave w takes lap
+// R*S + w, so each round covers S consecutive laps.  Per lap a wave runs
+// the MFMAs of its chunks (each followed by the refill of its ring slot
+// with the chunk RL laps ahead) and forms the eight terms
+// t_b = ((f32)dot_b * s_a) * d_b (q8_direct.rs:281).  Wave 0 adds its own
+// terms to the running sum at once; the other waves leave theirs in LDS.
+// Every round ends with an LDS-only barrier, after which wave 0 adds the
+// round's remaining S-1 laps in block order.  The f32 result is therefore
+// bit-identical to the sequential reference, and only the last round's
+// terms remain to be added after the sweep.
 // ---------------------------------------------------------------------------
+
+// Barrier for LDS traffic only: waits for this wave's LDS operations, not
+// for its outstanding global loads (the ring stays in flight).
+__device__ inline void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 template <int MR, int S, int TPW, int RL, int XR, bool FUSED, bool DEBUG>
 __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     ActIn in, int M, int kp, const float *__restrict__ sa_rows,
@@ -35,38 +45,33 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     constexpr int NW = S * TPW;               // waves per workgroup
     constexpr int LR = MR == 1 ? 1 : 2;       // rows per result lane
     constexpr int LG = (MR + 1) / 2;          // lane groups holding results
+    constexpr int TW = 8 * LR;                // terms per result lane per lap
     static_assert(!FUSED || MR == 1, "the fused prologue quantizes one row");
     extern __shared__ v4i s_lds[];
     const int wl = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int tw_ = wl / S;                   // tile of the wave within the WG
-    const int w = wl - tw_ * S;               // segment of the wave
+    const int w = wl - tw_ * S;               // lap slot of the wave
     const int T = blockIdx.x * TPW + tw_;
     const bool tile_ok = T < n_tiles;
     const int Tc = tile_ok ? T : n_tiles - 1; // address of a missing tile
     const int l = threadIdx.x & 63;
     const int r = l & 15, g = l >> 4;
-    const int q0 = split_lo(G, S, w);
-    const int q1 = tile_ok ? split_lo(G, S, w + 1) : q0;
-    const int nq = q1 - q0;                   // laps of this wave
-    const int c0 = 4 * q0;                    // first chunk of the segment
-    const int lastq = max(q1 - 1, 0);
-    const int maxq = (G + S - 1) / S;
-    const int tstride = 8 * maxq;             // floats per (lane, row) of terms
+    const int NR = (G + S - 1) / S;           // rounds
+    const int nq = tile_ok && w < G ? (G - w + S - 1) / S : 0;  // laps of this wave
     const size_t pitch = (size_t)n_tiles * kWave;
     const size_t spitch = (size_t)n_tiles * 16;
     const v4i *wp = tiles + (size_t)Tc * kWave + l;
     const v4i *sp = qscales + (size_t)Tc * 16 + r;
     const int n = T * 16 + r;
 
-    // LDS: [act M*kp][red NW floats][terms TPW x (S-1) x LG x 16 x LR x 8*maxq floats]
+    // LDS: [act M*kp][red NW floats][terms 2 x TPW x (S-1) x LG x 16 x TW floats]
     int8_t *s_act = reinterpret_cast<int8_t *>(s_lds);
     float *red = reinterpret_cast<float *>(s_act + (size_t)M * kp);
     float *terms = red + 4 * NW;
-    auto term_base = [&](int seg) {  // terms of segment seg >= 1 of this tile, this lane
-        return terms + ((size_t)((tw_ * (S - 1) + seg - 1) * LG + (g < LG ? g : 0)) * 16 + r) *
-                           LR * tstride;
+    auto tslot = [&](int par, int ww) {  // terms of wave ww >= 1 in round parity par, this lane
+        return terms +
+               ((((size_t)(par * TPW + tw_) * (S - 1) + (ww - 1)) * LG + (g < LG ? g : 0)) * 16 + r) * TW;
     };
-    float *tl = term_base(w > 0 ? w : 1);
 
     // A operand: lane (r, g) reads activation row r/2 (16 bytes of lane
     // group g of each chunk) and keeps the half of block 2p + (r & 1).
@@ -90,10 +95,10 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     }
     act_begin<NW, XR, FUSED>(in, n16, xr, s_act, red);
     // prime the ring in the steady state's issue order (a lap's quants, then
-    // its scales), indices clamped to the segment
+    // its scales), lap indices clamped to the tile
 #pragma unroll
     for (int u = 0; u < RL; ++u) {
-        const int q = min(q0 + u, lastq);
+        const int q = min(min(u, max(nq - 1, 0)) * S + w, G - 1);
 #pragma unroll
         for (int s = 0; s < 4; ++s)
             wr[u][s] = __builtin_nontemporal_load(wp + (size_t)(4 * q + s) * pitch);
@@ -104,15 +109,47 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
 #pragma unroll
     for (int j = 0; j < LR; ++j) fs[j] = 0.0f;
 
-    // Lap L of the segment in ring slot U.  REFILL: lap L + RL exists and is
-    // loaded into the slot; CHECK: skip padding blocks past nb (only the
-    // segment's last laps can hold them).
-    auto lap = [&](int L, auto slot, auto w0, bool refill, auto check)
-                   __attribute__((always_inline)) {
+    // End of round R: wave 0 adds laps R*S+1 .. R*S+S-1 (those that exist)
+    // in block order.
+    auto round_end = [&](int R) __attribute__((always_inline)) {
+        if constexpr (S > 1) {
+            lds_barrier();
+            if (w == 0) {
+                float4 tv[S - 1][TW / 4];
+#pragma unroll
+                for (int ww = 1; ww < S; ++ww) {
+                    const float4 *src = reinterpret_cast<const float4 *>(tslot(R & 1, ww));
+#pragma unroll
+                    for (int i = 0; i < TW / 4; ++i) tv[ww - 1][i] = src[i];
+                }
+#pragma unroll
+                for (int ww = 1; ww < S; ++ww) {
+                    const int cnt = min(nb - 8 * (R * S + ww), 8);  // valid blocks of the lap
+#pragma unroll
+                    for (int j = 0; j < LR; ++j) {
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) {
+                            const float4 v4 = tv[ww - 1][(8 * j + i) / 4];
+                            const int e = i & 3;
+                            const float t = e == 0 ? v4.x : e == 1 ? v4.y : e == 2 ? v4.z : v4.w;
+                            const float f = fs[j] + t;
+                            fs[j] = i < cnt ? f : fs[j];
+                        }
+                    }
+                }
+            }
+        }
+    };
+
+    // Lap L of this wave (round L, lap index L*S + w) in ring slot U.
+    // REFILL: lap L + RL exists and is loaded into the slot; CHECK: skip
+    // padding blocks past nb (only the tile's last lap can hold them).
+    auto lap = [&](int L, auto slot, bool refill, auto check) __attribute__((always_inline)) {
         constexpr int U = decltype(slot)::value;
+        const int q = L * S + w;
         v4i a[4];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) a[s] = ap[(size_t)(c0 + 4 * L + s) * 4];
+        for (int s = 0; s < 4; ++s) a[s] = ap[(size_t)(4 * q + s) * 4];
         int dt[4][2 * LR];
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
@@ -122,37 +159,56 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
 #pragma unroll
             for (int i = 0; i < 2 * LR; ++i) dt[s][i] = d[i];
             if (refill)
-                wr[U][s] =
-                    __builtin_nontemporal_load(wp + (size_t)(c0 + 4 * (L + RL) + s) * pitch);
+                wr[U][s] = __builtin_nontemporal_load(wp + (size_t)(4 * (q + RL * S) + s) * pitch);
         }
+        float tv[LR][8];
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const int bl = 8 * L + 2 * s + h;   // block within the segment
-                const int b = 8 * q0 + bl;
+                const unsigned word = (unsigned)sr[U][s];
+                const float d = f16_bits_to_f32(h ? (word >> 16) : (word & 0xFFFFu));
+#pragma unroll
+                for (int j = 0; j < LR; ++j) {
+                    float t = (float)dt[s][2 * j + h] * sa[j];
+                    tv[j][2 * s + h] = t * d;
+                }
+            }
+        }
+        if (w == 0) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int b = 8 * q + i;
                 if (!decltype(check)::value || b < nb) {
-                    const unsigned word = (unsigned)sr[U][s];
-                    const float d = f16_bits_to_f32(h ? (word >> 16) : (word & 0xFFFFu));
+#pragma unroll
+                    for (int j = 0; j < LR; ++j) fs[j] = fs[j] + tv[j][i];
+                }
+            }
+        } else if (g < LG) {
+            float4 *dst = reinterpret_cast<float4 *>(tslot(L & 1, w));
+#pragma unroll
+            for (int j = 0; j < LR; ++j) {
+                dst[2 * j] = float4{tv[j][0], tv[j][1], tv[j][2], tv[j][3]};
+                dst[2 * j + 1] = float4{tv[j][4], tv[j][5], tv[j][6], tv[j][7]};
+            }
+        }
+        if constexpr (DEBUG) {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int b = 8 * q + 2 * s + h;
 #pragma unroll
                     for (int j = 0; j < LR; ++j) {
-                        float t = (float)dt[s][2 * j + h] * sa[j];
-                        t = t * d;
-                        if constexpr (decltype(w0)::value) fs[j] = fs[j] + t;
-                        else if (g < LG) tl[j * tstride + bl] = t;
-                    }
-                    if constexpr (DEBUG) {
-#pragma unroll
-                        for (int j = 0; j < LR; ++j) {
-                            const int row = 2 * g + j;
-                            if (g < LG && row < M && n < N)
-                                block_dots[((size_t)row * N + n) * nb + b] = dt[s][2 * j + h];
-                        }
+                        const int row = 2 * g + j;
+                        if (b < nb && g < LG && row < M && n < N)
+                            block_dots[((size_t)row * N + n) * nb + b] = dt[s][2 * j + h];
                     }
                 }
             }
         }
-        if (refill) sr[U] = sp[(size_t)(q0 + L + RL) * spitch];
+        if (refill) sr[U] = sp[(size_t)(q + RL * S) * spitch];
+        round_end(L);
     };
 
     using T1 = std::true_type;
@@ -160,42 +216,20 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     // k full rounds of RL laps; the loop holds the rounds whose refills all
     // exist (branch-free, so the wait counts stay exact); the last full
     // round refills only the remainder's rem laps, which then run last.
-    auto sweep = [&](auto w0) __attribute__((always_inline)) {
+    {
         const int k = nq / RL, rem = nq - k * RL;
         for (int it = 0; it + 1 < k; ++it)
-            static_for<RL>([&](auto u) { lap(it * RL + u, u, w0, true, F0{}); });
+            static_for<RL>([&](auto u) { lap(it * RL + u, u, true, F0{}); });
         if (k > 0)
-            static_for<RL>([&](auto u) { lap((k - 1) * RL + u, u, w0, u < rem, T1{}); });
+            static_for<RL>([&](auto u) { lap((k - 1) * RL + u, u, u < rem, T1{}); });
         static_for<RL>([&](auto u) {
-            if (u < rem) lap(k * RL + u, u, w0, false, T1{});
+            if (u < rem) lap(k * RL + u, u, false, T1{});
         });
-    };
-    if (w == 0) sweep(T1{});
-    else sweep(F0{});
-
-    if constexpr (S > 1) {
-        __syncthreads();
-        if (w != 0 || g >= LG) return;
-        // continue the block-ordered fold over the later segments; the
-        // terms of a segment are contiguous per lane (16-byte reads)
-        for (int seg = 1; seg < S; ++seg) {
-            const int e0 = split_lo(G, S, seg), e1 = split_lo(G, S, seg + 1);
-            const int cnt = max(min(8 * (e1 - e0), nb - 8 * e0), 0);
-            const float *ts = term_base(seg);
-#pragma unroll
-            for (int j = 0; j < LR; ++j) {
-                const float4 *t4 = reinterpret_cast<const float4 *>(ts + j * tstride);
-                int bl = 0;
-                for (; bl + 8 <= cnt; bl += 8) {
-                    const float4 u = t4[bl / 4], v = t4[bl / 4 + 1];
-                    fs[j] = fs[j] + u.x; fs[j] = fs[j] + u.y; fs[j] = fs[j] + u.z; fs[j] = fs[j] + u.w;
-                    fs[j] = fs[j] + v.x; fs[j] = fs[j] + v.y; fs[j] = fs[j] + v.z; fs[j] = fs[j] + v.w;
-                }
-                for (; bl < cnt; ++bl) fs[j] = fs[j] + ts[j * tstride + bl];
-            }
-        }
     }
-    if (!tile_ok || g >= LG || n >= N) return;
+    // rounds in which this wave has no lap (the barrier count is uniform)
+    for (int R = nq; R < NR; ++R) round_end(R);
+
+    if (w != 0 || !tile_ok || g >= LG || n >= N) return;
 #pragma unroll
     for (int j = 0; j < LR; ++j) {
         const int row = 2 * g + j;
@@ -212,11 +246,10 @@ struct CfgQ8 {
 inline int mr_of(size_t m) { return m <= 1 ? 1 : m == 2 ? 2 : 4; }
 
 size_t lds_q8(int s, int tpw, size_t m, size_t kp, size_t G) {
-    const size_t maxq = (G + s - 1) / s;
+    (void)G;
     const size_t mr = (size_t)mr_of(m);
     const size_t lr = mr == 1 ? 1 : 2, lg = (mr + 1) / 2;
-    return m * kp + (size_t)s * tpw * 16 +
-           (size_t)tpw * (s - 1) * lg * 16 * lr * 8 * maxq * 4;
+    return m * kp + (size_t)s * tpw * 16 + 2 * (size_t)tpw * (s - 1) * lg * 16 * lr * 8 * 4;
 }
 
 // Configuration by the number of 16-row tiles (measured on MI355X).  Many

@@ -70,6 +70,14 @@ def lib():
         if not os.path.exists(LIB_PATH):
             raise ImportError(
                 f"{LIB_PATH} is not built; run __graft_entry__.build() first")
+        # torch ships its own libamdhip64.so.7 under the same soname as the
+        # system one the library links against; whichever is loaded first
+        # serves the whole process.  Load torch's first so that torch, whose
+        # tensors carry the device buffers, keeps the runtime it was built for.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         l = C.CDLL(LIB_PATH)
         for name, (args, res) in _SIGS.items():
             f = getattr(l, name)
