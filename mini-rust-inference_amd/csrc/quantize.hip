@@ -98,7 +98,22 @@ __global__ __launch_bounds__(kThreads) void k_quantize_tensor(
     }
 }
 
-// One block per row: quantize_symmetric of each row separately.
+__device__ inline float absmax4(float m, const float4 &v) {
+    return fmaxf(fmaxf(m, fmaxf(fabsf(v.x), fabsf(v.y))), fmaxf(fabsf(v.z), fabsf(v.w)));
+}
+
+// Offset of element kk (kk % 4 == 0 keeps 4 elements contiguous) in a
+// padded output row, chunk-permuted when perm.
+__device__ inline size_t row_pos(size_t kk, int perm) {
+    return perm ? (kk & ~(size_t)63) + q8_perm((int)(kk & 63)) : kk;
+}
+
+// One block per row: quantize_symmetric of each row separately.  NV > 0:
+// the row (16-byte aligned, k % 4 == 0, k <= NV * 4 * kThreads, 4-byte
+// aligned outputs) is loaded once as float4 into registers, NV loads in
+// flight per thread, and written four int8 at a time.  NV == 0: element-wise
+// path for every other shape.
+template <int NV>
 __global__ __launch_bounds__(kThreads) void k_quantize_rows(
     const float *__restrict__ x, size_t k, size_t ld, int perm,
     int8_t *__restrict__ q_pad, int8_t *__restrict__ q_plain,
@@ -106,24 +121,74 @@ __global__ __launch_bounds__(kThreads) void k_quantize_rows(
     __shared__ float red[kThreads / 64];
     const size_t r = blockIdx.x;
     const float *row = x + r * k;
+    const size_t t = threadIdx.x;
     float mx = 0.0f;
-    for (size_t i = threadIdx.x; i < k; i += blockDim.x)
-        mx = fmaxf(mx, fabsf(row[i]));
-    mx = block_max(mx, red);
-    const float scale = scale_of(mx);
-    const float inv = __fdiv_rn(1.0f, scale);
-    if (threadIdx.x == 0 && scales) scales[r] = scale;
-    for (size_t kk = threadIdx.x; kk < ld; kk += blockDim.x) {
-        int8_t q = 0;
-        if (kk < k) {
-            q = round_clamp_i8(row[kk] * inv);
-            if (q_plain) q_plain[r * k + kk] = q;
+    if constexpr (NV > 0) {
+        const float4 *r4 = reinterpret_cast<const float4 *>(row);
+        const size_t k4 = k / 4;
+        float4 v[NV];
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const size_t i = t + (size_t)j * kThreads;
+            v[j] = i < k4 ? r4[i] : float4{0.0f, 0.0f, 0.0f, 0.0f};
         }
-        if (q_pad) {
-            size_t pos = kk;
-            if (perm) pos = (kk & ~(size_t)63) + q8_perm((int)(kk & 63));
-            q_pad[r * ld + pos] = q;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) mx = absmax4(mx, v[j]);
+        mx = block_max(mx, red);
+        const float scale = scale_of(mx);
+        const float inv = __fdiv_rn(1.0f, scale);
+        if (t == 0 && scales) scales[r] = scale;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const size_t kk = 4 * (t + (size_t)j * kThreads);
+            if (kk < k) {
+                const int packed = ((int)round_clamp_i8(v[j].x * inv) & 255) |
+                                   (((int)round_clamp_i8(v[j].y * inv) & 255) << 8) |
+                                   (((int)round_clamp_i8(v[j].z * inv) & 255) << 16) |
+                                   ((int)round_clamp_i8(v[j].w * inv) << 24);
+                if (q_plain) *reinterpret_cast<int *>(q_plain + r * k + kk) = packed;
+                if (q_pad) *reinterpret_cast<int *>(q_pad + r * ld + row_pos(kk, perm)) = packed;
+            }
         }
+        // zero padding of the output row
+        if (q_pad)
+            for (size_t kk = k + 4 * t; kk < ld; kk += 4 * kThreads)
+                *reinterpret_cast<int *>(q_pad + r * ld + row_pos(kk, perm)) = 0;
+    } else {
+        for (size_t i = t; i < k; i += blockDim.x) mx = fmaxf(mx, fabsf(row[i]));
+        mx = block_max(mx, red);
+        const float scale = scale_of(mx);
+        const float inv = __fdiv_rn(1.0f, scale);
+        if (t == 0 && scales) scales[r] = scale;
+        for (size_t kk = t; kk < ld; kk += blockDim.x) {
+            int8_t q = 0;
+            if (kk < k) {
+                q = round_clamp_i8(row[kk] * inv);
+                if (q_plain) q_plain[r * k + kk] = q;
+            }
+            if (q_pad) q_pad[r * ld + row_pos(kk, perm)] = q;
+        }
+    }
+}
+
+// float4s per thread of the register-resident row path for k (0: none).
+inline int rows_nv(const float *x, size_t k, size_t ld, const int8_t *q_pad,
+                   const int8_t *q_plain) {
+    if ((k & 3) || (ld & 3) || (reinterpret_cast<uintptr_t>(x) & 15) ||
+        (reinterpret_cast<uintptr_t>(q_pad) & 3) || (reinterpret_cast<uintptr_t>(q_plain) & 3))
+        return 0;
+    const size_t per = (k / 4 + kThreads - 1) / kThreads;
+    return per <= 4 ? 4 : per <= 8 ? 8 : per <= 16 ? 16 : 0;
+}
+
+void launch_rows(const float *x, size_t m, size_t k, size_t ld, int perm, int8_t *q_pad,
+                 int8_t *q_plain, float *scales, hipStream_t s) {
+    const dim3 grid((unsigned)m), block(kThreads);
+    switch (rows_nv(x, k, ld, q_pad, q_plain)) {
+    case 4: hipLaunchKernelGGL(k_quantize_rows<4>, grid, block, 0, s, x, k, ld, perm, q_pad, q_plain, scales); break;
+    case 8: hipLaunchKernelGGL(k_quantize_rows<8>, grid, block, 0, s, x, k, ld, perm, q_pad, q_plain, scales); break;
+    case 16: hipLaunchKernelGGL(k_quantize_rows<16>, grid, block, 0, s, x, k, ld, perm, q_pad, q_plain, scales); break;
+    default: hipLaunchKernelGGL(k_quantize_rows<0>, grid, block, 0, s, x, k, ld, perm, q_pad, q_plain, scales); break;
     }
 }
 
@@ -279,9 +344,7 @@ mri_status launch_quantize_rows(const float *x, size_t m, size_t k,
                                 int8_t *q_pad, int8_t *q_plain,
                                 float *scales, hipStream_t s) {
     if (m == 0) return MRI_OK;
-    hipLaunchKernelGGL(k_quantize_rows, dim3((unsigned)m), dim3(kThreads), 0, s,
-                       x, k, q_pad ? ld_out : k, q8_perm_layout ? 1 : 0, q_pad,
-                       q_plain, scales);
+    launch_rows(x, m, k, q_pad ? ld_out : k, q8_perm_layout ? 1 : 0, q_pad, q_plain, scales, s);
     MRI_LAUNCHED("k_quantize_rows");
     return MRI_OK;
 }
@@ -290,8 +353,7 @@ mri_status launch_quantize_per_channel(const float *w, size_t n, size_t k,
                                        int8_t *data, float *scales,
                                        hipStream_t s) {
     if (n == 0) return MRI_OK;
-    hipLaunchKernelGGL(k_quantize_rows, dim3((unsigned)n), dim3(kThreads), 0, s,
-                       w, k, k, 0, data, (int8_t *)nullptr, scales);
+    launch_rows(w, n, k, k, 0, data, nullptr, scales, s);
     MRI_LAUNCHED("k_quantize_rows(per_channel)");
     return MRI_OK;
 }

@@ -1,11 +1,9 @@
-// skinny.hip — decode-shaped (M <= 32) quantized matmul on CDNA4 MFMA.
+// skinny.hip — decode-shaped (5..32 rows per launch; larger M loops over
+// 32-row slices) quantized matmul on CDNA4 MFMA.
 //
 // The weight stream dominates (M*K activation bytes vs N*K weight bytes), so
-// the kernel is built around streaming the 1 KiB weight chunks of one
-// 16-row tile per wave with deep software prefetch:
-//   * one wave (= one workgroup) per tile of 16 output channels, all of K;
-//   * per chunk (64 k): one 16-byte global load per lane for the weights and
-//     one 16-byte read per 16-row activation tile;
+// both kernels stream the slab-major 1 KiB weight chunks of one 16-row tile
+// per wave, with the activation rows read from a quantized [M][kp] buffer:
 //   * per-channel INT8: v_mfma_i32_16x16x64_i8 accumulates exact int32 dot
 //     products for 16 (m) x 16 (n) outputs; the f32 epilogue
 //     ((f32)acc * s_a) * s_w runs once at the end (int8.rs:93);
@@ -15,27 +13,15 @@
 //     q8_direct.rs:269-282, so the f32 result is bit-identical.
 // MFMA output mapping (16x16 family): lane l, register i holds row
 // (activation) m = 4*(l/16) + i and column (weight row) n = l % 16.
-//
-// This is the general M <= 32 path (one wave per tile, activations read from
-// a quantized [M][kp] buffer).  The M <= 4 decode case uses the K-split
-// kernels of gemv.hip instead.
+// The M <= 4 decode case uses the K-split kernels of gemv_int8.hip and
+// gemv_q8.hip instead.
 #include <type_traits>
 
-#include "common.hpp"
+#include "gemv_common.hpp"
 
 namespace mri {
+using namespace gemv;
 namespace {
-
-typedef int v4i __attribute__((ext_vector_type(4)));
-
-constexpr int kWave = 64;
-
-__device__ inline long lo8(const v4i &v) {
-    return (long)(((unsigned long)(unsigned)v.y << 32) | (unsigned)v.x);
-}
-__device__ inline long hi8(const v4i &v) {
-    return (long)(((unsigned long)(unsigned)v.w << 32) | (unsigned)v.z);
-}
 
 // ---------------------------------------------------------------------------
 // Per-channel INT8.  MT activation tiles of 16 rows; NI = output registers
@@ -146,154 +132,139 @@ __global__ __launch_bounds__(kWave) void k_skinny_int8(
 }
 
 // ---------------------------------------------------------------------------
-// Q8_0.  U must be a multiple of 4: one 16-byte scale load covers 8 blocks
-// = 4 chunks of the lane's weight row.
+// Q8_0, up to 32 rows: AG groups of 16 activation rows.  One wave per tile
+// of 16 output channels sweeps all of K in laps of one scale group (4
+// chunks = 8 blocks) and keeps RL laps of loads in flight: per chunk one
+// 16-byte load of the weight chunk and, per activation group, one 16-byte
+// load of the rows' matching activation bytes (chunk-permuted, so its two
+// halves are the A operands of the chunk's two blocks).  Per block and
+// group one v_mfma_i32_16x16x32_i8 gives the exact int32 dots of 16 rows x
+// 16 channels; each lane then adds ((f32)dot * s_a[m]) * d[n,b] to its
+// running sums in block order (q8_direct.rs:269-282), so the f32 result is
+// bit-identical.  The sweep has no global memory instruction other than the
+// ring's loads and no data-dependent branch, so every wait leaves the
+// younger loads in flight.  Rows m >= M read row 0's activations; their
+// results are never stored.
 // ---------------------------------------------------------------------------
-template <int MT, int NI, int U>
-__global__ __launch_bounds__(kWave) void k_skinny_q8_0(
-    const int8_t *__restrict__ act, int M, size_t kp,
-    const float *__restrict__ sa_rows, const v4i *__restrict__ tiles,
-    const v4i *__restrict__ qscales, int N, int P, int Q, int nb,
-    float *__restrict__ out, int32_t *__restrict__ block_dots) {
-    static_assert(U % 4 == 0, "U must cover whole scale groups");
-    const int T = blockIdx.x;
-    const int l = threadIdx.x;
+template <int AG, int TPW, int RL, bool DEBUG>
+__global__ __launch_bounds__(TPW * kWave) void k_skinny_q8_0(
+    const int8_t *__restrict__ act, int M, int kp, const float *__restrict__ sa_rows,
+    const v4i *__restrict__ tiles, const v4i *__restrict__ qscales, int N,
+    int n_tiles, int G, int nb, float *__restrict__ out,
+    int32_t *__restrict__ block_dots, int ns) {
+    // wave -> (tile, set of AG activation groups); the ns waves of a tile are
+    // adjacent, so they share a workgroup (or neighbouring ones) and the
+    // weight chunks they all stream are fetched from HBM once
+    const int wv = blockIdx.x * TPW + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int T = wv / ns;
+    const int a0 = (wv - T * ns) * AG;  // first activation group of the wave
+    if (T >= n_tiles) return;  // whole waves only; the kernel has no barrier
+    const int l = threadIdx.x & 63;
     const int r = l & 15, g = l >> 4;
-    const int Pe = (nb + 1) / 2;  // chunks holding real blocks
-    const size_t pitch = (size_t)gridDim.x * kWave;   // slab-major chunks
-    const size_t spitch = (size_t)gridDim.x * 16;     // slab-major scale groups
+    const size_t pitch = (size_t)n_tiles * kWave;
+    const size_t spitch = (size_t)n_tiles * 16;
     const v4i *wp = tiles + (size_t)T * kWave + l;
     const v4i *sp = qscales + (size_t)T * 16 + r;
-    const v4i *ap[MT];
-    bool aval[MT];
+    const int n = T * 16 + r;
+    const v4i *ap[AG];
+    float sa[AG][4], fs[AG][4];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-        const int m = mt * 16 + r;
-        aval[mt] = m < M;
-        ap[mt] = reinterpret_cast<const v4i *>(act + (size_t)(aval[mt] ? m : 0) * kp) + g;
+    for (int a = 0; a < AG; ++a) {
+        const int m = 16 * (a0 + a) + r;
+        ap[a] = reinterpret_cast<const v4i *>(act + (size_t)(m < M ? m : 0) * kp) + g;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sa[a][i] = sa_rows[min(16 * (a0 + a) + 4 * g + i, M - 1)];
+            fs[a][i] = 0.0f;
+        }
+    }
+    v4i wr[RL][4];
+    v4i xr[RL][4][AG];
+    v4i sr[RL];
+#pragma unroll
+    for (int u = 0; u < RL; ++u) {
+        const int q = min(u, G - 1);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            wr[u][c] = __builtin_nontemporal_load(wp + (size_t)(4 * q + c) * pitch);
+#pragma unroll
+            for (int a = 0; a < AG; ++a) xr[u][c][a] = ap[a][(size_t)(4 * q + c) * 4];
+        }
+        sr[u] = sp[(size_t)q * spitch];
     }
     const v4i zero = {0, 0, 0, 0};
-    float fs[MT][NI];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int i = 0; i < NI; ++i) fs[mt][i] = 0.0f;
 
-    v4i wb[2][U];
-    v4i ab[2][MT][U];
-    v4i sb[2][U / 4];
-    const int n = T * 16 + r;
-    const bool n_ok = n < N;
-
-    auto load_w = [&](int buf, int p0) __attribute__((always_inline)) {
+    // Lap L in ring slot U.  REFILL: lap L + RL exists and is loaded into
+    // the slot; CHECK: skip padding blocks past nb (last laps only).
+    auto lap = [&](int L, auto slot, bool refill, auto check) __attribute__((always_inline)) {
+        constexpr int U = decltype(slot)::value;
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int p = min(p0 + u, Pe - 1);
-            wb[buf][u] = __builtin_nontemporal_load(wp + (size_t)p * pitch);
-            if ((u & 3) == 0) sb[buf][u / 4] = sp[(size_t)(p / 4) * spitch];
-        }
-    };
-    auto load_a = [&](int buf, int p0) __attribute__((always_inline)) {
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-                ab[buf][mt][u] = ap[mt][(size_t)min(p0 + u, Pe - 1) * 4];
-    };
-
-    float sa[MT][NI];
-    // Phase 1 issues the 2U independent block MFMAs of a group; phase 2
-    // applies the f32 epilogue and adds the terms in block order.
-    auto compute = [&](int buf, int p0, auto guard) __attribute__((always_inline)) {
-        constexpr bool G = decltype(guard)::value;
-        v4i dots[U][2][MT];
-#pragma unroll
-        for (int u = 0; u < U; ++u)
+        for (int c = 0; c < 4; ++c) {
+            v4i d[2][AG];
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const long wv = h ? hi8(wb[buf][u]) : lo8(wb[buf][u]);
+                const long bv = h ? hi8(wr[U][c]) : lo8(wr[U][c]);
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    const v4i a = aval[mt] ? ab[buf][mt][u] : zero;
-                    dots[u][h][mt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
-                        h ? hi8(a) : lo8(a), wv, zero, 0, 0, 0);
-                }
+                for (int a = 0; a < AG; ++a)
+                    d[h][a] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+                        h ? hi8(xr[U][c][a]) : lo8(xr[U][c][a]), bv, zero, 0, 0, 0);
+            }
+            if (refill) {
+                const size_t p = (size_t)(4 * (L + RL) + c);
+                wr[U][c] = __builtin_nontemporal_load(wp + p * pitch);
+#pragma unroll
+                for (int a = 0; a < AG; ++a) xr[U][c][a] = ap[a][p * 4];
             }
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-#pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const int b = 2 * (p0 + u) + h;
-                if (!G || b < nb) {
-                    const int j = (2 * u + h) & 7;  // block within scale group
-                    const unsigned word = (unsigned)sb[buf][u / 4][j >> 1];
-                    const float d =
-                        f16_bits_to_f32((j & 1) ? (word >> 16) : (word & 0xFFFFu));
+                const int b = 8 * L + 2 * c + h;
+                if (!decltype(check)::value || b < nb) {
+                    const unsigned word = (unsigned)sr[U][c];
+                    const float ds = f16_bits_to_f32(h ? (word >> 16) : (word & 0xFFFFu));
 #pragma unroll
-                    for (int mt = 0; mt < MT; ++mt) {
+                    for (int a = 0; a < AG; ++a) {
 #pragma unroll
-                        for (int i = 0; i < NI; ++i) {
-                            float t = (float)dots[u][h][mt][i] * sa[mt][i];
-                            t = t * d;
-                            fs[mt][i] = fs[mt][i] + t;
+                        for (int i = 0; i < 4; ++i) {
+                            float t = (float)d[h][a][i] * sa[a][i];
+                            t = t * ds;
+                            fs[a][i] = fs[a][i] + t;
                         }
-                        if (block_dots && n_ok) {
+                        if constexpr (DEBUG) {
 #pragma unroll
-                            for (int i = 0; i < NI; ++i) {
-                                const int m = mt * 16 + 4 * g + i;
-                                if (m < M)
-                                    block_dots[((size_t)m * N + n) * nb + b] =
-                                        dots[u][h][mt][i];
+                            for (int i = 0; i < 4; ++i) {
+                                const int m = 16 * (a0 + a) + 4 * g + i;
+                                if (m < M && n < N)
+                                    block_dots[((size_t)m * N + n) * nb + b] = d[h][a][i];
                             }
                         }
                     }
                 }
             }
         }
+        if (refill) sr[U] = sp[(size_t)(L + RL) * spitch];
+        // keep the next lap's uses of its (younger) loads below this point
+        __builtin_amdgcn_sched_barrier(0);
     };
 
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            const int m = mt * 16 + 4 * g + i;
-            sa[mt][i] = m < M ? sa_rows[m] : 0.0f;
-        }
-    load_w(0, 0);
-    load_a(0, 0);
-
-    // Full groups (all 2U blocks real) run unguarded; the tail is guarded.
-    const int p_full =
-        (nb % 2 == 0) ? Pe - Pe % (2 * U) : (Pe - 1) - (Pe - 1) % (2 * U);
-    int p0 = 0;
-    for (; p0 < p_full; p0 += 2 * U) {
-        load_w(1, p0 + U);
-        load_a(1, p0 + U);
-        __builtin_amdgcn_sched_barrier(0);
-        compute(0, p0, std::false_type{});
-        __builtin_amdgcn_sched_barrier(0);
-        load_w(0, p0 + 2 * U);
-        load_a(0, p0 + 2 * U);
-        __builtin_amdgcn_sched_barrier(0);
-        compute(1, p0 + U, std::false_type{});
-        __builtin_amdgcn_sched_barrier(0);
+    using T1 = std::true_type;
+    using F0 = std::false_type;
+    {
+        const int k = G / RL, rem = G - k * RL;
+        for (int it = 0; it + 1 < k; ++it)
+            static_for<RL>([&](auto u) { lap(it * RL + u, u, true, F0{}); });
+        if (k > 0)
+            static_for<RL>([&](auto u) { lap((k - 1) * RL + u, u, u < rem, T1{}); });
+        static_for<RL>([&](auto u) {
+            if (u < rem) lap(k * RL + u, u, false, T1{});
+        });
     }
-    for (; p0 < Pe; p0 += U) {
-        // tail: one group at a time from buffer 0
-        __builtin_amdgcn_sched_barrier(0);
-        compute(0, p0, std::true_type{});
-        __builtin_amdgcn_sched_barrier(0);
-        load_w(0, p0 + U);
-        load_a(0, p0 + U);
-    }
-
-    if (!n_ok) return;
+    if (n >= N) return;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int a = 0; a < AG; ++a)
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            const int m = mt * 16 + 4 * g + i;
-            if (m < M) out[(size_t)m * N + n] = fs[mt][i];
+        for (int i = 0; i < 4; ++i) {
+            const int m = 16 * (a0 + a) + 4 * g + i;
+            if (m < M) out[(size_t)m * N + n] = fs[a][i];
         }
 }
 
@@ -309,15 +280,17 @@ void launch_i8(const int8_t *act, size_t m, size_t kp, const float *sa_ptr,
                        (int)w.n_out, (int)(w.kp / kChunkK), out, acc_out);
 }
 
-template <int MT, int NI, int U>
+// AG activation groups per wave, ns waves per tile (AG * ns groups of 16 rows).
+template <int AG, int TPW, int RL, bool DEBUG>
 void launch_q8(const int8_t *act, size_t m, size_t kp, const float *sa_rows,
-               const Q8MatrixDev &w, float *out, int32_t *block_dots, hipStream_t s) {
-    hipLaunchKernelGGL((k_skinny_q8_0<MT, NI, U>), dim3((unsigned)w.n_tiles),
-                       dim3(kWave), 0, s, act, (int)m, kp, sa_rows,
-                       reinterpret_cast<const v4i *>(w.tiles),
-                       reinterpret_cast<const v4i *>(w.scales), (int)w.n_out,
-                       (int)(w.kp / kChunkK), (int)(w.kp / (kQK * kQ8ScaleGroup)),
-                       (int)w.n_blocks, out, block_dots);
+               const Q8MatrixDev &w, float *out, int32_t *block_dots, int ns, hipStream_t s) {
+    const int G = (int)(((w.n_blocks + 1) / 2 + 3) / 4);  // laps holding real blocks
+    const size_t waves = w.n_tiles * (size_t)ns;
+    hipLaunchKernelGGL((k_skinny_q8_0<AG, TPW, RL, DEBUG>),
+                       dim3((unsigned)((waves + TPW - 1) / TPW)), dim3(TPW * kWave), 0, s,
+                       act, (int)m, (int)kp, sa_rows, reinterpret_cast<const v4i *>(w.tiles),
+                       reinterpret_cast<const v4i *>(w.scales), (int)w.n_out, (int)w.n_tiles, G,
+                       (int)w.n_blocks, out, block_dots, ns);
 }
 
 }  // namespace
@@ -353,8 +326,15 @@ mri_status launch_skinny_q8_0(const int8_t *act, size_t m,
         const float *sp = sa_rows + m0;
         float *o = out + m0 * w.n_out;
         int32_t *bd = block_dots ? block_dots + m0 * w.n_out * w.n_blocks : nullptr;
-        if (mc <= 16) launch_q8<1, 4, kU>(a, mc, kp, sp, w, o, bd, s);
-        else launch_q8<2, 4, 4>(a, mc, kp, sp, w, o, bd, s);
+        // one wave per tile and workgroup (measured on MI355X: splitting a
+        // tile's row groups over waves, or grouping tiles, is slower)
+        if (bd) {
+            if (mc <= 16) launch_q8<1, 1, 2, true>(a, mc, kp, sp, w, o, bd, 1, s);
+            else launch_q8<2, 1, 2, true>(a, mc, kp, sp, w, o, bd, 1, s);
+        } else {
+            if (mc <= 16) launch_q8<1, 1, 3, false>(a, mc, kp, sp, w, o, bd, 1, s);
+            else launch_q8<2, 1, 2, false>(a, mc, kp, sp, w, o, bd, 1, s);
+        }
         MRI_LAUNCHED("k_skinny_q8_0");
     }
     return MRI_OK;

@@ -58,13 +58,17 @@ def test_quantize_ties_and_specials():
     assert host(sd)[0] == 1.0 and not host(qd).any()
 
 
-def test_quantize_rows_and_per_channel():
+@pytest.mark.parametrize("m,k", [(9, 333), (5, 4096), (3, 11008), (6, 64)])
+def test_quantize_rows_and_per_channel(m, k):
+    # k % 4 != 0 takes the element-wise path, the others the float4 path
+    # (k = 11008: unrolled loop plus remainder)
     t = torch()
-    rng = np.random.default_rng(7)
-    x = rng.standard_normal((9, 333)).astype(F32)
-    x[4] = 0.0
+    rng = np.random.default_rng(7 + k)
+    x = rng.standard_normal((m, k)).astype(F32)
+    x[m // 2] = 0.0
+    x[0, k // 3] = np.nan
     q0, s0 = CF.quantize_rows(x)
-    qd, sd = empty((9, 333), t.int8), empty(9, t.float32)
+    qd, sd = empty((m, k), t.int8), empty(m, t.float32)
     mri().quantize_symmetric_rows(dev(x), qd, sd)
     assert np.array_equal(host(qd), q0) and np.array_equal(bits(host(sd)), bits(s0))
     w = (rng.standard_normal((37, 96)) * 0.02).astype(F32)
