@@ -94,6 +94,32 @@ mri_status scratch_get(hipStream_t stream, size_t bytes, void **ptr) {
     return MRI_OK;
 }
 
+// Per-(device, stream) workspace of the stream-K GEMM.  Zeroed whenever it
+// is (re)allocated; the kernel leaves its counters zero after every call.
+static std::mutex g_ws_mu;
+static std::map<std::pair<int, hipStream_t>, Scratch> g_ws;
+
+mri_status gemm_ws_get(hipStream_t stream, size_t bytes, void **ptr) {
+    int dev = 0;
+    MRI_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    Scratch &sc = g_ws[{dev, stream}];
+    if (sc.bytes < bytes) {
+        const size_t want = round_up(bytes, 1u << 20);
+        if (sc.ptr) {
+            MRI_HIP(hipStreamSynchronize(stream));
+            MRI_HIP(hipFree(sc.ptr));
+            sc.ptr = nullptr;
+            sc.bytes = 0;
+        }
+        MRI_HIP(hipMalloc(&sc.ptr, want));
+        MRI_HIP(hipMemset(sc.ptr, 0, want));
+        sc.bytes = want;
+    }
+    *ptr = sc.ptr;
+    return MRI_OK;
+}
+
 static inline bool aligned(const void *p, size_t a) {
     return (reinterpret_cast<uintptr_t>(p) % a) == 0;
 }
@@ -477,7 +503,12 @@ static mri_status matmul_int8_common(const char *fn, const int8_t *act_q, size_t
         auto *packed = static_cast<int8_t *>(base);
         st = launch_pack_gemm(act_q, m, k, k, d.kp, packed, s);
         if (st) return st;
-        return launch_gemm_int8(packed, m, sa_ptr, sa_stride, sa_value, d, out, acc_out, s);
+        void *ws = nullptr;
+        if (const size_t wsb = gemm_ws_bytes(m, d)) {
+            st = gemm_ws_get(s, wsb, &ws);
+            if (st) return st;
+        }
+        return launch_gemm_int8(packed, m, sa_ptr, sa_stride, sa_value, d, out, acc_out, ws, s);
     }
     const int8_t *act = nullptr;
     st = prepare_act(act_q, m, d, s, &act);
@@ -542,7 +573,12 @@ mri_status mri_matmul_int8_from_f32(const float *input, const size_t *dims, size
         st = launch_quantize_pack(input, m, k, d.kp, act, act_q_out, scale, partials, s);
         if (st) return st;
         if (d.n_out == 0) return MRI_OK;
-        return launch_gemm_int8(act, m, scale, 0, 0.0f, d, out, acc_out, s);
+        void *ws = nullptr;
+        if (const size_t wsb = gemm_ws_bytes(m, d)) {
+            st = gemm_ws_get(s, wsb, &ws);
+            if (st) return st;
+        }
+        return launch_gemm_int8(act, m, scale, 0, 0.0f, d, out, acc_out, ws, s);
     }
     st = launch_quantize_tensor(input, m, k, d.kp, false, act, act_q_out, scale, partials, s);
     if (st) return st;

@@ -178,9 +178,16 @@ __host__ __device__ inline size_t gemm_pack_offset(size_t m, size_t k, size_t mg
     const size_t lane = (m & 31) + 32 * ((kk & 31) >> 4);
     return (((p * mg + (m >> 5)) * 2 + h) * 64 + lane) * 16 + (kk & 15);
 }
+// Workspace of the stream-K GEMM for m rows (0: the shape does not use
+// one): int32 partial tiles plus per-tile counters.  The counters must be
+// zero when the workspace is first used; every call leaves them zero.
+size_t gemm_ws_bytes(size_t m, const QMatrixDev &w);
 mri_status launch_gemm_int8(const int8_t *act_packed, size_t m, const float *sa_ptr,
                             int sa_stride, float sa_value, const QMatrixDev &w,
-                            float *out, int32_t *acc_out, hipStream_t s);
+                            float *out, int32_t *acc_out, void *ws, hipStream_t s);
+// Per-(device, stream) GEMM workspace (capi.cpp), grow-only, zeroed when
+// (re)allocated.
+mri_status gemm_ws_get(hipStream_t stream, size_t bytes, void **ptr);
 
 // q4_0.hip
 mri_status launch_q4_0_dequant(const float *x, size_t m, size_t k,

@@ -34,6 +34,10 @@
 // are placed on the same XCD, so they share its L2.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <type_traits>
+#include <utility>
+
 #include "common.hpp"
 
 namespace mri {
@@ -43,6 +47,15 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 constexpr int kWave = 64;
 constexpr int kXcds = 8;
+
+template <typename F, int... I>
+__device__ inline void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ inline void static_for(F &&f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 #ifndef DMA_B
 #define DMA_B dma16_nt
 #endif
@@ -64,6 +77,14 @@ __device__ inline void dma16(const void *g, unsigned lds) {
 // that it does not evict the operand that every workgroup re-reads from L2.
 __device__ inline void dma16_nt(const void *g, unsigned lds) {
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
+                 :
+                 : "v"(g), "s"(lds)
+                 : "memory", "m0");
+}
+
+// 4 bytes per lane from g into LDS at byte address lds + 4 * lane.
+__device__ inline void dma4(const void *g, unsigned lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
                  :
                  : "v"(g), "s"(lds)
                  : "memory", "m0");
@@ -241,6 +262,390 @@ __global__ __launch_bounds__(WM * WN * kWave) void k_gemm_int8(
     }
 }
 
+// ---------------------------------------------------------------------------
+// Stream-K form for the larger products: 256 x 256 output tiles, eight waves
+// (4 x 2) of 64 x 128 each (8 accumulators of 32 x 32), a 4-stage LDS ring
+// of 32 KiB K steps, and the loads and LDS reads of the next steps placed
+// between the MFMAs of the current one.
+//
+// The K steps of all tiles form one sequence of iterations (tile-major, the
+// M tiles of a weight column block adjacent); every workgroup of a
+// persistent grid (one per CU) takes an equal contiguous range of it, so
+// the work is balanced whatever the tile count.  The ring runs on across
+// tile boundaries.  A tile whose K range is split between workgroups is
+// finished by whichever contributor arrives last: the others store their
+// int32 partial tile to a workspace slot and increment the tile's counter;
+// the last one adds the partials to its own (exact: int32 addition wraps
+// and is associative, as the reference's i32 sums), applies the f32
+// epilogue and resets the counter to zero for the next call.  No workgroup
+// waits for another.
+// ---------------------------------------------------------------------------
+constexpr int kSkNs = 4;                        // ring stages
+constexpr int kSkTileInts = 256 * 256;          // int32 of one partial tile
+constexpr int kSkMaxTiles = 65536;              // tile counters at the workspace start
+constexpr int kBufWord3 = 0x00020000;           // raw buffer resource, dword 3 (gfx950)
+constexpr int kScDevice = 16;                   // cache policy sc1: device scope
+constexpr int kWaitVm0 = 0x0F70;                // s_waitcnt vmcnt(0), others untouched
+
+// Split of `iters` iterations into nwg ranges: q = iters / nwg each, the
+// first rem = iters % nwg ranges one more.  Neither query divides by more
+// than a 32-bit uniform value.
+struct SkSplit {
+    int q, rem;
+    __device__ SkSplit(int iters, int nwg) : q(iters / nwg), rem(iters - iters / nwg * nwg) {}
+    // first iteration of range r
+    __device__ int start(int r) const { return r * q + min(r, rem); }
+    // range that holds iteration i (q >= 1)
+    __device__ int owner(int i) const {
+        const int b = (q + 1) * rem;
+        return i < b ? i / (q + 1) : rem + (i - b) / q;
+    }
+};
+
+template <int NS, int TN, bool ACC>
+__global__ __launch_bounds__(512) void k_gemm_sk(
+    const int8_t *__restrict__ act, int mg, const float *__restrict__ sa_ptr, int sa_stride,
+    float sa_value, const int8_t *__restrict__ tiles, const float *__restrict__ wscales,
+    int M, int N, int n_tiles, int P, int n_mt, int iters, float *__restrict__ out,
+    int32_t *__restrict__ acc_out, int32_t *__restrict__ ws, int *__restrict__ cnt) {
+    // 8 waves, 4 along M x 2 along N; wave (wm, wn) = (wv / 2, wv % 2) owns
+    // rows 64*wm.. (TM 32-row blocks) and columns 32*TN*wn.. (TN blocks) of
+    // a 256 x BN tile.  With TN = 4, 128 accumulator registers per wave stay
+    // in VGPRs beside the fragments, two waves per SIMD.
+    constexpr int NW = 8, TM = 2, BN = 64 * TN;
+    constexpr int LA = 16 / NW, LB = 2 * BN / 32 / NW;  // fragment loads per wave per step
+    constexpr int SA = 16 * 1024, SB = BN / 32 * 2048;  // bytes of one A / B stage
+    static_assert(TN == 2 || TN == 4, "tile width");
+    constexpr int WAIT = (NS - 3) * (LA + LB);
+    constexpr int WAIT0 = WAIT + LA + LB;
+    extern __shared__ v4i s_buf[];
+    __shared__ int s_last;
+    // activation row and weight column scales of a segment's tile, double
+    // buffered by segment parity: a wave may fill the next segment's while
+    // another still reads this one's
+    __shared__ __attribute__((aligned(16))) float s_scale[2][2][256];
+
+    const int nwg = (int)gridDim.x;  // a multiple of 8
+    // range index, XCD-major: the ranges of one XCD are adjacent, so the
+    // contributors of a tile (and the M tiles sharing weights) share its L2
+    const int r = (int)(blockIdx.x % kXcds) * (nwg / kXcds) + (int)(blockIdx.x / kXcds);
+    const SkSplit split(iters, nwg);  // nwg <= iters (the launcher's choice)
+    const int it0 = split.start(r), it1 = split.start(r + 1);
+
+    const int t = threadIdx.x;
+    const int wv = __builtin_amdgcn_readfirstlane(t >> 6), l = t & 63;
+    const int wm = wv >> 1, wn = wv & 1;
+    const unsigned ldsA = __builtin_amdgcn_readfirstlane((unsigned)(size_t)s_buf);
+    const unsigned ldsB = ldsA + NS * SA;
+    const size_t a_pitch = (size_t)mg * 2 * 1024;   // bytes per K step
+    const size_t b_pitch = (size_t)n_tiles * 1024;  // bytes per K slab
+
+    // Loads of iteration i (clamped to the range's last: loads past the end
+    // re-read it into a stage no later step reads, so every wait count is
+    // constant).  Fragment f = wv + NW*j: row / weight-column group f/2, k
+    // half f%2 (layouts as in k_gemm_int8).  The per-lane parts of the
+    // addresses are fixed; next_desc() adds the iteration's.
+    // Fragment f = wv + NW*j has the same k half (wv & 1) for every j, so the
+    // per-lane part of every A / B address is one offset: A lane l of the
+    // 1 KiB fragment, B piece (2*(f%2) + l/32)*16 + l%16 of stored chunk
+    // 2*(f/2) + (l%32)/16 of the block.
+    const unsigned a_loff = (unsigned)(((wv & 1) * kWave + l) * 16);
+    const unsigned b_loff = (unsigned)(((2 * (wv & 1) + (l >> 5)) * 16 + (l & 15)) * 16);
+    const int b_lsub = (l & 31) >> 4;
+    struct Desc {
+        size_t a_off, b_off;  // bytes of the K step
+        int g0, T0;           // first row group, first 16-row weight tile
+        unsigned sa, sb;      // LDS stages
+    };
+    // Load cursor: the loads are issued for iterations it0, it0 + 1, ... in
+    // order, one iteration per call of next_desc(), so the tile coordinates
+    // are carried forward instead of divided out each step.
+    int lc_i = it0, lc_n = 0, lc_p, lc_mt, lc_nt;
+    {
+        const int tl = it0 / P;
+        lc_p = it0 - tl * P;
+        lc_nt = tl / n_mt;
+        lc_mt = tl - lc_nt * n_mt;
+    }
+    auto next_desc = [&]() __attribute__((always_inline)) {
+        Desc d;
+        d.a_off = (size_t)lc_p * a_pitch;
+        d.b_off = (size_t)lc_p * b_pitch;
+        d.g0 = lc_mt * 8;
+        d.T0 = lc_nt * (BN / 16);
+        const int stg = lc_n % NS;
+        d.sa = ldsA + (unsigned)(stg * SA);
+        d.sb = ldsB + (unsigned)(stg * SB);
+        ++lc_n;
+        if (lc_i + 1 < it1) {  // else stay clamped to the range's last
+            ++lc_i;
+            if (++lc_p == P) {
+                lc_p = 0;
+                if (++lc_mt == n_mt) {
+                    lc_mt = 0;
+                    ++lc_nt;
+                }
+            }
+        }
+        return d;
+    };
+    auto dma = [&](const Desc &d, int j, bool b) __attribute__((always_inline)) {
+        const unsigned f = (unsigned)(wv + NW * j);
+        if (!b) {
+            const int g = min(d.g0 + (wv >> 1) + (NW / 2) * j, mg - 1);
+            dma16(act + d.a_off + (size_t)g * 2048 + a_loff, d.sa + f * 1024);
+        } else {
+            const int T = min(d.T0 + 2 * (wv >> 1) + NW * j + b_lsub, n_tiles - 1);
+            dma16(tiles + d.b_off + (size_t)T * 1024 + b_loff, d.sb + f * 1024);
+        }
+    };
+
+    v16i acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = v16i{};
+    // Fragments of one k half: the MFMAs of half h of a step read fa[h] /
+    // fb[h] while the other half's registers are refilled (half 1 of the
+    // same iteration, or half 0 of the next).
+    v4i fa[2][TM], fb[2][TN];  // [k half][tile]
+    auto rd_a = [&](int i, int h, int q) __attribute__((always_inline)) {
+        fa[h][q] = s_buf[(size_t)((unsigned)(i - it0) % NS) * (SA / 16) + (2 * (wm * TM + q) + h) * kWave + l];
+    };
+    auto rd_b = [&](int i, int h, int q) __attribute__((always_inline)) {
+        fb[h][q] = s_buf[(size_t)(NS * SA + ((unsigned)(i - it0) % NS) * SB) / 16 + (2 * (wn * TN + q) + h) * kWave + l];
+    };
+
+    // f32 epilogue (int8.rs:93).  Register group q of accumulator (i, j)
+    // holds 4 values: element e4 is tile row 32*(wm*TM + i) + 8*q +
+    // 4*(l/32) + e4 and column 32*(wn*TN + j) + l%32.  The scales come from
+    // LDS (s_scale), filled by load_scales when the segment starts: LDS
+    // reads do not wait for the output stores, where global loads issued
+    // after them would (one in-order counter covers loads and stores).
+    const unsigned lds_scale = __builtin_amdgcn_readfirstlane((unsigned)(size_t)&s_scale[0][0][0]);
+    auto load_scales = [&](int tl, int buf) __attribute__((always_inline)) {
+        const int m0 = (tl % n_mt) * 256, n0 = (tl / n_mt) * BN;
+        // waves 0-3: the 256 row scales, waves 4..: the BN column scales
+        const unsigned base = lds_scale + (unsigned)(buf * 2048 + wv * 256);
+        if (wv < 4) {
+            if (sa_ptr) dma4(sa_ptr + (size_t)min(m0 + 64 * wv + l, M - 1) * sa_stride, base);
+        } else if (wv < 4 + BN / 64) {
+            dma4(wscales + min(n0 + 64 * (wv - 4) + l, N - 1), base);
+        }
+    };
+    // Output stores go through buffer resources: the row step of an
+    // element (e4 * N * 4 bytes) is a uniform offset and the column block an
+    // immediate one, so a store needs no per-element address arithmetic, and
+    // rows past M fall outside the resource, where stores are dropped.
+    const int row_bytes = N * 4;
+    const __amdgpu_buffer_rsrc_t out_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        out, 0, (int)min((long long)M * N * 4, 0x7fffffffLL), kBufWord3);
+    const __amdgpu_buffer_rsrc_t acc_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        acc_out, 0, ACC ? (int)min((long long)M * N * 4, 0x7fffffffLL) : 0, kBufWord3);
+    auto col_scales = [&](int buf, float (&sw)[TN]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) sw[j] = s_scale[buf][1][32 * (wn * TN + j) + (l & 31)];
+    };
+    auto put4 = [&](int tl, int buf, const float (&sw)[TN], int i, int j, int q, const v4i &v)
+                    __attribute__((always_inline)) {
+        const int m0 = (tl % n_mt) * 256, n0 = (tl / n_mt) * BN;
+        const int n = n0 + 32 * (wn * TN + j) + (l & 31);
+        const int rt = 32 * (wm * TM + i) + 8 * q + 4 * (l >> 5);  // tile row of e4 = 0
+        typedef float v4f __attribute__((ext_vector_type(4)));
+        const v4f sa = sa_ptr ? *reinterpret_cast<const v4f *>(&s_scale[buf][0][rt])
+                              : v4f{sa_value, sa_value, sa_value, sa_value};
+        if (n >= N) return;
+        const int voff = (m0 + rt) * row_bytes + n * 4;
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+            float o = (float)v[e4] * sa[e4];
+            o = o * sw[j];
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, o), out_rsrc, voff,
+                                                  e4 * row_bytes, 0);
+            if constexpr (ACC)
+                __builtin_amdgcn_raw_buffer_store_b32(v[e4], acc_rsrc, voff, e4 * row_bytes, 0);
+        }
+    };
+    auto epilogue = [&](int tl, int buf) __attribute__((always_inline)) {
+        float sw[TN];
+        col_scales(buf, sw);
+        static_for<TM * TN * 4>([&](auto gg) {
+            constexpr int a = decltype(gg)::value / 4, q = decltype(gg)::value % 4;
+            put4(tl, buf, sw, a / TN, a % TN, q,
+                 v4i{acc[a / TN][a % TN][4 * q], acc[a / TN][a % TN][4 * q + 1],
+                     acc[a / TN][a % TN][4 * q + 2], acc[a / TN][a % TN][4 * q + 3]});
+        });
+    };
+    // Partial tile slot of range c in tile tl: 0 when the range starts in
+    // the tile (its first segment), else 1 (its last segment).  Slot layout:
+    // [wave][accumulator a][register group q][lane] x 16 bytes.  Partials
+    // are written and read with device-scope (sc1) buffer accesses, which
+    // reach the point of coherence of all XCDs, so neither side needs a
+    // cache-wide fence.
+    const __amdgpu_buffer_rsrc_t ws_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        ws, 0, (int)min((long long)nwg * 2 * kSkTileInts * 4, 0x7fffffffLL), kBufWord3);
+    auto slot_of = [&](int c, int tl) {
+        return split.start(c) >= tl * P ? 0 : 1;
+    };
+    auto slot_off = [&](int c, int slot) {  // byte offset of this lane's first vector
+        return (int)(((size_t)(2 * c + slot) * kSkTileInts +
+                      ((size_t)wv * (TM * TN * 4 * kWave) + l) * 4) * 4);
+    };
+    // End of a segment [k0, k1) of tile tl.  A split tile: every contributor
+    // stores its partial and counts itself; the one that counts last sums
+    // all slots (int32) and applies the epilogue.
+    auto finish = [&](int tl, int k0, int k1, int buf) __attribute__((always_inline)) {
+        // The scale loads, issued before the segment's first step, are
+        // complete and visible after the second step's wait and barrier; a
+        // one-step segment waits here.
+        if (k1 - k0 < 2) wait_barrier<0>();
+        if (k0 == 0 && k1 == P) {
+            epilogue(tl, buf);
+            return;
+        }
+        const int c0 = split.owner(tl * P), c1 = split.owner(tl * P + P - 1);
+        const int mine = slot_off(r, slot_of(r, tl));
+        static_for<TM * TN>([&](auto aa) {
+            constexpr int a = decltype(aa)::value;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    v4i{acc[a / TN][a % TN][4 * q], acc[a / TN][a % TN][4 * q + 1],
+                        acc[a / TN][a % TN][4 * q + 2], acc[a / TN][a % TN][4 * q + 3]},
+                    ws_rsrc, mine + (a * 4 + q) * kWave * 16, 0, kScDevice);
+        });
+        __builtin_amdgcn_s_waitcnt(kWaitVm0);  // the partial has reached the device
+        __syncthreads();
+        if (t == 0)
+            s_last = __hip_atomic_fetch_add(&cnt[tl], 1, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT) == c1 - c0;
+        __syncthreads();
+        if (!s_last) return;
+        // Sum of all slots, one accumulator (4 vectors) per pass; the next
+        // pass's loads are issued before this pass's stores (they would
+        // otherwise wait for the stores), up to four contributors at a time.
+        float sw[TN];
+        col_scales(buf, sw);
+        auto load_pass = [&](int a, int cb, v4i (&u)[4][4]) __attribute__((always_inline)) {
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) {
+                const int c = min(cb + cc, c1);
+                const int off = slot_off(c, slot_of(c, tl)) + a * 4 * kWave * 16;
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    u[cc][v] = __builtin_amdgcn_raw_buffer_load_b128(ws_rsrc, off + v * kWave * 16, 0,
+                                                                   kScDevice);
+            }
+        };
+        v4i u[4][4];
+        load_pass(0, c0, u);
+        static_for<TM * TN>([&](auto aa) {
+            constexpr int a = decltype(aa)::value;
+            v4i sum[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) sum[v] = v4i{0, 0, 0, 0};
+            for (int cb = c0;;) {
+#pragma unroll
+                for (int cc = 0; cc < 4; ++cc)
+                    if (cb + cc <= c1) {
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) sum[v] += u[cc][v];
+                    }
+                cb += 4;
+                if (cb > c1) break;
+                load_pass(a, cb, u);  // more than four contributors
+            }
+            if constexpr (a + 1 < TM * TN) load_pass(a + 1, c0, u);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) put4(tl, buf, sw, a / TN, a % TN, v, sum[v]);
+        });
+        if (t == 0)  // ready for the next call on this stream
+            __hip_atomic_store(&cnt[tl], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+
+    // prologue: the first segment's scales, iterations it0 .. it0 + NS - 2
+    load_scales(it0 / P, 0);
+#pragma unroll
+    for (int q = 0; q < NS - 1; ++q) {
+        const Desc d = next_desc();  // iteration it0 + q
+#pragma unroll
+        for (int j = 0; j < LA; ++j) dma(d, j, false);
+#pragma unroll
+        for (int j = 0; j < LB; ++j) dma(d, j, true);
+    }
+    wait_barrier<WAIT0>();
+    using RD = std::true_type;
+    using NORD = std::false_type;
+    // half 0 of iteration i (in LDS and visible)
+    auto read_h0 = [&](int i) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < TM; ++q) rd_a(i, 0, q);
+#pragma unroll
+        for (int q = 0; q < TN; ++q) rd_b(i, 0, q);
+    };
+    read_h0(it0);
+    // Step i: wait for iteration i+1's loads and barrier (all waves are
+    // past step i-1, whose stage is refilled next), then the 16 MFMAs of
+    // step i with the 4 loads of iteration i+NS-1 placed between them, and
+    // the fragment reads: half 1 of iteration i during half 0's MFMAs, and,
+    // unless it is the segment's last step, half 0 of iteration i+1 during
+    // half 1's.  Reads go in order of first use (A0, B0..B3, A1).
+    auto step = [&](int i, auto rd) __attribute__((always_inline)) {
+        const Desc d = next_desc();  // iteration i + NS - 1
+        wait_barrier<WAIT>();
+        static_for<2 * TM * TN>([&](auto kk) {
+            constexpr int k = decltype(kk)::value;
+            constexpr int h = k / (TM * TN), ii = (k / TN) % TM, jj = k % TN;
+            acc[ii][jj] =
+                __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[h][ii], fb[h][jj], acc[ii][jj], 0, 0, 0);
+            // load n goes with MFMA n * MF / (LA + LB)
+            constexpr int MF = 2 * TM * TN, ND = LA + LB;
+            constexpr int n = (k * ND + MF - 1) / MF;  // first load at or after MFMA k
+            if constexpr (n < ND && n * MF / ND == k) {
+                if constexpr (n < LA) dma(d, n, false);
+                else dma(d, n - LA, true);
+            }
+            // fragment read slot of the half: from its second MFMA when the
+            // half has more MFMAs than reads
+            constexpr int rr = k % (TM * TN) - (TM * TN > TM + TN ? 1 : 0);
+            if constexpr (rr >= 0 && rr < TM + TN && (h == 0 || decltype(rd)::value)) {
+                const int ir = h == 0 ? i : i + 1;
+                if constexpr (rr == 0) rd_a(ir, 1 - h, 0);
+                else if constexpr (rr <= TN) rd_b(ir, 1 - h, rr - 1);
+                else rd_a(ir, 1 - h, rr - TN);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    };
+    // Segments: the steps of one tile within the range, then the segment's
+    // end.  The last step reads no fragments ahead, so no fragment is held
+    // in registers across the end; the next segment's first ones are read
+    // after it (its stage is complete since the last step's wait, and
+    // refilled two steps later).
+    for (int i = it0, buf = 0; i < it1; buf ^= 1) {
+        const int tl = i / P;
+        const int s1 = min(it1, (tl + 1) * P);
+        int j = i;
+        for (; j + 1 < s1; ++j) step(j, RD{});
+        step(j, NORD{});
+        finish(tl, i - tl * P, s1 - tl * P, buf);
+        // nothing the compiler tracks may be outstanding where the next
+        // segment's loop starts, or it waits for it inside the loop
+        __builtin_amdgcn_s_waitcnt(kWaitVm0);
+#pragma unroll
+        for (int a = 0; a < TM; ++a)
+#pragma unroll
+            for (int b = 0; b < TN; ++b) acc[a][b] = v16i{};
+        i = s1;
+        if (i < it1) {
+            load_scales(i / P, buf ^ 1);
+            read_h0(i);
+        }
+    }
+    // no load may still be writing LDS when the workgroup ends
+    asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+}
+
 template <int BM, int BN, int WM, int WN, int NSA, int NSB>
 mri_status launch(const int8_t *act_packed, size_t m, const float *sa_ptr, int sa_stride,
                   float sa_value, const QMatrixDev &w, float *out, int32_t *acc_out,
@@ -265,16 +670,96 @@ mri_status launch(const int8_t *act_packed, size_t m, const float *sa_ptr, int s
     return MRI_OK;
 }
 
+// Stream-K geometry of an m-row product: workgroups (one per CU, at most
+// one per iteration, a multiple of 8) and iterations (tiles x K steps).
+struct SkShape {
+    int nwg = 0, iters = 0, n_mt = 0, n_tt = 0;
+};
+SkShape sk_shape(size_t m, const QMatrixDev &w, int bn) {
+    static int cus[64] = {};
+    int dev = 0;
+    SkShape sh;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return sh;
+    if (!cus[dev] &&
+        hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return sh;
+    sh.n_mt = (int)((m + 255) / 256);
+    sh.n_tt = sh.n_mt * (int)((w.n_tiles + bn / 16 - 1) / (bn / 16));
+    const long long iters = (long long)sh.n_tt * (long long)(w.kp / kChunkK);
+    // buffer offsets of the epilogue are 32-bit: the output must stay below 2 GiB
+    if (iters > (1LL << 30) || sh.n_tt > kSkMaxTiles ||
+        (long long)m * (long long)w.n_out * 4 > 0x7fffffffLL)
+        return SkShape{};
+    sh.iters = (int)iters;
+    sh.nwg = (int)(std::min<long long>(cus[dev], iters) / kXcds * kXcds);
+    return sh;
+}
+
+template <int TN>
+mri_status launch_sk(const int8_t *act_packed, size_t m, const float *sa_ptr, int sa_stride,
+                     float sa_value, const QMatrixDev &w, float *out, int32_t *acc_out,
+                     void *ws, const SkShape &sh, hipStream_t s) {
+    constexpr size_t lds = (size_t)kSkNs * (16 * 1024 + 2 * TN * 2048);
+    static bool attr_set = false;
+    if (!attr_set) {
+        MRI_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemm_sk<kSkNs, TN, false>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        MRI_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemm_sk<kSkNs, TN, true>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        attr_set = true;
+    }
+    auto *cnt = static_cast<int *>(ws);
+    auto *part = reinterpret_cast<int32_t *>(cnt + kSkMaxTiles);
+    auto *kern = acc_out ? &k_gemm_sk<kSkNs, TN, true> : &k_gemm_sk<kSkNs, TN, false>;
+    hipLaunchKernelGGL(kern, dim3((unsigned)sh.nwg), dim3(512), lds, s, act_packed,
+                       (int)gemm_row_groups(m), sa_ptr, sa_stride, sa_value, w.tiles, w.scales,
+                       (int)m, (int)w.n_out, (int)w.n_tiles, (int)(w.kp / kChunkK), sh.n_mt,
+                       sh.iters, out, acc_out, part, cnt);
+    MRI_LAUNCHED("k_gemm_sk");
+    return MRI_OK;
+}
+
 }  // namespace
 
+size_t gemm_ws_bytes(size_t m, const QMatrixDev &w) {
+    // the narrower tiles have the more tiles; both widths have the same grid
+    const SkShape sh = sk_shape(m, w, 128);
+    if (sh.nwg == 0) return 0;
+    // [tile counters, fixed place and size][partial tiles: 2 slots per workgroup]
+    return (size_t)kSkMaxTiles * sizeof(int) + (size_t)sh.nwg * 2 * kSkTileInts * sizeof(int32_t);
+}
+
 // act_packed: activations in the GEMM fragment layout (gemm_pack_bytes).
+// ws: gemm_ws_bytes(m, w) bytes; its first kSkMaxTiles ints (the tile
+// counters, at the same place for every shape) were zeroed when it was
+// allocated, and every call leaves them zero again.
 mri_status launch_gemm_int8(const int8_t *act_packed, size_t m, const float *sa_ptr,
                             int sa_stride, float sa_value, const QMatrixDev &w,
-                            float *out, int32_t *acc_out, hipStream_t s) {
+                            float *out, int32_t *acc_out, void *ws, hipStream_t s) {
     if (w.n_tiles == 0 || m == 0) return MRI_OK;
-    // 256 x 128 tiles when they still give at least half as many workgroups
-    // as CUs, else 128 x 128 (measured on MI355X at K = 4096).
+    // Whole-tile kernel: 256 x 128 tiles when they still give at least half
+    // as many workgroups as CUs, else 128 x 128.
     const size_t big = ((m + 255) / 256) * ((w.n_tiles + 7) / 8);
+    const size_t tiles_dp = big >= 128 ? big : ((m + 127) / 128) * ((w.n_tiles + 7) / 8);
+    // Stream-K pays for split tiles (partials through memory) and for rows
+    // padded to 256; whole tiles pay for idle CUs.  Measured on MI355X
+    // (K = 4096 and 11008, random int8 operands): whole tiles win when they
+    // fill 60-100% of one wave, or a third of it at M = 128, where half of
+    // stream-K's rows are padding; stream-K wins otherwise, with 256 x 256
+    // tiles only when they come in whole waves (no split tile).
+    const SkShape sh4 = sk_shape(m, w, 256), sh2 = sk_shape(m, w, 128);
+    if (ws && sh2.nwg > 0) {
+        const double fill = (double)tiles_dp / sh2.nwg;
+        const double row_eff = (double)m / ((double)sh2.n_mt * 256);
+        const bool dp = fill <= 1.0 && (fill >= 0.6 || fill >= 0.65 * row_eff);
+        if (!dp) {
+            if (sh4.nwg > 0 && sh4.n_tt >= sh4.nwg && sh4.n_tt % sh4.nwg == 0)
+                return launch_sk<4>(act_packed, m, sa_ptr, sa_stride, sa_value, w, out, acc_out,
+                                    ws, sh4, s);
+            return launch_sk<2>(act_packed, m, sa_ptr, sa_stride, sa_value, w, out, acc_out, ws,
+                                sh2, s);
+        }
+    }
     mri_status st =
         big >= 128 ? launch<256, 128, 4, 2, 4, 8>(act_packed, m, sa_ptr, sa_stride, sa_value, w,
                                                   out, acc_out, s)

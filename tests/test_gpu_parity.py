@@ -138,7 +138,8 @@ def test_matmul_int8_bit_exact(m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k", [(512, 11008, 4096), (300, 200, 1024), (2048, 512, 4096),
-                                   (64, 4096, 11008), (128, 4096, 4096)])
+                                   (64, 4096, 11008), (128, 4096, 4096), (512, 4096, 11008),
+                                   (2048, 8192, 4096)])
 def test_matmul_int8_prefill_closed_form(m, n, k):
     """Prefill-sized matmul_int8 (int8.rs:61-98) at full shapes: the int32
     accumulators against an exact float64 matmul (|sum| <= 127^2 * K < 2^53)
@@ -158,6 +159,34 @@ def test_matmul_int8_prefill_closed_form(m, n, k):
     mri().matmul_int8(dev(aq), sa, w, m, out, acc)
     assert np.array_equal(host(acc), acc0)
     assert_bits_equal(host(out), out0, "matmul_int8 prefill out")
+
+
+def test_matmul_int8_prefill_back_to_back():
+    """Consecutive prefill products of different shapes on one stream, with
+    and without the int32 output: every call starts from a clean state (the
+    split-tile bookkeeping is left as it was found)."""
+    t = torch()
+    cases = []
+    for m, n, k in [(300, 200, 1024), (2048, 512, 4096), (300, 200, 1024), (1024, 4096, 4096),
+                    (2048, 512, 4096)]:
+        rng = np.random.default_rng(m * 5 + n + k)
+        wq = rng.integers(-127, 128, (n, k)).astype(np.int8)
+        ws = rng.uniform(1e-4, 1e-3, n).astype(F32)
+        aq = rng.integers(-127, 128, (m, k)).astype(np.int8)
+        acc0 = (aq.astype(np.float64) @ wq.astype(np.float64).T).astype(np.int32)
+        cases.append((m, n, k, mri().QMatrix.from_host(wq, ws), dev(aq),
+                      acc0, (acc0.astype(F32) * F32(0.02)) * ws[None, :]))
+    outs = []
+    for i, (m, n, k, w, a, _, _) in enumerate(cases):
+        say(f"matmul_int8 back-to-back #{i} m={m} n={n} k={k}")
+        out = empty((m, n), t.float32)
+        acc = empty((m, n), t.int32) if i % 2 == 0 else None
+        mri().matmul_int8(a, F32(0.02), w, m, out, acc)
+        outs.append((out, acc))
+    for (m, n, k, _, _, acc0, out0), (out, acc) in zip(cases, outs):
+        if acc is not None:
+            assert np.array_equal(host(acc), acc0)
+        assert_bits_equal(host(out), out0, f"matmul_int8 back-to-back {m}x{n}x{k}")
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 64, 4096), (7, 40, 256), (48, 32, 128), (260, 96, 512)])
