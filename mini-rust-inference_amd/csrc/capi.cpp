@@ -48,7 +48,7 @@ static std::string fmt(const char *f, ...) {
 static std::mutex g_dev_mu;
 static std::map<int, int> g_dev_ok;  // device -> 1 gfx950, 0 other
 
-static mri_status current_device(int *dev) {
+mri_status current_device(int *dev) {
     MRI_HIP(hipGetDevice(dev));
     std::lock_guard<std::mutex> lk(g_dev_mu);
     auto it = g_dev_ok.find(*dev);

@@ -1,0 +1,378 @@
+// model.cpp — LlamaModelInt8 on the GPU (include/mri_llama.h).
+//
+// Host-side orchestration of one forward pass: every step is a kernel (or a
+// quantized projection entry point) enqueued on the caller's stream over
+// activation buffers that the model handle owns, sized for max_seq rows.
+// Nothing is copied back to the host except the generated token ids at the
+// end of mri_llama_generate_greedy.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "common.hpp"
+#include "mri_llama.h"
+
+struct mri_kv_cache {
+    size_t n_layers = 0, max_seq = 0, kvd = 0;
+    float *k = nullptr, *v = nullptr;  // [n_layers][max_seq][kvd]
+};
+
+namespace {
+
+struct Layer {
+    float *attn_norm = nullptr, *ffn_norm = nullptr;
+    mri_weight_ref w[7] = {};
+    bool set = false;
+};
+
+}  // namespace
+
+struct mri_llama {
+    mri_llama_config cfg{};
+    size_t hd = 0, qd = 0, kvd = 0;
+    float *embd = nullptr, *out_norm = nullptr;
+    mri_weight_ref output{};
+    std::vector<Layer> layers;
+    float *cos_t = nullptr, *sin_t = nullptr;  // [max_seq][hd/2]
+    // activations for up to max_seq rows
+    float *x = nullptr, *normed = nullptr, *tmp = nullptr, *q = nullptr, *k = nullptr,
+          *v = nullptr, *attn = nullptr, *gate = nullptr, *up = nullptr;
+    uint32_t *tok = nullptr;      // prompt ids [max_seq]
+    uint32_t *gen = nullptr;      // generated ids [max_seq + 1]
+    float *logits_buf = nullptr;  // prefill logits for generation, grown on demand
+    size_t logits_rows = 0;
+    std::vector<void *> allocs;
+};
+
+namespace mri {
+mri_status current_device(int *dev);
+}
+
+namespace {
+
+using namespace mri;
+
+std::string fmt_err(const char *f, size_t a, size_t b = 0, size_t c = 0) {
+    char buf[256];
+    snprintf(buf, sizeof buf, f, a, b, c);
+    return buf;
+}
+
+mri_status dalloc(mri_llama *m, size_t bytes, void **p) {
+    MRI_HIP(hipMalloc(p, bytes ? bytes : 4));
+    m->allocs.push_back(*p);
+    return MRI_OK;
+}
+
+template <typename T>
+mri_status dalloc_t(mri_llama *m, size_t count, T **p) {
+    void *v = nullptr;
+    mri_status st = dalloc(m, count * sizeof(T), &v);
+    *p = static_cast<T *>(v);
+    return st;
+}
+
+// Shape and handle checks of one projection weight.
+mri_status check_weight(const mri_weight_ref &w, size_t n_out, size_t k_in, const char *role) {
+    if (!w.ptr) return set_error(MRI_ERR_INVALID_ARGUMENT, std::string(role) + ": null weight");
+    if (w.n_out != n_out || w.k_in != k_in)
+        return set_error(MRI_ERR_INVALID_SHAPE,
+                         std::string(role) + fmt_err(": weight is [%zu, %zu], expected [%zu, ",
+                                                     w.n_out, w.k_in, n_out) +
+                             std::to_string(k_in) + "]");
+    switch (w.format) {
+    case MRI_WEIGHT_INT8: {
+        auto *h = static_cast<const mri_qmatrix *>(w.ptr);
+        if (mri_qmatrix_n_out(h) != n_out || mri_qmatrix_k_in(h) != k_in)
+            return set_error(MRI_ERR_INVALID_SHAPE, std::string(role) + ": handle shape differs");
+        return MRI_OK;
+    }
+    case MRI_WEIGHT_Q8_0: {
+        auto *h = static_cast<const mri_q8_0_matrix *>(w.ptr);
+        if (mri_q8_0_matrix_n_out(h) != n_out || mri_q8_0_matrix_k_in(h) != k_in)
+            return set_error(MRI_ERR_INVALID_SHAPE, std::string(role) + ": handle shape differs");
+        return MRI_OK;
+    }
+    case MRI_WEIGHT_Q4_0:
+        if (k_in % 32)
+            return set_error(MRI_ERR_INVALID_SHAPE,
+                             std::string(role) + ": Q4_0 k_in must be a multiple of 32");
+        return MRI_OK;
+    default:
+        return set_error(MRI_ERR_INVALID_ARGUMENT, std::string(role) + ": unknown weight format");
+    }
+}
+
+// out[rows, n_out] = in[rows, k_in] projected by w (forward_int8.rs:72-74).
+mri_status proj(const mri_weight_ref &w, const float *in, size_t rows, float *out,
+                hipStream_t s) {
+    const size_t dims[2] = {rows, w.k_in};
+    switch (w.format) {
+    case MRI_WEIGHT_INT8:
+        return mri_matmul_int8_from_f32(in, dims, 2, static_cast<const mri_qmatrix *>(w.ptr), out,
+                                        nullptr, nullptr, nullptr, s);
+    case MRI_WEIGHT_Q8_0:
+        return mri_matmul_q8_0_direct(in, dims, 2, static_cast<const mri_q8_0_matrix *>(w.ptr),
+                                      out, nullptr, nullptr, s);
+    default:
+        return mri_matmul_q4_0_dequant(in, dims, 2, static_cast<const uint8_t *>(w.ptr),
+                                       w.n_out * (w.k_in / 32) * 18, w.n_out, w.k_in, out, s);
+    }
+}
+
+#define TRY(call)                              \
+    do {                                       \
+        const mri_status _st = (call);         \
+        if (_st != MRI_OK) return _st;         \
+    } while (0)
+
+// TransformerBlockInt8::forward_cached (forward_int8.rs:207-216): attention
+// sublayer (:291-323) and FFN sublayer (:350-357) over the rows in m->x.
+mri_status block(mri_llama *m, size_t li, size_t rows, size_t start, mri_kv_cache *c,
+                 hipStream_t s) {
+    const mri_llama_config &g = m->cfg;
+    const Layer &L = m->layers[li];
+    float *kc = c->k + li * c->max_seq * c->kvd, *vc = c->v + li * c->max_seq * c->kvd;
+    TRY(launch_rmsnorm(m->x, L.attn_norm, rows, g.dim, g.eps, m->normed, s));
+    TRY(proj(L.w[0], m->normed, rows, m->q, s));
+    TRY(proj(L.w[1], m->normed, rows, m->k, s));
+    TRY(proj(L.w[2], m->normed, rows, m->v, s));
+    TRY(launch_rope_qkv(m->q, m->k, m->v, rows, m->qd, m->kvd, m->hd, m->cos_t, m->sin_t, start,
+                        kc, vc, s));
+    TRY(launch_attention(m->q, rows, kc, vc, g.n_heads, g.n_kv_heads, m->hd, start, m->attn, s));
+    TRY(proj(L.w[3], m->attn, rows, m->tmp, s));
+    TRY(launch_add(m->x, m->tmp, rows * g.dim, m->x, s));
+    TRY(launch_rmsnorm(m->x, L.ffn_norm, rows, g.dim, g.eps, m->normed, s));
+    TRY(proj(L.w[4], m->normed, rows, m->gate, s));
+    TRY(proj(L.w[5], m->normed, rows, m->up, s));
+    TRY(launch_swiglu(m->gate, m->up, rows * g.ffn_dim, m->gate, s));
+    TRY(proj(L.w[6], m->gate, rows, m->tmp, s));
+    return launch_add(m->x, m->tmp, rows * g.dim, m->x, s);
+}
+
+// embed -> blocks -> rmsnorm -> output projection for `rows` token ids
+// already on the device.
+mri_status run_rows(mri_llama *m, const uint32_t *tok_dev, size_t rows, size_t start,
+                    mri_kv_cache *c, float *logits, hipStream_t s) {
+    const mri_llama_config &g = m->cfg;
+    TRY(launch_embed(m->embd, tok_dev, rows, g.dim, m->x, s));
+    for (size_t li = 0; li < g.n_layers; ++li) TRY(block(m, li, rows, start, c, s));
+    TRY(launch_rmsnorm(m->x, m->out_norm, rows, g.dim, g.eps, m->normed, s));
+    return proj(m->output, m->normed, rows, logits, s);
+}
+
+mri_status check_run(mri_llama *m, size_t n, size_t start, mri_kv_cache *c) {
+    if (!m || !c) return set_error(MRI_ERR_INVALID_ARGUMENT, "null model or cache");
+    for (size_t li = 0; li < m->cfg.n_layers; ++li)
+        if (!m->layers[li].set)
+            return set_error(MRI_ERR_INVALID_ARGUMENT, fmt_err("layer %zu is not set", li));
+    if (c->n_layers != m->cfg.n_layers || c->kvd != m->kvd)
+        return set_error(MRI_ERR_SHAPE_MISMATCH, "KV cache shape does not match the model");
+    if (n == 0) return set_error(MRI_ERR_INVALID_SHAPE, "forward: token list must not be empty");
+    const size_t cap = std::min(c->max_seq, m->cfg.max_seq);
+    if (start + n > cap)
+        return set_error(MRI_ERR_INVALID_SHAPE,
+                         fmt_err("positions %zu..%zu exceed the cache / RoPE length %zu", start,
+                                 start + n - 1, cap));
+    return MRI_OK;
+}
+
+mri_status check_tokens(const mri_llama *m, const uint32_t *tokens, size_t n) {
+    if (!tokens) return set_error(MRI_ERR_INVALID_ARGUMENT, "null token list");
+    for (size_t i = 0; i < n; ++i)
+        if (tokens[i] >= m->cfg.vocab)
+            return set_error(MRI_ERR_INVALID_SHAPE,
+                             fmt_err("token id %zu >= vocab_size %zu", tokens[i], m->cfg.vocab));
+    return MRI_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+mri_status mri_llama_create(const mri_llama_config *cfg, const float *token_embd,
+                            const float *output_norm, mri_weight_ref output, mri_llama **out) {
+    if (!cfg || !out || !token_embd || !output_norm)
+        return set_error(MRI_ERR_INVALID_ARGUMENT, "null argument");
+    *out = nullptr;
+    const mri_llama_config g = *cfg;
+    if (!g.dim || !g.n_heads || !g.n_kv_heads || !g.vocab || !g.max_seq || !g.ffn_dim)
+        return set_error(MRI_ERR_INVALID_SHAPE, "llama: zero dimension");
+    if (g.dim % g.n_heads || g.n_heads % g.n_kv_heads || (g.dim / g.n_heads) % 2)
+        return set_error(MRI_ERR_INVALID_SHAPE,
+                         "llama: dim % n_heads, n_heads % n_kv_heads and head_dim % 2 must be 0");
+    const size_t hd = g.dim / g.n_heads;
+    if (!attention_supported(hd))
+        return set_error(MRI_ERR_UNSUPPORTED, "llama: head_dim must be 64 or 128");
+    int dev;
+    mri_status st = current_device(&dev);
+    if (st) return st;
+    TRY(check_weight(output, g.vocab, g.dim, "output"));
+    auto *m = new mri_llama();
+    m->cfg = g;
+    m->hd = hd;
+    m->qd = g.n_heads * hd;
+    m->kvd = g.n_kv_heads * hd;
+    m->output = output;
+    m->layers.resize(g.n_layers);
+    auto fail = [&](mri_status e) {
+        mri_llama_destroy(m);
+        return e;
+    };
+    const size_t R = g.max_seq;
+    if ((st = dalloc_t(m, g.vocab * g.dim, &m->embd)) || (st = dalloc_t(m, g.dim, &m->out_norm)) ||
+        (st = dalloc_t(m, R * hd / 2, &m->cos_t)) || (st = dalloc_t(m, R * hd / 2, &m->sin_t)) ||
+        (st = dalloc_t(m, R * g.dim, &m->x)) || (st = dalloc_t(m, R * g.dim, &m->normed)) ||
+        (st = dalloc_t(m, R * g.dim, &m->tmp)) || (st = dalloc_t(m, R * m->qd, &m->q)) ||
+        (st = dalloc_t(m, R * m->kvd, &m->k)) || (st = dalloc_t(m, R * m->kvd, &m->v)) ||
+        (st = dalloc_t(m, R * m->qd, &m->attn)) || (st = dalloc_t(m, R * g.ffn_dim, &m->gate)) ||
+        (st = dalloc_t(m, R * g.ffn_dim, &m->up)) || (st = dalloc_t(m, R, &m->tok)) ||
+        (st = dalloc_t(m, R + 1, &m->gen)))
+        return fail(st);
+    // RopeTable::new (ops/rope.rs): theta_i = 1 / base^(2i / head_dim) and
+    // angle = pos * theta_i in f32, with the C library's powf / cosf / sinf.
+    const size_t half = hd / 2;
+    std::vector<float> ct(R * half), stb(R * half);
+    for (size_t pos = 0; pos < R; ++pos)
+        for (size_t i = 0; i < half; ++i) {
+            const float e = (2.0f * (float)i) / (float)hd;
+            const float theta = 1.0f / powf(g.rope_base, e);
+            const float angle = (float)pos * theta;
+            ct[pos * half + i] = cosf(angle);
+            stb[pos * half + i] = sinf(angle);
+        }
+    hipError_t e;
+    if ((e = hipMemcpy(m->cos_t, ct.data(), ct.size() * 4, hipMemcpyHostToDevice)) ||
+        (e = hipMemcpy(m->sin_t, stb.data(), stb.size() * 4, hipMemcpyHostToDevice)) ||
+        (e = hipMemcpy(m->embd, token_embd, g.vocab * g.dim * 4, hipMemcpyHostToDevice)) ||
+        (e = hipMemcpy(m->out_norm, output_norm, g.dim * 4, hipMemcpyHostToDevice)))
+        return fail(hip_error(e, "llama_create upload"));
+    *out = m;
+    return MRI_OK;
+}
+
+mri_status mri_llama_set_layer(mri_llama *m, size_t li, const float *attn_norm,
+                               const float *ffn_norm, const mri_weight_ref w[7]) {
+    if (!m || !attn_norm || !ffn_norm || !w)
+        return set_error(MRI_ERR_INVALID_ARGUMENT, "null argument");
+    if (li >= m->cfg.n_layers)
+        return set_error(MRI_ERR_INVALID_ARGUMENT,
+                         fmt_err("layer %zu of %zu", li, m->cfg.n_layers));
+    const mri_llama_config &g = m->cfg;
+    static const char *kRole[7] = {"wq", "wk", "wv", "wo", "wgate", "wup", "wdown"};
+    const size_t shp[7][2] = {{m->qd, g.dim},      {m->kvd, g.dim},     {m->kvd, g.dim},
+                              {g.dim, m->qd},      {g.ffn_dim, g.dim},  {g.ffn_dim, g.dim},
+                              {g.dim, g.ffn_dim}};
+    for (int i = 0; i < 7; ++i) TRY(check_weight(w[i], shp[i][0], shp[i][1], kRole[i]));
+    Layer &L = m->layers[li];
+    if (!L.attn_norm) {
+        TRY(dalloc_t(m, g.dim, &L.attn_norm));
+        TRY(dalloc_t(m, g.dim, &L.ffn_norm));
+    }
+    MRI_HIP(hipMemcpy(L.attn_norm, attn_norm, g.dim * 4, hipMemcpyHostToDevice));
+    MRI_HIP(hipMemcpy(L.ffn_norm, ffn_norm, g.dim * 4, hipMemcpyHostToDevice));
+    for (int i = 0; i < 7; ++i) L.w[i] = w[i];
+    L.set = true;
+    return MRI_OK;
+}
+
+void mri_llama_destroy(mri_llama *m) {
+    if (!m) return;
+    for (void *p : m->allocs) (void)hipFree(p);
+    if (m->logits_buf) (void)hipFree(m->logits_buf);
+    delete m;
+}
+
+mri_status mri_kv_cache_create(size_t n_layers, size_t max_seq, size_t n_kv_heads,
+                               size_t head_dim, mri_kv_cache **out) {
+    if (!out) return set_error(MRI_ERR_INVALID_ARGUMENT, "null argument");
+    *out = nullptr;
+    auto *c = new mri_kv_cache();
+    c->n_layers = n_layers;
+    c->max_seq = max_seq;
+    c->kvd = n_kv_heads * head_dim;
+    const size_t bytes = n_layers * max_seq * c->kvd * sizeof(float);
+    hipError_t e;
+    if ((e = hipMalloc(&c->k, bytes ? bytes : 4)) || (e = hipMalloc(&c->v, bytes ? bytes : 4)) ||
+        (e = hipMemset(c->k, 0, bytes)) || (e = hipMemset(c->v, 0, bytes))) {
+        mri_kv_cache_destroy(c);
+        return hip_error(e, "kv_cache_create");
+    }
+    *out = c;
+    return MRI_OK;
+}
+
+void mri_kv_cache_destroy(mri_kv_cache *c) {
+    if (!c) return;
+    if (c->k) (void)hipFree(c->k);
+    if (c->v) (void)hipFree(c->v);
+    delete c;
+}
+
+mri_status mri_llama_forward_cached(mri_llama *m, const uint32_t *tokens, size_t n,
+                                    size_t start_pos, mri_kv_cache *c, float *logits,
+                                    void *stream) {
+    TRY(check_run(m, n, start_pos, c));
+    TRY(check_tokens(m, tokens, n));
+    if (!logits) return set_error(MRI_ERR_INVALID_ARGUMENT, "null logits");
+    auto s = static_cast<hipStream_t>(stream);
+    MRI_HIP(hipMemcpyAsync(m->tok, tokens, n * sizeof(uint32_t), hipMemcpyHostToDevice, s));
+    return run_rows(m, m->tok, n, start_pos, c, logits, s);
+}
+
+mri_status mri_llama_forward_decode(mri_llama *m, uint32_t token, size_t pos, mri_kv_cache *c,
+                                    float *logits, void *stream) {
+    return mri_llama_forward_cached(m, &token, 1, pos, c, logits, stream);
+}
+
+mri_status mri_llama_generate_greedy(mri_llama *m, const uint32_t *prompt, size_t n_prompt,
+                                     size_t n_steps, mri_kv_cache *c, uint32_t *tokens_out,
+                                     float *logits_out, void *stream) {
+    TRY(check_run(m, n_prompt + n_steps, 0, c));
+    if (n_prompt == 0)
+        return set_error(MRI_ERR_INVALID_SHAPE, "generate: prompt must not be empty");
+    TRY(check_tokens(m, prompt, n_prompt));
+    if (!tokens_out) return set_error(MRI_ERR_INVALID_ARGUMENT, "null tokens_out");
+    auto s = static_cast<hipStream_t>(stream);
+    const size_t V = m->cfg.vocab;
+    // prefill logits of every prompt row (the per-tensor activation scale of
+    // the INT8 output projection covers all of them, as LlamaModelInt8::forward)
+    if (m->logits_rows < n_prompt) {
+        if (m->logits_buf) {
+            MRI_HIP(hipStreamSynchronize(s));
+            MRI_HIP(hipFree(m->logits_buf));
+            m->logits_buf = nullptr;
+            m->logits_rows = 0;
+        }
+        MRI_HIP(hipMalloc(&m->logits_buf, n_prompt * V * sizeof(float)));
+        m->logits_rows = n_prompt;
+    }
+    MRI_HIP(hipMemcpyAsync(m->tok, prompt, n_prompt * sizeof(uint32_t), hipMemcpyHostToDevice, s));
+    TRY(run_rows(m, m->tok, n_prompt, 0, c, m->logits_buf, s));
+    const float *last = m->logits_buf + (n_prompt - 1) * V;
+    if (logits_out)
+        MRI_HIP(hipMemcpyAsync(logits_out, last, V * sizeof(float), hipMemcpyDeviceToDevice, s));
+    TRY(launch_argmax(last, 1, V, m->gen, s));
+    for (size_t i = 0; i < n_steps; ++i) {
+        float *lg = logits_out ? logits_out + (i + 1) * V : m->logits_buf;
+        TRY(run_rows(m, m->gen + i, 1, n_prompt + i, c, lg, s));
+        TRY(launch_argmax(lg, 1, V, m->gen + i + 1, s));
+    }
+    MRI_HIP(hipMemcpyAsync(tokens_out, m->gen, (n_steps + 1) * sizeof(uint32_t),
+                           hipMemcpyDeviceToHost, s));
+    MRI_HIP(hipStreamSynchronize(s));
+    return MRI_OK;
+}
+
+mri_status mri_argmax(const float *v, size_t rows, size_t n, uint32_t *idx, void *stream) {
+    if (rows && (!v || !idx)) return set_error(MRI_ERR_INVALID_ARGUMENT, "null pointer");
+    if (rows && n == 0) return set_error(MRI_ERR_INVALID_SHAPE, "argmax: empty rows");
+    return launch_argmax(v, rows, n, idx, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

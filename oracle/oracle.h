@@ -129,6 +129,25 @@ int orc_matmul_q4_0_dequant(const float *input, const size_t *dims,
                             size_t ndim, const uint8_t *w_q4, size_t n_bytes,
                             size_t n_out, size_t k, float *out);
 
+/* ---- decoder-layer steps (llama.c) ------------------------------------- */
+/* rmsnorm, ops/norm/rmsnorm.rs: x [rows, d] -> out, weight w [d]. */
+void orc_rmsnorm(const float *x, size_t rows, size_t d, const float *w, float eps, float *out);
+/* RopeTable::new, ops/rope.rs: cos/sin tables [max_seq][head_dim/2]. */
+void orc_rope_table(size_t max_seq, size_t head_dim, float base, float *cos_out,
+                    float *sin_out);
+/* rope_apply, ops/rope.rs: x [seq, n_heads, head_dim] in place. */
+int orc_rope_apply(float *x, size_t seq, size_t n_heads, size_t head_dim, const float *cos_t,
+                   const float *sin_t, size_t max_seq, size_t start_pos);
+/* grouped_query_attention_causal_with_offset, attention/gqa.rs:217-240;
+ * scratch holds seq_k floats. */
+int orc_gqa_causal(const float *q, size_t seq_q, const float *k, const float *v, size_t seq_k,
+                   size_t n_heads, size_t n_kv_heads, size_t head_dim, size_t start_pos,
+                   float *out, float *scratch);
+/* swiglu, ops/activation/swiglu.rs (silu_scalar, silu.rs:23-26). */
+void orc_swiglu(const float *gate, const float *up, size_t n, float *out);
+/* argmax, sampling/mod.rs:144-151 (last of equal maxima). */
+uint32_t orc_argmax(const float *v, size_t n);
+
 /* Message of the last non-OK status on this thread (TensorError reason). */
 const char *orc_last_error(void);
 

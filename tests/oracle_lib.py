@@ -76,6 +76,16 @@ def _sig(l):
     l.orc_matmul_q4_0_dequant.argtypes = [P, P, SZ, P, SZ, SZ, SZ, P]
     l.orc_last_error.restype = C.c_char_p
     l.orc_have_avx2.restype = C.c_int
+    l.orc_rmsnorm.argtypes = [P, SZ, SZ, P, C.c_float, P]
+    l.orc_rmsnorm.restype = None
+    l.orc_rope_table.argtypes = [SZ, SZ, C.c_float, P, P]
+    l.orc_rope_table.restype = None
+    l.orc_rope_apply.argtypes = [P, SZ, SZ, SZ, P, P, SZ, SZ]
+    l.orc_gqa_causal.argtypes = [P, SZ, P, P, SZ, SZ, SZ, SZ, SZ, P, P]
+    l.orc_swiglu.argtypes = [P, P, SZ, P]
+    l.orc_swiglu.restype = None
+    l.orc_argmax.argtypes = [P, SZ]
+    l.orc_argmax.restype = C.c_uint32
 
 
 def _p(a):
@@ -286,3 +296,129 @@ def matmul_q4_0_dequant(x, w_q4, n_out, k):
 
 def have_avx2() -> bool:
     return bool(lib().orc_have_avx2())
+
+
+# ---- decoder-layer steps (oracle/llama.c) --------------------------------
+def rmsnorm(x, w, eps):
+    x = _c(x, np.float32)
+    w = _c(w, np.float32)
+    d = w.size
+    out = np.empty_like(x)
+    lib().orc_rmsnorm(_p(x), x.size // d, d, _p(w), float(eps), _p(out))
+    return out
+
+
+def rope_table(max_seq, head_dim, base):
+    half = head_dim // 2
+    cos = np.empty((max_seq, half), np.float32)
+    sin = np.empty((max_seq, half), np.float32)
+    lib().orc_rope_table(max_seq, head_dim, float(base), _p(cos), _p(sin))
+    return cos, sin
+
+
+def rope_apply(x, n_heads, head_dim, cos, sin, start_pos):
+    """x [seq, n_heads*head_dim] (or [seq, n_heads, head_dim]); returns a copy."""
+    y = np.array(x, dtype=np.float32, copy=True, order="C")
+    seq = y.size // (n_heads * head_dim)
+    _check(lib().orc_rope_apply(_p(y), seq, n_heads, head_dim, _p(_c(cos, np.float32)),
+                                _p(_c(sin, np.float32)), cos.shape[0], start_pos))
+    return y
+
+
+def gqa_causal(q, k, v, n_heads, n_kv_heads, head_dim, start_pos):
+    q, k, v = _c(q, np.float32), _c(k, np.float32), _c(v, np.float32)
+    seq_q = q.size // (n_heads * head_dim)
+    seq_k = k.size // (n_kv_heads * head_dim)
+    out = np.empty((seq_q, n_heads * head_dim), np.float32)
+    scratch = np.empty(max(seq_k, 1), np.float32)
+    _check(lib().orc_gqa_causal(_p(q), seq_q, _p(k), _p(v), seq_k, n_heads, n_kv_heads,
+                                head_dim, start_pos, _p(out), _p(scratch)))
+    return out
+
+
+def swiglu(gate, up):
+    g, u = _c(gate, np.float32), _c(up, np.float32)
+    out = np.empty_like(g)
+    lib().orc_swiglu(_p(g), _p(u), g.size, _p(out))
+    return out
+
+
+def argmax(v):
+    v = _c(v, np.float32)
+    return int(lib().orc_argmax(_p(v), v.size))
+
+
+# ---- LlamaModelInt8 composition (model/llama/forward_int8.rs) ------------
+class Proj:
+    """One projection weight in one of the three formats: "int8"
+    (QuantizedMatrix: data [N,K] int8 + scales [N], projected by
+    matmul_int8_from_f32, forward_int8.rs:72-74), "q8_0" (raw Q8_0 bytes,
+    matmul_q8_0_direct) or "q4_0" (raw Q4_0 bytes, matmul_q4_0_dequant)."""
+
+    def __init__(self, fmt, n_out, k_in, data, scales=None):
+        self.fmt, self.n_out, self.k_in, self.data, self.scales = fmt, n_out, k_in, data, scales
+
+    def __call__(self, x):
+        if self.fmt == "int8":
+            return matmul_int8_from_f32(x, self.data, self.scales)[0]
+        if self.fmt == "q8_0":
+            return matmul_q8_0_direct(x, self.data, self.n_out, self.k_in)
+        return matmul_q4_0_dequant(x, self.data, self.n_out, self.k_in)
+
+
+class LlamaOracle:
+    """LlamaModelInt8 with a KvCache (forward_int8.rs:148-402, 416-546):
+    forward_cached() is embed -> TransformerBlockInt8::forward_cached per
+    layer -> rmsnorm -> output projection (logits of every row);
+    forward_decode() the one-token step.  layers: list of dicts with keys
+    attn_norm, ffn_norm and wq wk wv wo wgate wup wdown (Proj)."""
+
+    def __init__(self, cfg, token_embd, layers, output_norm, output):
+        self.cfg = cfg
+        self.token_embd = _c(token_embd, np.float32)
+        self.layers = layers
+        self.output_norm = _c(output_norm, np.float32)
+        self.output = output
+        hd = cfg["head_dim"]
+        self.cos, self.sin = rope_table(cfg["max_seq"], hd, cfg["rope_base"])
+        kvd = cfg["n_kv_heads"] * hd
+        self.k_cache = np.zeros((len(layers), cfg["max_seq"], kvd), np.float32)
+        self.v_cache = np.zeros_like(self.k_cache)
+
+    def embed(self, tokens):  # forward_int8.rs:125-140
+        for t in tokens:
+            if t >= self.token_embd.shape[0]:
+                raise OracleError(INVALID_SHAPE, f"token id {t} >= vocab_size")
+        return self.token_embd[np.asarray(tokens, dtype=np.int64)].copy()
+
+    def block(self, li, x, start_pos):
+        """attn_sublayer_cached (forward_int8.rs:291-323) + ffn_sublayer
+        (:350-357); the decode step (:325-348) is the same with seq = 1."""
+        c, L = self.cfg, self.layers[li]
+        nh, nkv, hd = c["n_heads"], c["n_kv_heads"], c["head_dim"]
+        seq = x.shape[0]
+        normed = rmsnorm(x, L["attn_norm"], c["eps"])
+        q = L["wq"](normed)
+        k = L["wk"](normed)
+        v = L["wv"](normed)
+        q = rope_apply(q, nh, hd, self.cos, self.sin, start_pos)
+        k = rope_apply(k, nkv, hd, self.cos, self.sin, start_pos)
+        self.k_cache[li, start_pos:start_pos + seq] = k   # cached.rs write_k / write_v
+        self.v_cache[li, start_pos:start_pos + seq] = v
+        total = start_pos + seq
+        attn = gqa_causal(q, self.k_cache[li, :total], self.v_cache[li, :total], nh, nkv, hd,
+                          start_pos)
+        x = x + L["wo"](attn)
+        normed = rmsnorm(x, L["ffn_norm"], c["eps"])
+        h = swiglu(L["wgate"](normed), L["wup"](normed))
+        return x + L["wdown"](h)
+
+    def forward_cached(self, tokens, start_pos=0):
+        x = self.embed(tokens)
+        for li in range(len(self.layers)):
+            x = self.block(li, x, start_pos)
+        x = rmsnorm(x, self.output_norm, self.cfg["eps"])
+        return self.output(x)
+
+    def forward_decode(self, token, pos):
+        return self.forward_cached([token], pos)[0]

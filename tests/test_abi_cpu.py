@@ -9,24 +9,32 @@ import numpy as np
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "mri_qmatmul.h")
+HEADERS = {"mri_qmatmul": os.path.join(ROOT, "include", "mri_qmatmul.h"),
+           "mri_llama": os.path.join(ROOT, "include", "mri_llama.h")}
 
 
-def declared_functions():
-    src = open(HEADER).read()
+def declared_functions(module="mri_qmatmul"):
+    src = open(HEADERS[module]).read()
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
     return sorted(set(re.findall(r"\b(mri_[a-z0-9_]+)\s*\(", src)))
 
 
-def test_header_and_binding_agree():
-    import mri_qmatmul
-    assert sorted(mri_qmatmul.EXPORTED) == declared_functions()
+def test_every_header_has_a_binding():
+    assert sorted(HEADERS) == sorted(f[:-2] for f in os.listdir(os.path.join(ROOT, "include"))
+                                     if f.endswith(".h"))
 
 
-def test_library_exports_every_declared_symbol():
+@pytest.mark.parametrize("module", sorted(HEADERS))
+def test_header_and_binding_agree(module):
+    import importlib
+    assert sorted(importlib.import_module(module).EXPORTED) == declared_functions(module)
+
+
+@pytest.mark.parametrize("module", sorted(HEADERS))
+def test_library_exports_every_declared_symbol(module):
     import mri_qmatmul
     lib = mri_qmatmul.lib()
-    for name in declared_functions():
+    for name in declared_functions(module):
         assert hasattr(lib, name), name
     assert b"gfx950" in lib.mri_version()
 
@@ -81,3 +89,26 @@ def test_fails_loudly_without_gpu():
     rc = M.lib().mri_q8_0_matrix_from_raw_bytes(raw.ctypes.data_as(C.c_void_p), 34, 1,
                                                 32, C.byref(h))
     assert rc != 0 and _status(rc) in ("HipError", "Unsupported")
+
+
+def test_llama_argument_errors_before_device_work():
+    """Shape errors of the model API (forward_int8.rs / config checks) come
+    before any device call."""
+    import mri_llama as L
+    lib = L.lib()
+    h = C.c_void_p()
+    emb = np.zeros(4, np.float32)
+    bad = L.Config(dim=6, n_heads=4, n_kv_heads=2, ffn_dim=8, vocab=2, max_seq=4, eps=1e-6,
+                   rope_base=1e4, n_layers=1)  # dim % n_heads != 0
+    rc = lib.mri_llama_create(C.byref(bad), emb.ctypes.data_as(C.c_void_p),
+                              emb.ctypes.data_as(C.c_void_p), L.WeightRef(0, None, 0, 0),
+                              C.byref(h))
+    assert _status(rc) == "InvalidShape"
+    odd = L.Config(dim=96, n_heads=2, n_kv_heads=2, ffn_dim=8, vocab=2, max_seq=4, eps=1e-6,
+                   rope_base=1e4, n_layers=1)  # head_dim 48: no attention kernel for it
+    rc = lib.mri_llama_create(C.byref(odd), emb.ctypes.data_as(C.c_void_p),
+                              emb.ctypes.data_as(C.c_void_p), L.WeightRef(0, None, 0, 0),
+                              C.byref(h))
+    assert _status(rc) == "Unsupported"
+    assert _status(lib.mri_llama_forward_cached(None, None, 0, 0, None, None, None)) \
+        == "InvalidArgument"

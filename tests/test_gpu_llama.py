@@ -1,0 +1,191 @@
+"""GPU LlamaModelInt8 (include/mri_llama.h) against the CPU oracle's
+composition (tests/oracle_lib.py LlamaOracle over oracle/llama.c).
+
+Tolerances.  The layer's f32 sums (RMSNorm, softmax denominator, attention
+value sum) and exp differ from the reference in rounding only.  With Q4_0
+weights (W4A32, no activation quantization) that is all that differs, and
+the logits agree to 1e-4 of their largest magnitude.  INT8 and Q8_0
+projections quantize their inputs to int8: a last-bit difference in an
+activation can move one element across a rounding boundary, which changes
+that element by one quantization step, so the logits of those models are
+compared to 2e-2 of their largest magnitude (a wrong head, position or
+mask moves them by O(1)) and greedy tokens by their oracle margin."""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from gpu_util import dev, empty, host
+
+pytestmark = pytest.mark.gpu
+
+F32 = np.float32
+
+
+def torch():
+    import torch as t
+    return t
+
+
+def mods():
+    import mri_llama as L
+    import mri_qmatmul as Q
+    return L, Q
+
+
+def build(fmt, seed=0, d=256, nh=4, nkv=2, ffn=512, vocab=300, max_seq=48, n_layers=2):
+    """The same random model on both sides."""
+    L, Q = mods()
+    rng = np.random.default_rng(seed)
+    hd = d // nh
+    cfg = dict(dim=d, n_heads=nh, n_kv_heads=nkv, head_dim=hd, ffn=ffn, vocab=vocab,
+               max_seq=max_seq, eps=1e-6, rope_base=10000.0)
+
+    def proj(n, k):
+        w = (rng.standard_normal((n, k)) * 0.05).astype(F32)
+        if fmt == "int8":
+            data, scales = O.quantize_per_channel(w, n, k)
+            return O.Proj("int8", n, k, data, scales), Q.QMatrix.from_host(data, scales)
+        if fmt == "q8_0":
+            raw = O.quantize_q8_0(w)
+            return O.Proj("q8_0", n, k, raw), Q.Q8Matrix.from_raw_bytes(raw, n, k)
+        raw = O.quantize_q4_0(w)
+        return O.Proj("q4_0", n, k, raw), (dev(raw), n, k)
+
+    o_layers, g_layers = [], []
+    for _ in range(n_layers):
+        an = rng.uniform(0.8, 1.2, d).astype(F32)
+        fn = rng.uniform(0.8, 1.2, d).astype(F32)
+        ol, gl = dict(attn_norm=an, ffn_norm=fn), dict(attn_norm=an, ffn_norm=fn)
+        for name, (n, k) in (("wq", (nh * hd, d)), ("wk", (nkv * hd, d)), ("wv", (nkv * hd, d)),
+                             ("wo", (d, nh * hd)), ("wgate", (ffn, d)), ("wup", (ffn, d)),
+                             ("wdown", (d, ffn))):
+            ol[name], gl[name] = proj(n, k)
+        o_layers.append(ol)
+        g_layers.append(gl)
+    embd = rng.standard_normal((vocab, d)).astype(F32)
+    onorm = rng.uniform(0.8, 1.2, d).astype(F32)
+    o_out, g_out = proj(vocab, d)
+    oracle = O.LlamaOracle(cfg, embd, o_layers, onorm, o_out)
+    gpu = L.Llama(cfg, embd, onorm, g_out, g_layers)
+    return oracle, gpu, rng
+
+
+def close(got, ref, frac):
+    scale = float(np.abs(ref).max())
+    err = float(np.abs(got - ref).max())
+    assert err <= frac * scale, f"max |gpu - ref| = {err:.3g} > {frac} * {scale:.3g}"
+
+
+TOL = {"q4_0": 1e-4, "q8_0": 2e-2, "int8": 2e-2}
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0", "int8"])
+def test_llama_prefill_and_decode_logits(fmt):
+    """forward_cached over a prompt, then forward_decode steps (teacher
+    forced: both sides see the same tokens)."""
+    t = torch()
+    oracle, gpu, rng = build(fmt, seed={"q4_0": 1, "q8_0": 2, "int8": 3}[fmt])
+    toks = rng.integers(0, 300, 24).tolist()
+    cache = gpu.kv_cache()
+    logits = empty((20, 300), t.float32)
+    gpu.forward_cached(toks[:20], 0, cache, logits)
+    ref = oracle.forward_cached(toks[:20], 0)
+    close(host(logits), ref, TOL[fmt])
+    one = empty((300,), t.float32)
+    for p in range(20, 24):
+        gpu.forward_decode(toks[p], p, cache, one)
+        close(host(one), oracle.forward_decode(toks[p], p), TOL[fmt])
+
+
+def test_llama_gqa_and_mha_head_dim_128():
+    """n_kv_heads == n_heads (MHA) with head_dim 128, the 7B geometry, and a
+    prefill that starts past position 0."""
+    t = torch()
+    oracle, gpu, rng = build("q4_0", seed=5, d=256, nh=2, nkv=2, ffn=384, max_seq=40,
+                             n_layers=1)
+    toks = rng.integers(0, 300, 30).tolist()
+    cache = gpu.kv_cache()
+    lg = empty((17, 300), t.float32)
+    gpu.forward_cached(toks[:17], 0, cache, lg)
+    close(host(lg), oracle.forward_cached(toks[:17], 0), 1e-4)
+    lg2 = empty((13, 300), t.float32)
+    gpu.forward_cached(toks[17:], 17, cache, lg2)  # a second chunk at start_pos 17
+    close(host(lg2), oracle.forward_cached(toks[17:], 17), 1e-4)
+
+
+def test_llama_decode_matches_prefill_rows_q8_0():
+    """Per-row activation quantization: decoding token p after a prefill of
+    0..p-1 gives prefill row p (the oracle's rows are bit-identical; the GPU
+    attention sums differ in order between the two launch shapes only)."""
+    t = torch()
+    _, gpu, rng = build("q8_0", seed=7)
+    toks = rng.integers(0, 300, 16).tolist()
+    c1 = gpu.kv_cache()
+    full = empty((16, 300), t.float32)
+    gpu.forward_cached(toks, 0, c1, full)
+    c2 = gpu.kv_cache()
+    part = empty((12, 300), t.float32)
+    gpu.forward_cached(toks[:12], 0, c2, part)
+    one = empty((300,), t.float32)
+    for p in range(12, 16):
+        gpu.forward_decode(toks[p], p, c2, one)
+        close(host(one), host(full)[p], 2e-2)
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+def test_llama_generate_greedy(fmt):
+    """Device-resident greedy loop: every chosen token is the oracle's
+    argmax of the oracle's logits on the same (teacher-forced) prefix, or
+    within the comparison tolerance of it."""
+    t = torch()
+    oracle, gpu, rng = build(fmt, seed=11)
+    prompt = rng.integers(0, 300, 16).tolist()
+    cache = gpu.kv_cache()
+    steps = 12
+    lg = empty((steps + 1, 300), t.float32)
+    toks = gpu.generate_greedy(prompt, steps, cache, lg)
+    assert toks.shape == (steps + 1,)
+    ref_rows = [oracle.forward_cached(prompt, 0)[-1]]
+    for i in range(steps):
+        ref_rows.append(oracle.forward_decode(int(toks[i]), len(prompt) + i))
+    ref = np.stack(ref_rows)
+    close(host(lg), ref, TOL[fmt])
+    g = host(lg)
+    for i in range(steps + 1):
+        assert toks[i] == O.argmax(g[i])  # the GPU picked its own argmax
+        margin = ref[i].max() - ref[i][toks[i]]
+        assert margin <= TOL[fmt] * np.abs(ref[i]).max(), f"step {i}: margin {margin}"
+
+
+def test_argmax_last_of_ties():
+    t = torch()
+    L, _ = mods()
+    rng = np.random.default_rng(4)
+    v = rng.standard_normal((3, 32000)).astype(F32)
+    v[1, 5] = v[1, 31999] = v[1, 777] = 9.0  # ties: the last wins
+    v[2, :] = -1.0
+    idx = empty((3,), t.int32)
+    L.argmax(dev(v), idx)
+    got = host(idx).view(np.uint32)
+    assert got[0] == O.argmax(v[0]) and got[1] == 31999 and got[2] == 31999
+
+
+def test_llama_errors():
+    t = torch()
+    L, Q = mods()
+    _, gpu, _ = build("q8_0", seed=13, n_layers=1)
+    cache = gpu.kv_cache()
+    lg = empty((4, 300), t.float32)
+    with pytest.raises(Q.MriError) as e:
+        gpu.forward_cached([1, 2, 300], 0, cache, lg)  # id >= vocab (forward_int8.rs:132)
+    assert e.value.kind == "InvalidShape"
+    with pytest.raises(Q.MriError) as e:
+        gpu.forward_cached([1, 2], 47, cache, lg)  # past the cache
+    assert e.value.kind == "InvalidShape"
+    with pytest.raises(Q.MriError) as e:
+        gpu.forward_cached([], 0, cache, lg)
+    assert e.value.kind == "InvalidShape"
+    other = L.KvCache(2, 48, 2, 64)  # two layers: not this model's cache
+    with pytest.raises(Q.MriError) as e:
+        gpu.forward_cached([1], 0, other, lg)
+    assert e.value.kind == "ShapeMismatch"
