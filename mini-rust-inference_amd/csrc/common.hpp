@@ -200,15 +200,17 @@ mri_status launch_embed(const float *table, const uint32_t *tokens, size_t rows,
 mri_status launch_rmsnorm(const float *x, const float *w, size_t rows, size_t d, float eps,
                           float *out, hipStream_t s);
 // RoPE of q in place; rotated k and v rows into the cache at start_pos + s.
-mri_status launch_rope_qkv(float *q, const float *k, const float *v, size_t seq, size_t qd,
-                           size_t kvd, size_t head_dim, const float *cos_t, const float *sin_t,
+mri_status launch_rope_qkv(float *q, const float *k, const float *v, size_t seq, size_t n_heads,
+                           size_t n_kv, size_t head_dim, const float *cos_t, const float *sin_t,
                            size_t start_pos, float *kc, float *vc, hipStream_t s);
 bool attention_supported(size_t head_dim);
 // Causal GQA of seq_q query rows (positions start_pos ..) against cache rows
-// 0 .. start_pos + seq_q - 1.
+// 0 .. start_pos + seq_q - 1.  part: attention_part_floats(...) floats of
+// workspace for the split-key one-row form (nullable: one workgroup per head).
+size_t attention_part_floats(size_t n_heads, size_t head_dim, size_t max_seq);
 mri_status launch_attention(const float *q, size_t seq_q, const float *kc, const float *vc,
                             size_t n_heads, size_t n_kv_heads, size_t head_dim,
-                            size_t start_pos, float *out, hipStream_t s);
+                            size_t start_pos, float *out, float *part, hipStream_t s);
 mri_status launch_swiglu(const float *gate, const float *up, size_t n, float *out,
                          hipStream_t s);
 mri_status launch_add(const float *a, const float *b, size_t n, float *out, hipStream_t s);

@@ -31,18 +31,30 @@ __device__ inline float wave_max(float v) {
 }
 
 // ---- embedding lookup (forward_int8.rs:125-140) ------------------------------
-// x[r, :] = table[tokens[r], :].  Token ids are checked against the vocabulary
-// on the host, or come from the argmax kernel (always < vocab).
+// x[r, :] = table[tokens[r], :], 1024 floats per workgroup.  Token ids are
+// checked against the vocabulary on the host, or come from the argmax
+// kernel (always < vocab).  d % 4 == 0 (the float4 path) or any d.
+template <bool V4>
 __global__ __launch_bounds__(256) void k_embed(const float *__restrict__ table,
                                                const uint32_t *__restrict__ tokens, int d,
                                                float *__restrict__ x) {
     const size_t src = (size_t)tokens[blockIdx.x] * d, dst = (size_t)blockIdx.x * d;
-    for (int i = threadIdx.x; i < d; i += 256) x[dst + i] = table[src + i];
+    const int i = (blockIdx.y * 256 + threadIdx.x) * 4;
+    if constexpr (V4) {
+        if (i < d)
+            *reinterpret_cast<float4 *>(x + dst + i) =
+                *reinterpret_cast<const float4 *>(table + src + i);
+    } else {
+        for (int e = i; e < min(i + 4, d); ++e) x[dst + e] = table[src + e];
+    }
 }
 
 // ---- RMSNorm (ops/norm/rmsnorm.rs) ------------------------------------------------
 // One workgroup per row: mean_sq = sum(x*x) / d, rms_inv = 1 / sqrt(mean_sq +
-// eps) (correctly rounded divide and sqrt), out = w * (x * rms_inv).
+// eps) (correctly rounded divide and sqrt), out = w * (x * rms_inv).  NV > 0:
+// the row is read once into registers, NV float4 per thread (d % 4 == 0,
+// d <= 1024 * NV); NV == 0: any d, two passes.
+template <int NV>
 __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x,
                                                  const float *__restrict__ w, int d, float eps,
                                                  float *__restrict__ out) {
@@ -50,9 +62,29 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x,
     const float *xr = x + (size_t)blockIdx.x * d;
     float *orow = out + (size_t)blockIdx.x * d;
     float acc = 0.0f;
-    for (int i = threadIdx.x; i < d; i += 256) {
-        const float sq = xr[i] * xr[i];
-        acc = acc + sq;
+    float4 xv[NV > 0 ? NV : 1];
+    if constexpr (NV > 0) {
+#pragma unroll
+        for (int c = 0; c < NV; ++c) {
+            const int i = (c * 256 + threadIdx.x) * 4;
+            xv[c] = i < d ? *reinterpret_cast<const float4 *>(xr + i) : float4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int c = 0; c < NV; ++c) {
+            float sq = xv[c].x * xv[c].x;
+            acc = acc + sq;
+            sq = xv[c].y * xv[c].y;
+            acc = acc + sq;
+            sq = xv[c].z * xv[c].z;
+            acc = acc + sq;
+            sq = xv[c].w * xv[c].w;
+            acc = acc + sq;
+        }
+    } else {
+        for (int i = threadIdx.x; i < d; i += 256) {
+            const float sq = xr[i] * xr[i];
+            acc = acc + sq;
+        }
     }
     acc = wave_sum(acc);
     if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = acc;
@@ -60,9 +92,25 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x,
     const float sum = ((s_part[0] + s_part[1]) + s_part[2]) + s_part[3];
     const float mean_sq = sum / (float)d;
     const float rms_inv = 1.0f / sqrtf(mean_sq + eps);
-    for (int i = threadIdx.x; i < d; i += 256) {
-        const float t = xr[i] * rms_inv;
-        orow[i] = w[i] * t;
+    if constexpr (NV > 0) {
+#pragma unroll
+        for (int c = 0; c < NV; ++c) {
+            const int i = (c * 256 + threadIdx.x) * 4;
+            if (i < d) {
+                const float4 wv = *reinterpret_cast<const float4 *>(w + i);
+                float4 o;
+                o.x = wv.x * (xv[c].x * rms_inv);
+                o.y = wv.y * (xv[c].y * rms_inv);
+                o.z = wv.z * (xv[c].z * rms_inv);
+                o.w = wv.w * (xv[c].w * rms_inv);
+                *reinterpret_cast<float4 *>(orow + i) = o;
+            }
+        }
+    } else {
+        for (int i = threadIdx.x; i < d; i += 256) {
+            const float t = xr[i] * rms_inv;
+            orow[i] = w[i] * t;
+        }
     }
 }
 
@@ -70,63 +118,74 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x,
 // Row s of q (n_heads heads) and k (n_kv heads) is rotated with table row
 // start_pos + s: pair (2i, 2i+1) -> (x0*c - x1*s, x1*c + x0*s).  q is
 // rotated in place; the rotated k row and the v row are written to the
-// cache at position start_pos + s (write_k / write_v).
-__global__ __launch_bounds__(256) void k_rope_qkv(float *__restrict__ q,
-                                                  const float *__restrict__ k,
-                                                  const float *__restrict__ v, int qd, int kvd,
-                                                  int half, const float *__restrict__ cos_t,
-                                                  const float *__restrict__ sin_t, int start_pos,
-                                                  float *__restrict__ kc,
-                                                  float *__restrict__ vc) {
-    const int s = blockIdx.x, pos = start_pos + s;
-    const float *ct = cos_t + (size_t)pos * half, *st = sin_t + (size_t)pos * half;
-    float *qr = q + (size_t)s * qd;
-    for (int p = threadIdx.x; p < qd / 2; p += 256) {
-        const int i = p % half;
-        const float c = ct[i], sn = st[i];
-        const float x0 = qr[2 * p], x1 = qr[2 * p + 1];
-        const float a0 = x0 * c, a1 = x1 * sn, b0 = x1 * c, b1 = x0 * sn;
-        qr[2 * p] = a0 - a1;
-        qr[2 * p + 1] = b0 + b1;
+// cache at position start_pos + s (write_k / write_v).  Workgroup (s, y):
+// one head of row s, y < n_heads a q head, then the k heads, then the v
+// heads; thread i owns pair i (half = head_dim / 2 <= 64 threads).
+__global__ __launch_bounds__(64) void k_rope_qkv(float *__restrict__ q,
+                                                 const float *__restrict__ k,
+                                                 const float *__restrict__ v, int qd, int kvd,
+                                                 int half, int n_heads, int n_kv,
+                                                 const float *__restrict__ cos_t,
+                                                 const float *__restrict__ sin_t, int start_pos,
+                                                 float *__restrict__ kc,
+                                                 float *__restrict__ vc) {
+    const int s = blockIdx.x, pos = start_pos + s, y = blockIdx.y, i = threadIdx.x;
+    if (i >= half) return;
+    const int hd = 2 * half;
+    if (y >= n_heads + n_kv) {  // v head: copy
+        const int off = (y - n_heads - n_kv) * hd + 2 * i;
+        const float2 vv = *reinterpret_cast<const float2 *>(v + (size_t)s * kvd + off);
+        *reinterpret_cast<float2 *>(vc + (size_t)pos * kvd + off) = vv;
+        return;
     }
-    const float *kr = k + (size_t)s * kvd;
-    float *kd = kc + (size_t)pos * kvd;
-    for (int p = threadIdx.x; p < kvd / 2; p += 256) {
-        const int i = p % half;
-        const float c = ct[i], sn = st[i];
-        const float x0 = kr[2 * p], x1 = kr[2 * p + 1];
-        const float a0 = x0 * c, a1 = x1 * sn, b0 = x1 * c, b1 = x0 * sn;
-        kd[2 * p] = a0 - a1;
-        kd[2 * p + 1] = b0 + b1;
+    const float c = cos_t[(size_t)pos * half + i], sn = sin_t[(size_t)pos * half + i];
+    const float *src;
+    float *dst;
+    if (y < n_heads) {
+        src = dst = q + (size_t)s * qd + y * hd + 2 * i;
+    } else {
+        src = k + (size_t)s * kvd + (y - n_heads) * hd + 2 * i;
+        dst = kc + (size_t)pos * kvd + (y - n_heads) * hd + 2 * i;
     }
-    const float *vr = v + (size_t)s * kvd;
-    float *vd = vc + (size_t)pos * kvd;
-    for (int i = threadIdx.x; i < kvd; i += 256) vd[i] = vr[i];
+    const float2 xv = *reinterpret_cast<const float2 *>(src);
+    const float a0 = xv.x * c, a1 = xv.y * sn, b0 = xv.y * c, b1 = xv.x * sn;
+    *reinterpret_cast<float2 *>(dst) = float2{a0 - a1, b0 + b1};
 }
 
 // ---- causal grouped-query attention (attention/gqa.rs:217-240) --------------------------
-// Workgroup (query block b, head h): QB query rows i (absolute positions
-// start_pos + i) against the keys 0 .. L-1 of kv head h / groups in the
-// cache, L = start_pos + last row + 1.  Same three passes as the reference:
-//  1. scores: lane j of the workgroup owns key j and computes its dot product
-//     with each of the QB queries sequentially over the head dimension
-//     (matmul_naive's order), times 1/sqrt(head_dim); keys after a row's
-//     position get -inf (causal mask).  The queries sit in LDS and are read
-//     as broadcasts; each key row is read once per workgroup.
+// Prefill form.  Workgroup (query block, head h): QB query rows i (absolute
+// positions start_pos + i) against the keys 0 .. L-1 of kv head
+// h / groups in the cache, L = start_pos + the block's last row + 1.  The
+// reference's three passes:
+//  1. scores, one 64-key tile at a time: the tile is loaded by the whole
+//     workgroup at once (one load latency per tile) and stored transposed,
+//     kT[p][key] with a row pitch of 65 floats, so that lane `key` reading
+//     kT[p][key] and the loading lanes writing it hit distinct banks.  Lane
+//     `key` of wave w computes the dot products of its key with queries w,
+//     w + 4, ... sequentially over the head dimension (matmul_naive's order),
+//     times 1/sqrt(head_dim); keys past a row's position get -inf.
 //  2. softmax per row: max, exp(s - max), sum, times 1/sum.
-//  3. values: wave w sums its quarter of the keys, lane l owning dims
-//     HD/64 * l ..; the four partial rows are added in wave order.
-// LDS: queries [QB][HD], weights [QB][Lcap], partials [4][QB][HD].
+//  3. values, one 64-key tile at a time (row-major in LDS): lane l of wave w
+//     owns dims HD/64 * l .. of queries w, w + 4, ... and sums the keys in
+//     order, as the reference.
+// LDS: queries [QB][HD], one tile [max(HD*65, 64*HD)], weights [QB][lcap].
+template <int HD>
+constexpr int attn_tile_floats() { return HD * 65 > 64 * HD ? HD * 65 : 64 * HD; }
+
 template <int HD, int QB>
 __global__ __launch_bounds__(256) void k_attention(
     const float *__restrict__ q, int qd, const float *__restrict__ kc,
     const float *__restrict__ vc, int kvd, int seq_q, int start_pos, int groups, int lcap,
     float scale, float *__restrict__ out) {
     constexpr int E = HD / kWave;  // dims per lane in the value pass
+    constexpr int R = QB / 4;      // queries per wave
+    constexpr int KT = 64;         // keys per tile
+    constexpr int P4 = HD / 4;     // float4 per key row
+    static_assert(QB % 4 == 0, "query block");
     extern __shared__ float s_mem[];
-    float *s_q = s_mem;                    // [QB][HD]
-    float *s_p = s_q + QB * HD;            // [QB][lcap]
-    float *s_o = s_p + (size_t)QB * lcap;  // [4][QB][HD]
+    float *s_q = s_mem;                          // [QB][HD]
+    float *s_t = s_q + QB * HD;                  // tile
+    float *s_p = s_t + attn_tile_floats<HD>();   // [QB][lcap]
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     const int h = blockIdx.y, kh = h / groups;
     const int i0 = blockIdx.x * QB;
@@ -136,33 +195,50 @@ __global__ __launch_bounds__(256) void k_attention(
         const int qq = e / HD, p = e % HD;
         s_q[e] = qq < nq ? q[(size_t)(i0 + qq) * qd + h * HD + p] : 0.0f;
     }
-    __syncthreads();
     // 1. scores
-    for (int j = t; j < L; j += 256) {
-        float acc[QB];
+    for (int j0 = 0; j0 < L; j0 += KT) {
+        __syncthreads();  // the previous tile is consumed (and s_q written)
 #pragma unroll
-        for (int qq = 0; qq < QB; ++qq) acc[qq] = 0.0f;
-        const float4 *kr = reinterpret_cast<const float4 *>(kc + (size_t)j * kvd + kh * HD);
-#pragma unroll 4
-        for (int p4 = 0; p4 < HD / 4; ++p4) {
-            const float4 kv = kr[p4];
+        for (int u = 0; u < KT * P4 / 256; ++u) {
+            const int idx = t + 256 * u, key = idx / P4, p4 = idx % P4;
+            float4 kv = float4{0, 0, 0, 0};
+            if (j0 + key < L)
+                kv = *reinterpret_cast<const float4 *>(kc + (size_t)(j0 + key) * kvd + kh * HD +
+                                                       4 * p4);
+            s_t[(4 * p4 + 0) * 65 + key] = kv.x;
+            s_t[(4 * p4 + 1) * 65 + key] = kv.y;
+            s_t[(4 * p4 + 2) * 65 + key] = kv.z;
+            s_t[(4 * p4 + 3) * 65 + key] = kv.w;
+        }
+        __syncthreads();
+        float acc[R];
 #pragma unroll
-            for (int qq = 0; qq < QB; ++qq) {
-                const float4 qv = reinterpret_cast<const float4 *>(s_q + qq * HD)[p4];
-                float m0 = qv.x * kv.x;
-                acc[qq] = acc[qq] + m0;
-                m0 = qv.y * kv.y;
-                acc[qq] = acc[qq] + m0;
-                m0 = qv.z * kv.z;
-                acc[qq] = acc[qq] + m0;
-                m0 = qv.w * kv.w;
-                acc[qq] = acc[qq] + m0;
+        for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+        for (int p4 = 0; p4 < P4; ++p4) {
+            float kk[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) kk[c] = s_t[(4 * p4 + c) * 65 + lane];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float4 qv = reinterpret_cast<const float4 *>(s_q + (wv + 4 * r) * HD)[p4];
+                float m0 = qv.x * kk[0];
+                acc[r] = acc[r] + m0;
+                m0 = qv.y * kk[1];
+                acc[r] = acc[r] + m0;
+                m0 = qv.z * kk[2];
+                acc[r] = acc[r] + m0;
+                m0 = qv.w * kk[3];
+                acc[r] = acc[r] + m0;
             }
         }
+        const int j = j0 + lane;
+        if (j < L) {
 #pragma unroll
-        for (int qq = 0; qq < QB; ++qq) {
-            const float sc = acc[qq] * scale;
-            s_p[qq * lcap + j] = j <= start_pos + i0 + qq ? sc + 0.0f : -INFINITY;
+            for (int r = 0; r < R; ++r) {
+                const int qq = wv + 4 * r;
+                const float sc = acc[r] * scale;
+                s_p[qq * lcap + j] = j <= start_pos + i0 + qq ? sc + 0.0f : -INFINITY;
+            }
         }
     }
     __syncthreads();
@@ -182,41 +258,148 @@ __global__ __launch_bounds__(256) void k_attention(
         const float inv = 1.0f / sum;
         for (int j = lane; j < L; j += kWave) row[j] = row[j] * inv;
     }
-    __syncthreads();
-    // 3. weighted values: wave wv sums keys [j0, j1)
-    const int j0 = (int)((long long)L * wv / 4), j1 = (int)((long long)L * (wv + 1) / 4);
-    float o[QB][E];
+    // 3. weighted values
+    float o[R][E];
 #pragma unroll
-    for (int qq = 0; qq < QB; ++qq)
+    for (int r = 0; r < R; ++r)
 #pragma unroll
-        for (int e = 0; e < E; ++e) o[qq][e] = 0.0f;
-    for (int j = j0; j < j1; ++j) {
-        const float *vr = vc + (size_t)j * kvd + kh * HD + lane * E;
-        float vv[E];
+        for (int e = 0; e < E; ++e) o[r][e] = 0.0f;
+    for (int j0 = 0; j0 < L; j0 += KT) {
+        __syncthreads();  // softmax done / the previous tile consumed
 #pragma unroll
-        for (int e = 0; e < E; ++e) vv[e] = vr[e];
+        for (int u = 0; u < KT * P4 / 256; ++u) {
+            const int idx = t + 256 * u, key = idx / P4, p4 = idx % P4;
+            float4 vv = float4{0, 0, 0, 0};
+            if (j0 + key < L)
+                vv = *reinterpret_cast<const float4 *>(vc + (size_t)(j0 + key) * kvd + kh * HD +
+                                                       4 * p4);
+            reinterpret_cast<float4 *>(s_t)[idx] = vv;  // [key][HD]
+        }
+        __syncthreads();
+        const int jn = min(KT, L - j0);
+        for (int j = 0; j < jn; ++j) {
+            float vv[E];
 #pragma unroll
-        for (int qq = 0; qq < QB; ++qq) {
-            const float w = s_p[qq * lcap + j];
+            for (int e = 0; e < E; ++e) vv[e] = s_t[j * HD + lane * E + e];
 #pragma unroll
-            for (int e = 0; e < E; ++e) {
-                const float m0 = w * vv[e];
-                o[qq][e] = o[qq][e] + m0;
+            for (int r = 0; r < R; ++r) {
+                const float w = s_p[(wv + 4 * r) * lcap + j0 + j];
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    const float m0 = w * vv[e];
+                    o[r][e] = o[r][e] + m0;
+                }
             }
         }
     }
 #pragma unroll
-    for (int qq = 0; qq < QB; ++qq)
+    for (int r = 0; r < R; ++r) {
+        const int qq = wv + 4 * r;
+        if (qq < nq)
 #pragma unroll
-        for (int e = 0; e < E; ++e) s_o[(wv * QB + qq) * HD + lane * E + e] = o[qq][e];
-    __syncthreads();
-    for (int e = t; e < nq * HD; e += 256) {
-        const int qq = e / HD, p = e % HD;
-        const float r = ((s_o[(0 * QB + qq) * HD + p] + s_o[(1 * QB + qq) * HD + p]) +
-                         s_o[(2 * QB + qq) * HD + p]) +
-                        s_o[(3 * QB + qq) * HD + p];
-        out[(size_t)(i0 + qq) * qd + h * HD + p] = r;
+            for (int e = 0; e < E; ++e) out[(size_t)(i0 + qq) * qd + h * HD + lane * E + e] = o[r][e];
     }
+}
+
+// Decode form (one query row), split over the keys.  Workgroup (chunk c,
+// head h) takes keys [64c, 64c + 64) of the L = start_pos + 1 visible ones:
+// thread t forms the partial dot of key t % 64 over dims (t / 64) * HD/4 ..,
+// the four partials are added in order; then the chunk's max m_c, weights
+// e_j = exp(s_j - m_c) and their sum l_c, and the chunk's weighted value
+// sum o_c (four key quarters added in order).  part: [heads][chunks][HD+2].
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_decode_part(
+    const float *__restrict__ q, const float *__restrict__ kc, const float *__restrict__ vc,
+    int kvd, int L, int groups, float scale, float *__restrict__ part) {
+    constexpr int Q4 = HD / 16;  // float4 per thread in the score pass
+    constexpr int E = HD / kWave;
+    __shared__ float s_s[4][64];
+    __shared__ float s_w[64];
+    __shared__ float s_o[4][HD];
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    const int c = blockIdx.x, h = blockIdx.y, kh = h / groups, nch = gridDim.x;
+    const int j = 64 * c + lane;
+    const float *qr = q + (size_t)h * HD + wv * (HD / 4);
+    float acc = 0.0f;
+    if (j < L) {
+        const float4 *kr = reinterpret_cast<const float4 *>(kc + (size_t)j * kvd + kh * HD +
+                                                            wv * (HD / 4));
+        float4 kv[Q4];
+#pragma unroll
+        for (int u = 0; u < Q4; ++u) kv[u] = kr[u];
+#pragma unroll
+        for (int u = 0; u < Q4; ++u) {
+            const float4 qv = reinterpret_cast<const float4 *>(qr)[u];
+            float m0 = qv.x * kv[u].x;
+            acc = acc + m0;
+            m0 = qv.y * kv[u].y;
+            acc = acc + m0;
+            m0 = qv.z * kv[u].z;
+            acc = acc + m0;
+            m0 = qv.w * kv[u].w;
+            acc = acc + m0;
+        }
+    }
+    s_s[wv][lane] = acc;
+    __syncthreads();
+    if (wv == 0) {
+        const float sc = (((s_s[0][lane] + s_s[1][lane]) + s_s[2][lane]) + s_s[3][lane]) * scale;
+        const float sv = j < L ? sc : -INFINITY;
+        const float m = wave_max(sv);
+        const float e = j < L ? expf(sv - m) : 0.0f;
+        const float l = wave_sum(e);
+        s_w[lane] = e;
+        if (lane == 0) {
+            part[((size_t)h * nch + c) * (HD + 2)] = m;
+            part[((size_t)h * nch + c) * (HD + 2) + 1] = l;
+        }
+    }
+    __syncthreads();
+    // weighted values: wave wv sums keys 16wv .. 16wv + 15 of the chunk
+    float o[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) o[e] = 0.0f;
+    float vv[16][E];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+        const int jj = 64 * c + 16 * wv + u;
+#pragma unroll
+        for (int e = 0; e < E; ++e)
+            vv[u][e] = jj < L ? vc[(size_t)jj * kvd + kh * HD + lane * E + e] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+        const float w = s_w[16 * wv + u];
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const float m0 = w * vv[u][e];
+            o[e] = o[e] + m0;
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) s_o[wv][lane * E + e] = o[e];
+    __syncthreads();
+    for (int d = t; d < HD; d += 256)
+        part[((size_t)h * nch + c) * (HD + 2) + 2 + d] =
+            ((s_o[0][d] + s_o[1][d]) + s_o[2][d]) + s_o[3][d];
+}
+
+// Combines the chunks of head blockIdx.x: m = max m_c,
+// out = sum_c o_c e^(m_c - m) / sum_c l_c e^(m_c - m).
+template <int HD>
+__global__ __launch_bounds__(HD) void k_attn_decode_combine(const float *__restrict__ part,
+                                                            int nch, float *__restrict__ out) {
+    const int h = blockIdx.x, d = threadIdx.x;
+    const float *ph = part + (size_t)h * nch * (HD + 2);
+    float m = -INFINITY;
+    for (int c = 0; c < nch; ++c) m = fmaxf(m, ph[c * (HD + 2)]);
+    float l = 0.0f, o = 0.0f;
+    for (int c = 0; c < nch; ++c) {
+        const float f = expf(ph[c * (HD + 2)] - m);
+        l = l + ph[c * (HD + 2) + 1] * f;
+        o = o + ph[c * (HD + 2) + 2 + d] * f;
+    }
+    out[(size_t)h * HD + d] = o / l;
 }
 
 // ---- SwiGLU (ops/activation/swiglu.rs): out = gate / (1 + exp(-gate)) * up ----
@@ -230,6 +413,20 @@ __global__ __launch_bounds__(256) void k_swiglu(const float *__restrict__ gate,
         out[i] = s * up[i];
     }
 }
+// The same, 4 elements per thread (n % 4 == 0, 16-byte aligned rows).
+__global__ __launch_bounds__(256) void k_swiglu4(const float4 *__restrict__ gate,
+                                                 const float4 *__restrict__ up, size_t n4,
+                                                 float4 *__restrict__ out) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
+        const float4 g = gate[i], u = up[i];
+        float4 o;
+        o.x = g.x / (1.0f + expf(-g.x)) * u.x;
+        o.y = g.y / (1.0f + expf(-g.y)) * u.y;
+        o.z = g.z / (1.0f + expf(-g.z)) * u.z;
+        o.w = g.w / (1.0f + expf(-g.w)) * u.w;
+        out[i] = o;
+    }
+}
 
 // ---- residual add (forward_int8.rs:100-121): out = a + b -------------------------------
 __global__ __launch_bounds__(256) void k_add(const float *__restrict__ a,
@@ -237,6 +434,14 @@ __global__ __launch_bounds__(256) void k_add(const float *__restrict__ a,
                                              float *__restrict__ out) {
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
         out[i] = a[i] + b[i];
+}
+__global__ __launch_bounds__(256) void k_add4(const float4 *__restrict__ a,
+                                              const float4 *__restrict__ b, size_t n4,
+                                              float4 *__restrict__ out) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
+        const float4 x = a[i], y = b[i];
+        out[i] = float4{x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w};
+    }
 }
 
 // ---- greedy argmax (sampling/mod.rs:144-151) ----------------------------------------
@@ -249,10 +454,20 @@ __global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ v, in
     const float *row = v + (size_t)blockIdx.x * n;
     float bv = -INFINITY;
     int bi = -1;
-    for (int i = threadIdx.x; i < n; i += 1024) {
-        const float x = row[i];
-        if (bi < 0 || x >= bv) {
-            if (!(x != x)) {
+    // 8 loads in flight per thread; within a thread indices only grow, so
+    // ">=" keeps the last of equal values
+    for (int i0 = threadIdx.x; i0 < n; i0 += 8 * 1024) {
+        float xs[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int i = i0 + u * 1024;
+            xs[u] = i < n ? row[i] : -INFINITY;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int i = i0 + u * 1024;
+            const float x = xs[u];
+            if (i < n && !(x != x) && (bi < 0 || x >= bv)) {
                 bv = x;
                 bi = i;
             }
@@ -285,10 +500,10 @@ __global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ v, in
     }
 }
 
-// query rows per attention workgroup: the largest of 16, 4, 1 whose LDS fits
+// query rows per prefill workgroup: 16, else 4 when the weight rows do not fit
 template <int HD, int QB>
 size_t attn_lds(int lcap) {
-    return (size_t)(QB * HD + (size_t)QB * lcap + 4 * QB * HD) * sizeof(float);
+    return (size_t)(QB * HD + attn_tile_floats<HD>() + (size_t)QB * lcap) * sizeof(float);
 }
 
 template <int HD, int QB>
@@ -314,17 +529,26 @@ mri_status attn_launch(const float *q, int qd, const float *kc, const float *vc,
 template <int HD>
 mri_status attn_dispatch(const float *q, int qd, const float *kc, const float *vc, int kvd,
                          int seq_q, int start_pos, int groups, int n_heads, float *out,
-                         hipStream_t s) {
-    const int lcap = (start_pos + seq_q + 3) / 4 * 4;
+                         float *part, hipStream_t s) {
+    const int L = start_pos + seq_q;
+    if (seq_q == 1 && part) {
+        const int nch = (L + 63) / 64;
+        const float scale = 1.0f / sqrtf((float)HD);
+        hipLaunchKernelGGL(k_attn_decode_part<HD>, dim3(nch, n_heads), dim3(256), 0, s, q, kc,
+                           vc, kvd, L, groups, scale, part);
+        MRI_LAUNCHED("k_attn_decode_part");
+        hipLaunchKernelGGL(k_attn_decode_combine<HD>, dim3(n_heads), dim3(HD), 0, s, part, nch,
+                           out);
+        MRI_LAUNCHED("k_attn_decode_combine");
+        return MRI_OK;
+    }
+    const int lcap = (L + 3) / 4 * 4;
     constexpr size_t kMax = 160 * 1024;
-    if (seq_q > 1 && attn_lds<HD, 16>(lcap) <= kMax)
+    if (attn_lds<HD, 16>(lcap) <= kMax)
         return attn_launch<HD, 16>(q, qd, kc, vc, kvd, seq_q, start_pos, groups, n_heads, out,
                                    s);
-    if (seq_q > 1 && attn_lds<HD, 4>(lcap) <= kMax)
+    if (attn_lds<HD, 4>(lcap) <= kMax)
         return attn_launch<HD, 4>(q, qd, kc, vc, kvd, seq_q, start_pos, groups, n_heads, out,
-                                  s);
-    if (attn_lds<HD, 1>(lcap) <= kMax)
-        return attn_launch<HD, 1>(q, qd, kc, vc, kvd, seq_q, start_pos, groups, n_heads, out,
                                   s);
     return set_error(MRI_ERR_UNSUPPORTED, "attention: context too long for one workgroup");
 }
@@ -336,10 +560,16 @@ inline unsigned grid_for(size_t n) {
 
 }  // namespace
 
+inline bool al16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
 mri_status launch_embed(const float *table, const uint32_t *tokens, size_t rows, size_t d,
                         float *x, hipStream_t s) {
     if (!rows) return MRI_OK;
-    hipLaunchKernelGGL(k_embed, dim3((unsigned)rows), dim3(256), 0, s, table, tokens, (int)d, x);
+    const dim3 grid((unsigned)rows, (unsigned)((d + 1023) / 1024));
+    if (d % 4 == 0 && al16(table) && al16(x))
+        hipLaunchKernelGGL(k_embed<true>, grid, dim3(256), 0, s, table, tokens, (int)d, x);
+    else
+        hipLaunchKernelGGL(k_embed<false>, grid, dim3(256), 0, s, table, tokens, (int)d, x);
     MRI_LAUNCHED("k_embed");
     return MRI_OK;
 }
@@ -347,49 +577,79 @@ mri_status launch_embed(const float *table, const uint32_t *tokens, size_t rows,
 mri_status launch_rmsnorm(const float *x, const float *w, size_t rows, size_t d, float eps,
                           float *out, hipStream_t s) {
     if (!rows) return MRI_OK;
-    hipLaunchKernelGGL(k_rmsnorm, dim3((unsigned)rows), dim3(256), 0, s, x, w, (int)d, eps, out);
+    const dim3 g((unsigned)rows), b(256);
+    const bool v4 = d % 4 == 0 && al16(x) && al16(w) && al16(out);
+    if (v4 && d <= 1024)
+        hipLaunchKernelGGL(k_rmsnorm<1>, g, b, 0, s, x, w, (int)d, eps, out);
+    else if (v4 && d <= 2048)
+        hipLaunchKernelGGL(k_rmsnorm<2>, g, b, 0, s, x, w, (int)d, eps, out);
+    else if (v4 && d <= 4096)
+        hipLaunchKernelGGL(k_rmsnorm<4>, g, b, 0, s, x, w, (int)d, eps, out);
+    else if (v4 && d <= 8192)
+        hipLaunchKernelGGL(k_rmsnorm<8>, g, b, 0, s, x, w, (int)d, eps, out);
+    else
+        hipLaunchKernelGGL(k_rmsnorm<0>, g, b, 0, s, x, w, (int)d, eps, out);
     MRI_LAUNCHED("k_rmsnorm");
     return MRI_OK;
 }
 
-mri_status launch_rope_qkv(float *q, const float *k, const float *v, size_t seq, size_t qd,
-                           size_t kvd, size_t head_dim, const float *cos_t, const float *sin_t,
+mri_status launch_rope_qkv(float *q, const float *k, const float *v, size_t seq, size_t n_heads,
+                           size_t n_kv, size_t head_dim, const float *cos_t, const float *sin_t,
                            size_t start_pos, float *kc, float *vc, hipStream_t s) {
     if (!seq) return MRI_OK;
-    hipLaunchKernelGGL(k_rope_qkv, dim3((unsigned)seq), dim3(256), 0, s, q, k, v, (int)qd,
-                       (int)kvd, (int)(head_dim / 2), cos_t, sin_t, (int)start_pos, kc, vc);
+    if (head_dim % 2 || head_dim > 128)
+        return set_error(MRI_ERR_UNSUPPORTED, "rope: head_dim must be even and <= 128");
+    const int qd = (int)(n_heads * head_dim), kvd = (int)(n_kv * head_dim);
+    hipLaunchKernelGGL(k_rope_qkv, dim3((unsigned)seq, (unsigned)(n_heads + 2 * n_kv)), dim3(64),
+                       0, s, q, k, v, qd, kvd, (int)(head_dim / 2), (int)n_heads, (int)n_kv,
+                       cos_t, sin_t, (int)start_pos, kc, vc);
     MRI_LAUNCHED("k_rope_qkv");
     return MRI_OK;
 }
 
 bool attention_supported(size_t head_dim) { return head_dim == 64 || head_dim == 128; }
 
+size_t attention_part_floats(size_t n_heads, size_t head_dim, size_t max_seq) {
+    return n_heads * ((max_seq + 63) / 64) * (head_dim + 2);
+}
+
 mri_status launch_attention(const float *q, size_t seq_q, const float *kc, const float *vc,
                             size_t n_heads, size_t n_kv_heads, size_t head_dim,
-                            size_t start_pos, float *out, hipStream_t s) {
+                            size_t start_pos, float *out, float *part, hipStream_t s) {
     if (!seq_q) return MRI_OK;
     const int qd = (int)(n_heads * head_dim), kvd = (int)(n_kv_heads * head_dim);
     const int groups = (int)(n_heads / n_kv_heads);
     if (head_dim == 128)
         return attn_dispatch<128>(q, qd, kc, vc, kvd, (int)seq_q, (int)start_pos, groups,
-                                  (int)n_heads, out, s);
+                                  (int)n_heads, out, part, s);
     if (head_dim == 64)
         return attn_dispatch<64>(q, qd, kc, vc, kvd, (int)seq_q, (int)start_pos, groups,
-                                 (int)n_heads, out, s);
+                                 (int)n_heads, out, part, s);
     return set_error(MRI_ERR_UNSUPPORTED, "attention: head_dim must be 64 or 128");
 }
 
 mri_status launch_swiglu(const float *gate, const float *up, size_t n, float *out,
                          hipStream_t s) {
     if (!n) return MRI_OK;
-    hipLaunchKernelGGL(k_swiglu, dim3(grid_for(n)), dim3(256), 0, s, gate, up, n, out);
+    if (n % 4 == 0 && al16(gate) && al16(up) && al16(out))
+        hipLaunchKernelGGL(k_swiglu4, dim3(grid_for(n / 4)), dim3(256), 0, s,
+                           reinterpret_cast<const float4 *>(gate),
+                           reinterpret_cast<const float4 *>(up), n / 4,
+                           reinterpret_cast<float4 *>(out));
+    else
+        hipLaunchKernelGGL(k_swiglu, dim3(grid_for(n)), dim3(256), 0, s, gate, up, n, out);
     MRI_LAUNCHED("k_swiglu");
     return MRI_OK;
 }
 
 mri_status launch_add(const float *a, const float *b, size_t n, float *out, hipStream_t s) {
     if (!n) return MRI_OK;
-    hipLaunchKernelGGL(k_add, dim3(grid_for(n)), dim3(256), 0, s, a, b, n, out);
+    if (n % 4 == 0 && al16(a) && al16(b) && al16(out))
+        hipLaunchKernelGGL(k_add4, dim3(grid_for(n / 4)), dim3(256), 0, s,
+                           reinterpret_cast<const float4 *>(a), reinterpret_cast<const float4 *>(b),
+                           n / 4, reinterpret_cast<float4 *>(out));
+    else
+        hipLaunchKernelGGL(k_add, dim3(grid_for(n)), dim3(256), 0, s, a, b, n, out);
     MRI_LAUNCHED("k_add");
     return MRI_OK;
 }

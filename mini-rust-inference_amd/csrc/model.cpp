@@ -44,6 +44,7 @@ struct mri_llama {
           *v = nullptr, *attn = nullptr, *gate = nullptr, *up = nullptr;
     uint32_t *tok = nullptr;      // prompt ids [max_seq]
     uint32_t *gen = nullptr;      // generated ids [max_seq + 1]
+    float *attn_part = nullptr;   // split-key decode attention partials
     float *logits_buf = nullptr;  // prefill logits for generation, grown on demand
     size_t logits_rows = 0;
     std::vector<void *> allocs;
@@ -142,9 +143,10 @@ mri_status block(mri_llama *m, size_t li, size_t rows, size_t start, mri_kv_cach
     TRY(proj(L.w[0], m->normed, rows, m->q, s));
     TRY(proj(L.w[1], m->normed, rows, m->k, s));
     TRY(proj(L.w[2], m->normed, rows, m->v, s));
-    TRY(launch_rope_qkv(m->q, m->k, m->v, rows, m->qd, m->kvd, m->hd, m->cos_t, m->sin_t, start,
-                        kc, vc, s));
-    TRY(launch_attention(m->q, rows, kc, vc, g.n_heads, g.n_kv_heads, m->hd, start, m->attn, s));
+    TRY(launch_rope_qkv(m->q, m->k, m->v, rows, g.n_heads, g.n_kv_heads, m->hd, m->cos_t,
+                        m->sin_t, start, kc, vc, s));
+    TRY(launch_attention(m->q, rows, kc, vc, g.n_heads, g.n_kv_heads, m->hd, start, m->attn,
+                         m->attn_part, s));
     TRY(proj(L.w[3], m->attn, rows, m->tmp, s));
     TRY(launch_add(m->x, m->tmp, rows * g.dim, m->x, s));
     TRY(launch_rmsnorm(m->x, L.ffn_norm, rows, g.dim, g.eps, m->normed, s));
@@ -232,7 +234,8 @@ mri_status mri_llama_create(const mri_llama_config *cfg, const float *token_embd
         (st = dalloc_t(m, R * m->kvd, &m->k)) || (st = dalloc_t(m, R * m->kvd, &m->v)) ||
         (st = dalloc_t(m, R * m->qd, &m->attn)) || (st = dalloc_t(m, R * g.ffn_dim, &m->gate)) ||
         (st = dalloc_t(m, R * g.ffn_dim, &m->up)) || (st = dalloc_t(m, R, &m->tok)) ||
-        (st = dalloc_t(m, R + 1, &m->gen)))
+        (st = dalloc_t(m, R + 1, &m->gen)) ||
+        (st = dalloc_t(m, attention_part_floats(g.n_heads, hd, R), &m->attn_part)))
         return fail(st);
     // RopeTable::new (ops/rope.rs): theta_i = 1 / base^(2i / head_dim) and
     // angle = pos * theta_i in f32, with the C library's powf / cosf / sinf.
