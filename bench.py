@@ -26,6 +26,13 @@ f32, the Q4_0 W4A32 decode GEMV, and the reference's rayon+AVX2
 matmul_int8_parallel restatement on the INT8 decode shape (one core, as
 the reference: one row) and on a bounded row sample of the prefill shape
 (all cores).
+
+Decoder layer (the 7B-dims LlamaModelInt8 configuration): one random-init
+layer (hidden 4096, 32 heads of 128, SwiGLU 11008, RMSNorm eps 1e-6, RoPE
+base 10000) with the output head (vocab 32000), Q8_0 weights (and per-channel
+INT8, the reference model's own format): a 512-token prefill
+(forward_cached) and 128 greedy decode steps (generate_greedy, token ids
+kept on the device), seeded random prompt ids.
 """
 import argparse
 import json
@@ -172,6 +179,88 @@ def bench_int8_prefill(torch, M, T, m, n, k, steps, warmup, seed=7):
                             nrot)
     ms_f32 = T.per_call_ms(lambda i: M.matmul_int8_from_f32(x, ws[i], out), steps, warmup, nrot)
     return ms_rows, ms_f32
+
+
+LAYER = dict(dim=4096, n_heads=32, n_kv_heads=32, ffn=11008, vocab=32000, eps=1e-6,
+             rope_base=10000.0)
+
+
+def layer_decode_bytes(fmt, ctx):
+    """Weight bytes read per decode token (7 projections + output head) plus
+    the K and V cache rows read by attention at context length ctx."""
+    d, f, v = LAYER["dim"], LAYER["ffn"], LAYER["vocab"]
+    shapes = [(d, d)] * 4 + [(f, d)] * 2 + [(d, f), (v, d)]
+    if fmt == "q8_0":
+        w = sum(n * (k // 32) * 34 for n, k in shapes)
+    else:
+        w = sum(n * k + 4 * n for n, k in shapes)
+    return w + 2 * ctx * d * 4
+
+
+def bench_layer(torch, M, fmt, n_prompt=512, n_steps=128, seed=21):
+    """Returns a dict of the decoder-layer figures for weight format fmt."""
+    import numpy as np
+    import mri_llama as L
+    c = dict(LAYER, max_seq=n_prompt + n_steps)
+    d, f, v = c["dim"], c["ffn"], c["vocab"]
+    rng = np.random.default_rng(seed)
+    sd = [seed]
+
+    def w(n, k):
+        sd[0] += 1
+        if fmt == "q8_0":
+            g = torch.Generator(device="cuda").manual_seed(sd[0])
+            nb = k // 32
+            q = torch.randint(-127, 128, (n, nb, 32), dtype=torch.int8, device="cuda",
+                              generator=g)
+            dd = (torch.rand((n, nb), device="cuda", generator=g) * 0.0018 + 0.0002).half()
+            raw = torch.empty((n, nb, 34), dtype=torch.uint8, device="cuda")
+            raw[:, :, 0:2] = dd.view(torch.uint8).view(n, nb, 2)
+            raw[:, :, 2:] = q.view(torch.uint8)
+            return M.Q8Matrix.from_raw_device(raw.view(-1), n, k)
+        data, scales = int8_weights_device(torch, M, n, k, sd[0])
+        return M.QMatrix.from_device(data, scales)
+
+    layer = dict(attn_norm=np.ones(d, np.float32), ffn_norm=np.ones(d, np.float32),
+                 wq=w(d, d), wk=w(d, d), wv=w(d, d), wo=w(d, d), wgate=w(f, d), wup=w(f, d),
+                 wdown=w(d, f))
+    emb = rng.standard_normal((v, d), dtype=np.float32)
+    model = L.Llama(c, emb, np.ones(d, np.float32), w(v, d), [layer])
+    del emb
+    cache = model.kv_cache()
+    prompt = rng.integers(0, v, n_prompt).tolist()
+    logits = torch.empty((n_prompt, v), device="cuda")
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+    model.forward_cached(prompt, 0, cache, logits)  # warm (workspaces, code objects)
+    model.generate_greedy(prompt, 8, cache)
+    pre = []
+    for _ in range(3):
+        e0, e1 = ev(), ev()
+        e0.record()
+        model.forward_cached(prompt, 0, cache, logits)
+        e1.record()
+        torch.cuda.synchronize()
+        pre.append(e0.elapsed_time(e1))
+    gen = []
+    for _ in range(2):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        toks = model.generate_greedy(prompt, n_steps, cache)
+        gen.append((time.perf_counter() - t0) * 1e3)
+    assert int(toks.max()) < v
+    pre_ms, gen_ms = min(pre), min(gen)
+    dec_us = (gen_ms - pre_ms) / n_steps * 1e3
+    nbytes = layer_decode_bytes(fmt, n_prompt + n_steps // 2)
+    gbs = nbytes / (dec_us * 1e-6) / 1e9
+    model.close()
+    return {"prefill_512_ms": round(pre_ms, 3),
+            "prefill_tokens_per_s": round(n_prompt / (pre_ms * 1e-3), 1),
+            "decode_us_per_token": round(dec_us, 2),
+            "decode_tokens_per_s": round(1e6 / dec_us, 1),
+            "generate_512_plus_128_ms": round(gen_ms, 3),
+            "decode_bytes_per_token": nbytes,
+            "decode_GB_s": round(gbs, 1), "decode_frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "first_tokens": [int(t) for t in toks[:4]]}
 
 
 def cpu_q8_direct(raw_np, x_np, n, k, budget_s):
@@ -321,6 +410,13 @@ def main():
             "us": round(ms_q4 * 1e3, 2), "GB_s": round(gbs, 1),
             "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
         log(f"q4_0 decode: {ms_q4*1e3:.2f} us {gbs:.0f} GB/s")
+
+        layer = {}
+        for fmt in ("q8_0", "int8"):
+            layer[fmt] = bench_layer(torch, M, fmt)
+            log(f"decoder layer {fmt}: prefill 512 {layer[fmt]['prefill_512_ms']:.2f} ms, "
+                f"decode {layer[fmt]['decode_us_per_token']:.1f} us/token")
+        secondary["decoder_layer_7b_512_plus_128"] = layer
 
         if not args.no_cpu:
             wq, sc = wq_d.cpu().numpy(), sc_d.cpu().numpy()

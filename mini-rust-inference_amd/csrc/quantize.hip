@@ -226,8 +226,9 @@ __global__ __launch_bounds__(kThreads) void k_dot_i8(
 // returns its row and first k.
 __device__ inline void pack_piece(size_t e, size_t mg, size_t *row, size_t *k0) {
     const size_t lane = e & 63, t = e >> 6;
-    const size_t h = t & 1, t2 = t >> 1;
-    const size_t g = t2 % mg, p = t2 / mg;
+    const size_t h = t & 1;
+    const unsigned t2 = (unsigned)(t >> 1), mgu = (unsigned)mg;  // 32-bit: t2 < pieces / 128
+    const size_t g = t2 % mgu, p = t2 / mgu;
     *row = 32 * g + (lane & 31);
     *k0 = 64 * p + 32 * h + 16 * (lane >> 5);
 }
@@ -249,15 +250,41 @@ __global__ __launch_bounds__(kThreads) void k_quantize_pack(
     if (blockIdx.x == 0 && threadIdx.x == 0 && scale_out) *scale_out = scale;
     const size_t pieces = mg * 32 * kp / 16;
     const size_t stride = (size_t)gridDim.x * blockDim.x;
+    // whole 16-element pieces of rows with k % 4 == 0 (16-byte aligned x):
+    // four float4 loads; a plain int8 copy as one 16-byte store when its
+    // rows are 16-byte aligned too
+    const bool v4 = k % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+    const bool p16 = k % 16 == 0 && (reinterpret_cast<uintptr_t>(q_plain) & 15) == 0;
     for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < pieces; e += stride) {
         size_t r, k0;
         pack_piece(e, mg, &r, &k0);
         int8_t q[16];
+        if (v4 && r < m && k0 + 16 <= k) {
+            const float4 *src = reinterpret_cast<const float4 *>(x + r * k + k0);
+            float4 f[4];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const size_t kk = k0 + j;
-            q[j] = (r < m && kk < k) ? round_clamp_i8(x[r * k + kk] * inv) : (int8_t)0;
-            if (q_plain && r < m && kk < k) q_plain[r * k + kk] = q[j];
+            for (int u = 0; u < 4; ++u) f[u] = src[u];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                q[4 * u + 0] = round_clamp_i8(f[u].x * inv);
+                q[4 * u + 1] = round_clamp_i8(f[u].y * inv);
+                q[4 * u + 2] = round_clamp_i8(f[u].z * inv);
+                q[4 * u + 3] = round_clamp_i8(f[u].w * inv);
+            }
+            if (q_plain) {
+                if (p16)
+                    *reinterpret_cast<int4 *>(q_plain + r * k + k0) =
+                        *reinterpret_cast<const int4 *>(q);
+                else
+                    for (int j = 0; j < 16; ++j) q_plain[r * k + k0 + j] = q[j];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const size_t kk = k0 + j;
+                q[j] = (r < m && kk < k) ? round_clamp_i8(x[r * k + kk] * inv) : (int8_t)0;
+                if (q_plain && r < m && kk < k) q_plain[r * k + kk] = q[j];
+            }
         }
         *reinterpret_cast<int4 *>(packed + e * 16) = *reinterpret_cast<const int4 *>(q);
     }
@@ -269,16 +296,24 @@ __global__ __launch_bounds__(kThreads) void k_pack_gemm(
     int8_t *__restrict__ packed) {
     const size_t pieces = mg * 32 * kp / 16;
     const size_t stride = (size_t)gridDim.x * blockDim.x;
+    // whole pieces of 16-byte aligned rows move as one 16-byte load
+    const bool v16 = ld % 16 == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0;
     for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < pieces; e += stride) {
         size_t r, k0;
         pack_piece(e, mg, &r, &k0);
-        int8_t q[16];
+        int4 v;
+        if (v16 && r < m && k0 + 16 <= k) {
+            v = *reinterpret_cast<const int4 *>(src + r * ld + k0);
+        } else {
+            int8_t q[16];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const size_t kk = k0 + j;
-            q[j] = (r < m && kk < k) ? src[r * ld + kk] : (int8_t)0;
+            for (int j = 0; j < 16; ++j) {
+                const size_t kk = k0 + j;
+                q[j] = (r < m && kk < k) ? src[r * ld + kk] : (int8_t)0;
+            }
+            v = *reinterpret_cast<const int4 *>(q);
         }
-        *reinterpret_cast<int4 *>(packed + e * 16) = *reinterpret_cast<const int4 *>(q);
+        *reinterpret_cast<int4 *>(packed + e * 16) = v;
     }
 }
 
