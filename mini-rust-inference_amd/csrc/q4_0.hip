@@ -9,10 +9,23 @@
 // which differs from the sequential sum only by rounding (the documented
 // 1e-5 * max(|ref|, sum|terms|) contract).
 //
-// Mapping: one wave per weight row, two lanes per block (8 quant bytes =
-// 16 elements each); a step covers 32 blocks, so K = 4096 takes 4 steps.
-// Raw blocks are 18 bytes (2-byte aligned), so the row is read with 16-bit
-// loads; the loads of consecutive lanes are contiguous.
+// Two forms.
+//
+// k_q4_0_lds (16-byte aligned weights, K % 256 == 0, so that every row
+// starts on 16 bytes; M <= 4): a workgroup takes R consecutive weight rows,
+// one contiguous byte range, and moves them to LDS with 16-byte loads (all
+// in flight at once); the activations are read from L2.  Lane l of a step
+// covers elements 8*(l%4) .. +8 of block l/4 (4 quant
+// bytes: low nibble = even element): it reads its 8 activations once and
+// applies them to each of the wave's R/4 rows as d * (sum x*nib - 8 * sum x)
+// (the regrouping below; the activation sum is shared by the rows).  Lane
+// partials are added by a wave reduction.
+//
+// k_q4_0_dequant (any 2-byte aligned layout): one wave per weight row, two
+// lanes per block (8 quant bytes = 16 elements each), with the sum regrouped
+// per block as sum_b d_b * (sum_e x_e * nib_e - 8 * sum_e x_e).
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace mri {
@@ -89,12 +102,123 @@ __global__ __launch_bounds__(kThreads) void k_q4_0_dequant(
     }
 }
 
+template <int R>
+__global__ __launch_bounds__(kThreads) void k_q4_0_lds(const float *__restrict__ x, int M, int K,
+                                                       const uint8_t *__restrict__ w, int N,
+                                                       float *__restrict__ out) {
+    constexpr int RW = R / 4;  // rows per wave
+    extern __shared__ int4 s_raw[];
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    const int nb = K / 32, row_bytes = nb * kQ4Bytes;
+    const int n0 = blockIdx.x * R, rows = min(R, N - n0);
+    const uint8_t *s_w = reinterpret_cast<const uint8_t *>(s_raw);
+    {
+        // every load in flight before the first store (at most 12 pieces a
+        // thread: the launcher keeps R rows within 48 KiB)
+        const int4 *src = reinterpret_cast<const int4 *>(w + (size_t)n0 * row_bytes);
+        const int n16 = rows * row_bytes / 16;
+        int4 v[12];
+#pragma unroll
+        for (int u = 0; u < 12; ++u) v[u] = src[min(t + kThreads * u, n16 - 1)];  // n16 >= 1
+#pragma unroll
+        for (int u = 0; u < 12; ++u) {
+            const int i = t + kThreads * u;
+            if (i < n16) s_raw[i] = v[u];
+        }
+    }
+    __syncthreads();
+    const int steps = (nb * 4 + 63) / 64;
+    // rows past `rows` read stale LDS and are never stored
+    for (int m = 0; m < M; ++m) {
+        const float *xm = x + (size_t)m * K;
+        float acc[RW];
+#pragma unroll
+        for (int r = 0; r < RW; ++r) acc[r] = 0.0f;
+        for (int st = 0; st < steps; ++st) {
+            const int idx = st * 64 + lane, p = idx & 3;
+            const bool ok = (idx >> 2) < nb;
+            const int b = ok ? idx >> 2 : nb - 1;
+            const float4 *xv = reinterpret_cast<const float4 *>(xm + 32 * b + 8 * p);
+            float4 xa = xv[0], xb = xv[1];
+            if (!ok) xa = xb = float4{0, 0, 0, 0};
+            float dq[RW];
+            unsigned lo[RW], hi[RW];
+#pragma unroll
+            for (int r = 0; r < RW; ++r) {
+                const uint8_t *blk = s_w + (size_t)(wv * RW + r) * row_bytes + b * kQ4Bytes;
+                dq[r] = f16_bits_to_f32(*reinterpret_cast<const uint16_t *>(blk));
+                const unsigned q =
+                    (unsigned)*reinterpret_cast<const uint16_t *>(blk + 2 + 4 * p) |
+                    ((unsigned)*reinterpret_cast<const uint16_t *>(blk + 4 + 4 * p) << 16);
+                lo[r] = q & 0x0F0F0F0Fu;          // elements 0, 2, 4, 6 (low nibbles)
+                hi[r] = (q >> 4) & 0x0F0F0F0Fu;   // elements 1, 3, 5, 7
+            }
+            // d * sum_e x_e * (nib_e - 8) = d * (sum_e x_e * nib_e - 8 * sum_e x_e);
+            // the activation sum is shared by the wave's rows, and the rows'
+            // chains are interleaved
+            const float xs = ((xa.x + xa.y) + (xa.z + xa.w)) + ((xb.x + xb.y) + (xb.z + xb.w));
+            float sn[RW];
+#pragma unroll
+            for (int r = 0; r < RW; ++r) sn[r] = xa.x * (float)(lo[r] & 0xFF);
+#pragma unroll
+            for (int r = 0; r < RW; ++r) sn[r] = fmaf(xa.y, (float)(hi[r] & 0xFF), sn[r]);
+#pragma unroll
+            for (int r = 0; r < RW; ++r) sn[r] = fmaf(xa.z, (float)((lo[r] >> 8) & 0xFF), sn[r]);
+#pragma unroll
+            for (int r = 0; r < RW; ++r) sn[r] = fmaf(xa.w, (float)((hi[r] >> 8) & 0xFF), sn[r]);
+#pragma unroll
+            for (int r = 0; r < RW; ++r) sn[r] = fmaf(xb.x, (float)((lo[r] >> 16) & 0xFF), sn[r]);
+#pragma unroll
+            for (int r = 0; r < RW; ++r) sn[r] = fmaf(xb.y, (float)((hi[r] >> 16) & 0xFF), sn[r]);
+#pragma unroll
+            for (int r = 0; r < RW; ++r) sn[r] = fmaf(xb.z, (float)(lo[r] >> 24), sn[r]);
+#pragma unroll
+            for (int r = 0; r < RW; ++r) sn[r] = fmaf(xb.w, (float)(hi[r] >> 24), sn[r]);
+#pragma unroll
+            for (int r = 0; r < RW; ++r) acc[r] = fmaf(dq[r], fmaf(-8.0f, xs, sn[r]), acc[r]);
+        }
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+            float v = acc[r];
+            for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+            const int row = wv * RW + r;
+            if (lane == 0 && row < rows) out[(size_t)m * N + n0 + row] = v;
+        }
+    }
+}
+
+size_t q4_lds_bytes(int r, size_t k) { return (size_t)r * (k / 32) * kQ4Bytes; }
+
+template <int R>
+mri_status launch_lds(const float *x, size_t m, size_t k, const uint8_t *w, size_t n_out,
+                      float *out, hipStream_t s) {
+    static bool attr_set = false;
+    if (!attr_set) {
+        MRI_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_q4_0_lds<R>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+        attr_set = true;
+    }
+    hipLaunchKernelGGL(k_q4_0_lds<R>, dim3((unsigned)((n_out + R - 1) / R)), dim3(kThreads),
+                       q4_lds_bytes(R, k), s, x, (int)m, (int)k, w, (int)n_out, out);
+    MRI_LAUNCHED("k_q4_0_lds");
+    return MRI_OK;
+}
+
 }  // namespace
 
 mri_status launch_q4_0_dequant(const float *x, size_t m, size_t k,
                                const uint8_t *w, size_t n_out, float *out,
                                hipStream_t s) {
     if (m == 0 || n_out == 0) return MRI_OK;
+    // the staged form: 16-byte aligned rows (K % 256 == 0) and operands, and
+    // at most 64 KiB of LDS per workgroup (several workgroups per CU)
+    const bool al = ((uintptr_t)w & 15) == 0 && ((uintptr_t)x & 15) == 0 && k % 256 == 0;
+    if (al && m <= 4 && k <= (1u << 16) && n_out <= (1u << 30)) {
+        // rows per workgroup: 16, 8 or 4, as ~40 KiB of LDS allows
+        if (q4_lds_bytes(16, k) <= 40 * 1024) return launch_lds<16>(x, m, k, w, n_out, out, s);
+        if (q4_lds_bytes(8, k) <= 40 * 1024) return launch_lds<8>(x, m, k, w, n_out, out, s);
+        if (q4_lds_bytes(4, k) <= 48 * 1024) return launch_lds<4>(x, m, k, w, n_out, out, s);
+    }
     const size_t waves = (n_out + kRowsPerWave - 1) / kRowsPerWave;
     size_t grid = (waves + (kThreads / 64) - 1) / (kThreads / 64);
     if (grid < 1) grid = 1;

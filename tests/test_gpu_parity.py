@@ -273,7 +273,9 @@ def test_q8_0_reference_encoder_weights():
 # ---- Q4_0 ----------------------------------------------------------------------------
 
 @pytest.mark.parametrize("m,n,k", [(1, 16, 32), (1, 300, 4096), (3, 20, 96),
-                                   (2, 64, 11008), (5, 7, 64)])
+                                   (2, 64, 11008), (5, 7, 64), (1, 11008, 4096),
+                                   (3, 4096, 11008), (2, 37, 512), (4, 21, 256),
+                                   (1, 1000, 32768)])
 def test_matmul_q4_0_dequant_tolerance(m, n, k):
     say(f"matmul_q4_0 m={m} n={n} k={k}")
     t = torch()
@@ -287,6 +289,12 @@ def test_matmul_q4_0_dequant_tolerance(m, n, k):
     scale = np.maximum(np.abs(out0), CF.q4_0_terms_abs_sum(x, raw, n, k))
     err = np.abs(got.astype(np.float64) - out0)
     assert np.all(err <= 1e-5 * scale), float(np.max(err / scale))
+    if k % 256 == 0 and m > 1:  # the staged form from a 16-byte aligned, unaligned-row x
+        xo = torch().zeros(m * k + 1, dtype=t.float32, device="cuda")
+        xo[1:] = dev(x).view(-1)
+        out2 = empty((m, n), t.float32)
+        mri().matmul_q4_0_dequant(xo[1:], dev(raw), n, k, out2, shape=(m, k))
+        assert np.array_equal(host(out2), got)
 
 
 # ---- error behaviour (TensorError kinds and order) ------------------------------------
