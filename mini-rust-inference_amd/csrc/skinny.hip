@@ -154,8 +154,13 @@ __global__ __launch_bounds__(TPW * kWave) void k_skinny_q8_0(
     int32_t *__restrict__ block_dots, int ns) {
     // wave -> (tile, set of AG activation groups); the ns waves of a tile are
     // adjacent, so they share a workgroup (or neighbouring ones) and the
-    // weight chunks they all stream are fetched from HBM once
-    const int wv = blockIdx.x * TPW + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // weight chunks they all stream are fetched from HBM once.  With several
+    // workgroups per tile the grid (a multiple of 8) is taken XCD-major:
+    // workgroups are dispatched to the 8 XCDs round-robin, and consecutive
+    // indices of one XCD share its L2.
+    int blk = blockIdx.x;
+    if (ns > TPW) blk = (int)(blockIdx.x % 8) * (int)(gridDim.x / 8) + (int)(blockIdx.x / 8);
+    const int wv = blk * TPW + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int T = wv / ns;
     const int a0 = (wv - T * ns) * AG;  // first activation group of the wave
     if (T >= n_tiles) return;  // whole waves only; the kernel has no barrier
@@ -286,8 +291,10 @@ void launch_q8(const int8_t *act, size_t m, size_t kp, const float *sa_rows,
                const Q8MatrixDev &w, float *out, int32_t *block_dots, int ns, hipStream_t s) {
     const int G = (int)(((w.n_blocks + 1) / 2 + 3) / 4);  // laps holding real blocks
     const size_t waves = w.n_tiles * (size_t)ns;
+    size_t grid = (waves + TPW - 1) / TPW;
+    if (ns > TPW) grid = (grid + 7) / 8 * 8;  // XCD-major mapping (whole waves past the end exit)
     hipLaunchKernelGGL((k_skinny_q8_0<AG, TPW, RL, DEBUG>),
-                       dim3((unsigned)((waves + TPW - 1) / TPW)), dim3(TPW * kWave), 0, s,
+                       dim3((unsigned)grid), dim3(TPW * kWave), 0, s,
                        act, (int)m, (int)kp, sa_rows, reinterpret_cast<const v4i *>(w.tiles),
                        reinterpret_cast<const v4i *>(w.scales), (int)w.n_out, (int)w.n_tiles, G,
                        (int)w.n_blocks, out, block_dots, ns);
@@ -320,6 +327,16 @@ mri_status launch_skinny_q8_0(const int8_t *act, size_t m,
                               hipStream_t s) {
     if (w.n_tiles == 0 || m == 0) return MRI_OK;
     const size_t kp = w.kp;
+    if (m > 32) {
+        // one launch for all rows: ceil(m/32) waves of 32 rows per weight
+        // tile, four to a workgroup; the weights stream from HBM about once
+        // instead of once per 32-row slice
+        const int ns = (int)((m + 31) / 32);
+        if (block_dots) launch_q8<2, 4, 2, true>(act, m, kp, sa_rows, w, out, block_dots, ns, s);
+        else launch_q8<2, 4, 2, false>(act, m, kp, sa_rows, w, out, block_dots, ns, s);
+        MRI_LAUNCHED("k_skinny_q8_0");
+        return MRI_OK;
+    }
     for (size_t m0 = 0; m0 < m; m0 += 32) {
         const size_t mc = m - m0 < 32 ? m - m0 : 32;
         const int8_t *a = act + m0 * kp;
