@@ -419,6 +419,91 @@ void mri_q8_0_matrix_destroy(mri_q8_0_matrix *w) {
     delete w;
 }
 
+}  // extern "C"
+
+namespace mri {
+
+// Row concatenation of weight handles with one k_in whose n_out are whole
+// tiles (multiples of 16): in the slab-major layout, slab p of the fused
+// matrix is the parts' slab p side by side, so each part is one pitched copy
+// of its tiles (and, for Q8_0, of its scale groups).  The result is a new
+// handle; the parts are not modified.
+mri_status concat_qmatrix(const mri_qmatrix *const *parts, int n, hipStream_t s,
+                          mri_qmatrix **out) {
+    *out = nullptr;
+    size_t rows = 0;
+    for (int i = 0; i < n; ++i) {
+        if (parts[i]->d.n_out % kTileN || parts[i]->d.k_in != parts[0]->d.k_in)
+            return set_error(MRI_ERR_INVALID_SHAPE, "concat: parts must be whole tiles of one K");
+        rows += parts[i]->d.n_out;
+    }
+    auto *h = new mri_qmatrix();
+    mri_status st = alloc_qmatrix(rows, parts[0]->d.k_in, h->d);
+    const size_t P = h->d.kp / kChunkK;
+    size_t t0 = 0;
+    for (int i = 0; i < n && !st; ++i) {
+        const QMatrixDev &d = parts[i]->d;
+        hipError_t e = hipMemcpy2DAsync(h->d.tiles + t0 * 1024, h->d.n_tiles * 1024, d.tiles,
+                                        d.n_tiles * 1024, d.n_tiles * 1024, P,
+                                        hipMemcpyDeviceToDevice, s);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(h->d.scales + t0 * kTileN, d.scales,
+                               d.n_tiles * kTileN * sizeof(float), hipMemcpyDeviceToDevice, s);
+        if (e != hipSuccess) st = hip_error(e, "concat_qmatrix");
+        t0 += d.n_tiles;
+    }
+    if (st) {
+        mri_qmatrix_destroy(h);
+        return st;
+    }
+    *out = h;
+    return MRI_OK;
+}
+
+mri_status concat_q8_0_matrix(const mri_q8_0_matrix *const *parts, int n, hipStream_t s,
+                              mri_q8_0_matrix **out) {
+    *out = nullptr;
+    size_t rows = 0;
+    for (int i = 0; i < n; ++i) {
+        if (parts[i]->d.n_out % kTileN || parts[i]->d.k_in != parts[0]->d.k_in)
+            return set_error(MRI_ERR_INVALID_SHAPE, "concat: parts must be whole tiles of one K");
+        rows += parts[i]->d.n_out;
+    }
+    auto *h = new mri_q8_0_matrix();
+    Q8MatrixDev &d = h->d;
+    const Q8MatrixDev &d0 = parts[0]->d;
+    d.n_out = rows;
+    d.k_in = d0.k_in;
+    d.n_blocks = d0.n_blocks;
+    d.n_tiles = rows / kTileN;
+    d.kp = d0.kp;
+    d.device = d0.device;
+    const size_t P = d.kp / kChunkK, Q = d.kp / (kQK * kQ8ScaleGroup);
+    hipError_t e = hipMalloc(&d.tiles, d.n_tiles * P * 1024 + 256);
+    if (e == hipSuccess) e = hipMalloc(&d.scales, d.n_tiles * Q * kTileN * 16 + 256);
+    size_t t0 = 0;
+    for (int i = 0; i < n && e == hipSuccess; ++i) {
+        const Q8MatrixDev &pd = parts[i]->d;
+        e = hipMemcpy2DAsync(d.tiles + t0 * 1024, d.n_tiles * 1024, pd.tiles, pd.n_tiles * 1024,
+                             pd.n_tiles * 1024, P, hipMemcpyDeviceToDevice, s);
+        if (e == hipSuccess)  // scale group q of tile T: 16 rows x 16 bytes at (q*n_tiles + T)*256
+            e = hipMemcpy2DAsync(reinterpret_cast<uint8_t *>(d.scales) + t0 * 256,
+                                 d.n_tiles * 256, pd.scales, pd.n_tiles * 256, pd.n_tiles * 256,
+                                 Q, hipMemcpyDeviceToDevice, s);
+        t0 += pd.n_tiles;
+    }
+    if (e != hipSuccess) {
+        mri_q8_0_matrix_destroy(h);
+        return hip_error(e, "concat_q8_0_matrix");
+    }
+    *out = h;
+    return MRI_OK;
+}
+
+}  // namespace mri
+
+extern "C" {
+
 // ===========================================================================
 // quantizers
 // ===========================================================================

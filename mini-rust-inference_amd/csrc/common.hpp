@@ -194,25 +194,44 @@ mri_status launch_q4_0_dequant(const float *x, size_t m, size_t k,
                                const uint8_t *w, size_t n_out, float *out,
                                hipStream_t s);
 
+// capi.cpp: row concatenation of weight handles (whole 16-row tiles, one K)
+// into a new handle, for fused projections that share their input.
+mri_status concat_qmatrix(const mri_qmatrix *const *parts, int n, hipStream_t s,
+                          mri_qmatrix **out);
+mri_status concat_q8_0_matrix(const mri_q8_0_matrix *const *parts, int n, hipStream_t s,
+                              mri_q8_0_matrix **out);
+
 // llama.hip: the decoder layer's non-matmul steps (f32 rows in HBM).
 mri_status launch_embed(const float *table, const uint32_t *tokens, size_t rows, size_t d,
                         float *x, hipStream_t s);
 mri_status launch_rmsnorm(const float *x, const float *w, size_t rows, size_t d, float eps,
                           float *out, hipStream_t s);
+// x_out = table[tokens] (rows), out = rmsnorm(x_out): one pass.
+mri_status launch_embed_rmsnorm(const float *table, const uint32_t *tokens, size_t rows,
+                                size_t d, const float *w, float eps, float *x_out, float *out,
+                                hipStream_t s);
+// x += delta, out = rmsnorm(x): one pass.
+mri_status launch_add_rmsnorm(float *x, const float *delta, size_t rows, size_t d,
+                              const float *w, float eps, float *out, hipStream_t s);
 // RoPE of q in place; rotated k and v rows into the cache at start_pos + s.
+// q_stride / kv_stride: floats between consecutive rows of q and of k, v.
 mri_status launch_rope_qkv(float *q, const float *k, const float *v, size_t seq, size_t n_heads,
-                           size_t n_kv, size_t head_dim, const float *cos_t, const float *sin_t,
-                           size_t start_pos, float *kc, float *vc, hipStream_t s);
+                           size_t n_kv, size_t head_dim, size_t q_stride, size_t kv_stride,
+                           const float *cos_t, const float *sin_t, size_t start_pos, float *kc,
+                           float *vc, hipStream_t s);
 bool attention_supported(size_t head_dim);
 // Causal GQA of seq_q query rows (positions start_pos ..) against cache rows
 // 0 .. start_pos + seq_q - 1.  part: attention_part_floats(...) floats of
 // workspace for the split-key one-row form (nullable: one workgroup per head).
 size_t attention_part_floats(size_t n_heads, size_t head_dim, size_t max_seq);
-mri_status launch_attention(const float *q, size_t seq_q, const float *kc, const float *vc,
-                            size_t n_heads, size_t n_kv_heads, size_t head_dim,
+mri_status launch_attention(const float *q, size_t q_stride, size_t seq_q, const float *kc,
+                            const float *vc, size_t n_heads, size_t n_kv_heads, size_t head_dim,
                             size_t start_pos, float *out, float *part, hipStream_t s);
 mri_status launch_swiglu(const float *gate, const float *up, size_t n, float *out,
                          hipStream_t s);
+// rows of [gate | up] (2 * ffn floats each) -> rows of ffn.
+mri_status launch_swiglu_rows(const float *gu, size_t rows, size_t ffn, float *out,
+                              hipStream_t s);
 mri_status launch_add(const float *a, const float *b, size_t n, float *out, hipStream_t s);
 mri_status launch_argmax(const float *v, size_t rows, size_t n, uint32_t *idx, hipStream_t s);
 

@@ -54,12 +54,19 @@ __global__ __launch_bounds__(256) void k_embed(const float *__restrict__ table,
 // eps) (correctly rounded divide and sqrt), out = w * (x * rms_inv).  NV > 0:
 // the row is read once into registers, NV float4 per thread (d % 4 == 0,
 // d <= 1024 * NV); NV == 0: any d, two passes.
-template <int NV>
-__global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x,
-                                                 const float *__restrict__ w, int d, float eps,
-                                                 float *__restrict__ out) {
+// MODE 1 (NV > 0): the row is first gathered from an embedding table,
+// table[tokens[row]], and also stored to x_out (embed + the first norm).
+// MODE 2 (NV > 0): the row is first x + delta (the residual add,
+// forward_int8.rs:100-121), stored back to x_out (= x) before the norm.
+template <int NV, int MODE = 0>
+// (x and x_out are the same buffer in MODE 2: neither is restrict.)
+__global__ __launch_bounds__(256) void k_rmsnorm(const float *x, const float *__restrict__ w,
+                                                 int d, float eps, float *__restrict__ out,
+                                                 const uint32_t *__restrict__ tokens = nullptr,
+                                                 const float *__restrict__ delta = nullptr,
+                                                 float *x_out = nullptr) {
     __shared__ float s_part[4];
-    const float *xr = x + (size_t)blockIdx.x * d;
+    const float *xr = MODE == 1 ? x + (size_t)tokens[blockIdx.x] * d : x + (size_t)blockIdx.x * d;
     float *orow = out + (size_t)blockIdx.x * d;
     float acc = 0.0f;
     float4 xv[NV > 0 ? NV : 1];
@@ -68,6 +75,24 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x,
         for (int c = 0; c < NV; ++c) {
             const int i = (c * 256 + threadIdx.x) * 4;
             xv[c] = i < d ? *reinterpret_cast<const float4 *>(xr + i) : float4{0, 0, 0, 0};
+        }
+        if constexpr (MODE == 2) {
+#pragma unroll
+            for (int c = 0; c < NV; ++c) {
+                const int i = (c * 256 + threadIdx.x) * 4;
+                if (i < d) {
+                    const float4 dv =
+                        *reinterpret_cast<const float4 *>(delta + (size_t)blockIdx.x * d + i);
+                    xv[c] = float4{xv[c].x + dv.x, xv[c].y + dv.y, xv[c].z + dv.z, xv[c].w + dv.w};
+                }
+            }
+        }
+        if constexpr (MODE != 0) {
+#pragma unroll
+            for (int c = 0; c < NV; ++c) {
+                const int i = (c * 256 + threadIdx.x) * 4;
+                if (i < d) *reinterpret_cast<float4 *>(x_out + (size_t)blockIdx.x * d + i) = xv[c];
+            }
         }
 #pragma unroll
         for (int c = 0; c < NV; ++c) {
@@ -123,8 +148,8 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x,
 // heads; thread i owns pair i (half = head_dim / 2 <= 64 threads).
 __global__ __launch_bounds__(64) void k_rope_qkv(float *__restrict__ q,
                                                  const float *__restrict__ k,
-                                                 const float *__restrict__ v, int qd, int kvd,
-                                                 int half, int n_heads, int n_kv,
+                                                 const float *__restrict__ v, int qs, int kvs,
+                                                 int kvd, int half, int n_heads, int n_kv,
                                                  const float *__restrict__ cos_t,
                                                  const float *__restrict__ sin_t, int start_pos,
                                                  float *__restrict__ kc,
@@ -134,7 +159,7 @@ __global__ __launch_bounds__(64) void k_rope_qkv(float *__restrict__ q,
     const int hd = 2 * half;
     if (y >= n_heads + n_kv) {  // v head: copy
         const int off = (y - n_heads - n_kv) * hd + 2 * i;
-        const float2 vv = *reinterpret_cast<const float2 *>(v + (size_t)s * kvd + off);
+        const float2 vv = *reinterpret_cast<const float2 *>(v + (size_t)s * kvs + off);
         *reinterpret_cast<float2 *>(vc + (size_t)pos * kvd + off) = vv;
         return;
     }
@@ -142,9 +167,9 @@ __global__ __launch_bounds__(64) void k_rope_qkv(float *__restrict__ q,
     const float *src;
     float *dst;
     if (y < n_heads) {
-        src = dst = q + (size_t)s * qd + y * hd + 2 * i;
+        src = dst = q + (size_t)s * qs + y * hd + 2 * i;
     } else {
-        src = k + (size_t)s * kvd + (y - n_heads) * hd + 2 * i;
+        src = k + (size_t)s * kvs + (y - n_heads) * hd + 2 * i;
         dst = kc + (size_t)pos * kvd + (y - n_heads) * hd + 2 * i;
     }
     const float2 xv = *reinterpret_cast<const float2 *>(src);
@@ -174,7 +199,7 @@ constexpr int attn_tile_floats() { return HD * 65 > 64 * HD ? HD * 65 : 64 * HD;
 
 template <int HD, int QB>
 __global__ __launch_bounds__(256) void k_attention(
-    const float *__restrict__ q, int qd, const float *__restrict__ kc,
+    const float *__restrict__ q, int qs, int qd, const float *__restrict__ kc,
     const float *__restrict__ vc, int kvd, int seq_q, int start_pos, int groups, int lcap,
     float scale, float *__restrict__ out) {
     constexpr int E = HD / kWave;  // dims per lane in the value pass
@@ -193,7 +218,7 @@ __global__ __launch_bounds__(256) void k_attention(
     const int L = start_pos + i0 + nq;  // keys the block's last row sees
     for (int e = t; e < QB * HD; e += 256) {
         const int qq = e / HD, p = e % HD;
-        s_q[e] = qq < nq ? q[(size_t)(i0 + qq) * qd + h * HD + p] : 0.0f;
+        s_q[e] = qq < nq ? q[(size_t)(i0 + qq) * qs + h * HD + p] : 0.0f;
     }
     // 1. scores
     for (int j0 = 0; j0 < L; j0 += KT) {
@@ -386,18 +411,36 @@ __global__ __launch_bounds__(256) void k_attn_decode_part(
 
 // Combines the chunks of head blockIdx.x: m = max m_c,
 // out = sum_c o_c e^(m_c - m) / sum_c l_c e^(m_c - m).
+// Chunk maxima and sums are read once, in parallel, into LDS (up to 1024
+// chunks); each thread then reads its dimension of every chunk with the
+// loads issued ahead of the sums.
 template <int HD>
 __global__ __launch_bounds__(HD) void k_attn_decode_combine(const float *__restrict__ part,
                                                             int nch, float *__restrict__ out) {
+    __shared__ float s_m[1024], s_l[1024];
     const int h = blockIdx.x, d = threadIdx.x;
     const float *ph = part + (size_t)h * nch * (HD + 2);
+    for (int c = d; c < nch; c += HD) {
+        s_m[c] = ph[c * (HD + 2)];
+        s_l[c] = ph[c * (HD + 2) + 1];
+    }
+    __syncthreads();
     float m = -INFINITY;
-    for (int c = 0; c < nch; ++c) m = fmaxf(m, ph[c * (HD + 2)]);
+    for (int c = 0; c < nch; ++c) m = fmaxf(m, s_m[c]);
     float l = 0.0f, o = 0.0f;
-    for (int c = 0; c < nch; ++c) {
-        const float f = expf(ph[c * (HD + 2)] - m);
-        l = l + ph[c * (HD + 2) + 1] * f;
-        o = o + ph[c * (HD + 2) + 2 + d] * f;
+    for (int c0 = 0; c0 < nch; c0 += 16) {
+        float ov[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u)
+            ov[u] = c0 + u < nch ? ph[(c0 + u) * (HD + 2) + 2 + d] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            if (c0 + u < nch) {
+                const float f = expf(s_m[c0 + u] - m);
+                l = l + s_l[c0 + u] * f;
+                o = o + ov[u] * f;
+            }
+        }
     }
     out[(size_t)h * HD + d] = o / l;
 }
@@ -419,6 +462,22 @@ __global__ __launch_bounds__(256) void k_swiglu4(const float4 *__restrict__ gate
                                                  float4 *__restrict__ out) {
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
         const float4 g = gate[i], u = up[i];
+        float4 o;
+        o.x = g.x / (1.0f + expf(-g.x)) * u.x;
+        o.y = g.y / (1.0f + expf(-g.y)) * u.y;
+        o.z = g.z / (1.0f + expf(-g.z)) * u.z;
+        o.w = g.w / (1.0f + expf(-g.w)) * u.w;
+        out[i] = o;
+    }
+}
+
+// Rows of [gate | up] (the fused gate/up projection, 2*ffn floats a row)
+// into rows of ffn: the same function, 4 elements per thread (ffn % 4 == 0).
+__global__ __launch_bounds__(256) void k_swiglu_rows4(const float4 *__restrict__ gu, int ffn4,
+                                                      size_t n4, float4 *__restrict__ out) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
+        const size_t r = i / ffn4, j = i - r * ffn4;
+        const float4 g = gu[r * 2 * ffn4 + j], u = gu[r * 2 * ffn4 + ffn4 + j];
         float4 o;
         o.x = g.x / (1.0f + expf(-g.x)) * u.x;
         o.y = g.y / (1.0f + expf(-g.y)) * u.y;
@@ -454,17 +513,14 @@ __global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ v, in
     const float *row = v + (size_t)blockIdx.x * n;
     float bv = -INFINITY;
     int bi = -1;
-    // 8 loads in flight per thread; within a thread indices only grow, so
-    // ">=" keeps the last of equal values
-    for (int i0 = threadIdx.x; i0 < n; i0 += 8 * 1024) {
-        float xs[8];
+    // 32 loads in flight per thread (one pass up to 32768 values); within a
+    // thread indices only grow, so ">=" keeps the last of equal values
+    for (int i0 = threadIdx.x; i0 < n; i0 += 32 * 1024) {
+        float xs[32];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int i = i0 + u * 1024;
-            xs[u] = i < n ? row[i] : -INFINITY;
-        }
+        for (int u = 0; u < 32; ++u) xs[u] = row[min(i0 + u * 1024, n - 1)];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < 32; ++u) {
             const int i = i0 + u * 1024;
             const float x = xs[u];
             if (i < n && !(x != x) && (bi < 0 || x >= bv)) {
@@ -507,7 +563,7 @@ size_t attn_lds(int lcap) {
 }
 
 template <int HD, int QB>
-mri_status attn_launch(const float *q, int qd, const float *kc, const float *vc, int kvd,
+mri_status attn_launch(const float *q, int qs, int qd, const float *kc, const float *vc, int kvd,
                        int seq_q, int start_pos, int groups, int n_heads, float *out,
                        hipStream_t s) {
     const int L = start_pos + seq_q;
@@ -521,17 +577,17 @@ mri_status attn_launch(const float *q, int qd, const float *kc, const float *vc,
     }
     const float scale = 1.0f / sqrtf((float)HD);
     hipLaunchKernelGGL((k_attention<HD, QB>), dim3((seq_q + QB - 1) / QB, n_heads), dim3(256),
-                       lds, s, q, qd, kc, vc, kvd, seq_q, start_pos, groups, lcap, scale, out);
+                       lds, s, q, qs, qd, kc, vc, kvd, seq_q, start_pos, groups, lcap, scale, out);
     MRI_LAUNCHED("k_attention");
     return MRI_OK;
 }
 
 template <int HD>
-mri_status attn_dispatch(const float *q, int qd, const float *kc, const float *vc, int kvd,
+mri_status attn_dispatch(const float *q, int qs, int qd, const float *kc, const float *vc, int kvd,
                          int seq_q, int start_pos, int groups, int n_heads, float *out,
                          float *part, hipStream_t s) {
     const int L = start_pos + seq_q;
-    if (seq_q == 1 && part) {
+    if (seq_q == 1 && part && L <= 1024 * 64) {  // the combine holds <= 1024 chunks
         const int nch = (L + 63) / 64;
         const float scale = 1.0f / sqrtf((float)HD);
         hipLaunchKernelGGL(k_attn_decode_part<HD>, dim3(nch, n_heads), dim3(256), 0, s, q, kc,
@@ -545,11 +601,11 @@ mri_status attn_dispatch(const float *q, int qd, const float *kc, const float *v
     const int lcap = (L + 3) / 4 * 4;
     constexpr size_t kMax = 160 * 1024;
     if (attn_lds<HD, 16>(lcap) <= kMax)
-        return attn_launch<HD, 16>(q, qd, kc, vc, kvd, seq_q, start_pos, groups, n_heads, out,
-                                   s);
+        return attn_launch<HD, 16>(q, qs, qd, kc, vc, kvd, seq_q, start_pos, groups, n_heads,
+                                   out, s);
     if (attn_lds<HD, 4>(lcap) <= kMax)
-        return attn_launch<HD, 4>(q, qd, kc, vc, kvd, seq_q, start_pos, groups, n_heads, out,
-                                  s);
+        return attn_launch<HD, 4>(q, qs, qd, kc, vc, kvd, seq_q, start_pos, groups, n_heads,
+                                  out, s);
     return set_error(MRI_ERR_UNSUPPORTED, "attention: context too long for one workgroup");
 }
 
@@ -593,16 +649,71 @@ mri_status launch_rmsnorm(const float *x, const float *w, size_t rows, size_t d,
     return MRI_OK;
 }
 
+// Embedding gather + RMSNorm (x_out = table[tokens], out = rmsnorm(x_out)),
+// or residual add + RMSNorm (x += delta, out = rmsnorm(x)).  Falls back to
+// the separate kernels for shapes the one-pass form does not take.
+mri_status launch_embed_rmsnorm(const float *table, const uint32_t *tokens, size_t rows,
+                                size_t d, const float *w, float eps, float *x_out, float *out,
+                                hipStream_t s) {
+    if (!rows) return MRI_OK;
+    if (d % 4 || d > 8192 || !al16(table) || !al16(w) || !al16(out) || !al16(x_out)) {
+        mri_status st = launch_embed(table, tokens, rows, d, x_out, s);
+        if (st) return st;
+        return launch_rmsnorm(x_out, w, rows, d, eps, out, s);
+    }
+    const dim3 g((unsigned)rows), b(256);
+    if (d <= 1024)
+        hipLaunchKernelGGL((k_rmsnorm<1, 1>), g, b, 0, s, table, w, (int)d, eps, out, tokens,
+                           nullptr, x_out);
+    else if (d <= 2048)
+        hipLaunchKernelGGL((k_rmsnorm<2, 1>), g, b, 0, s, table, w, (int)d, eps, out, tokens,
+                           nullptr, x_out);
+    else if (d <= 4096)
+        hipLaunchKernelGGL((k_rmsnorm<4, 1>), g, b, 0, s, table, w, (int)d, eps, out, tokens,
+                           nullptr, x_out);
+    else
+        hipLaunchKernelGGL((k_rmsnorm<8, 1>), g, b, 0, s, table, w, (int)d, eps, out, tokens,
+                           nullptr, x_out);
+    MRI_LAUNCHED("k_rmsnorm");
+    return MRI_OK;
+}
+
+mri_status launch_add_rmsnorm(float *x, const float *delta, size_t rows, size_t d,
+                              const float *w, float eps, float *out, hipStream_t s) {
+    if (!rows) return MRI_OK;
+    if (d % 4 || d > 8192 || !al16(x) || !al16(delta) || !al16(w) || !al16(out)) {
+        mri_status st = launch_add(x, delta, rows * d, x, s);
+        if (st) return st;
+        return launch_rmsnorm(x, w, rows, d, eps, out, s);
+    }
+    const dim3 g((unsigned)rows), b(256);
+    if (d <= 1024)
+        hipLaunchKernelGGL((k_rmsnorm<1, 2>), g, b, 0, s, x, w, (int)d, eps, out, nullptr,
+                           delta, x);
+    else if (d <= 2048)
+        hipLaunchKernelGGL((k_rmsnorm<2, 2>), g, b, 0, s, x, w, (int)d, eps, out, nullptr,
+                           delta, x);
+    else if (d <= 4096)
+        hipLaunchKernelGGL((k_rmsnorm<4, 2>), g, b, 0, s, x, w, (int)d, eps, out, nullptr,
+                           delta, x);
+    else
+        hipLaunchKernelGGL((k_rmsnorm<8, 2>), g, b, 0, s, x, w, (int)d, eps, out, nullptr,
+                           delta, x);
+    MRI_LAUNCHED("k_rmsnorm");
+    return MRI_OK;
+}
+
 mri_status launch_rope_qkv(float *q, const float *k, const float *v, size_t seq, size_t n_heads,
-                           size_t n_kv, size_t head_dim, const float *cos_t, const float *sin_t,
-                           size_t start_pos, float *kc, float *vc, hipStream_t s) {
+                           size_t n_kv, size_t head_dim, size_t q_stride, size_t kv_stride,
+                           const float *cos_t, const float *sin_t, size_t start_pos, float *kc,
+                           float *vc, hipStream_t s) {
     if (!seq) return MRI_OK;
     if (head_dim % 2 || head_dim > 128)
         return set_error(MRI_ERR_UNSUPPORTED, "rope: head_dim must be even and <= 128");
-    const int qd = (int)(n_heads * head_dim), kvd = (int)(n_kv * head_dim);
+    const int kvd = (int)(n_kv * head_dim);
     hipLaunchKernelGGL(k_rope_qkv, dim3((unsigned)seq, (unsigned)(n_heads + 2 * n_kv)), dim3(64),
-                       0, s, q, k, v, qd, kvd, (int)(head_dim / 2), (int)n_heads, (int)n_kv,
-                       cos_t, sin_t, (int)start_pos, kc, vc);
+                       0, s, q, k, v, (int)q_stride, (int)kv_stride, kvd, (int)(head_dim / 2),
+                       (int)n_heads, (int)n_kv, cos_t, sin_t, (int)start_pos, kc, vc);
     MRI_LAUNCHED("k_rope_qkv");
     return MRI_OK;
 }
@@ -613,17 +724,17 @@ size_t attention_part_floats(size_t n_heads, size_t head_dim, size_t max_seq) {
     return n_heads * ((max_seq + 63) / 64) * (head_dim + 2);
 }
 
-mri_status launch_attention(const float *q, size_t seq_q, const float *kc, const float *vc,
-                            size_t n_heads, size_t n_kv_heads, size_t head_dim,
+mri_status launch_attention(const float *q, size_t q_stride, size_t seq_q, const float *kc,
+                            const float *vc, size_t n_heads, size_t n_kv_heads, size_t head_dim,
                             size_t start_pos, float *out, float *part, hipStream_t s) {
     if (!seq_q) return MRI_OK;
     const int qd = (int)(n_heads * head_dim), kvd = (int)(n_kv_heads * head_dim);
-    const int groups = (int)(n_heads / n_kv_heads);
+    const int groups = (int)(n_heads / n_kv_heads), qs = (int)q_stride;
     if (head_dim == 128)
-        return attn_dispatch<128>(q, qd, kc, vc, kvd, (int)seq_q, (int)start_pos, groups,
+        return attn_dispatch<128>(q, qs, qd, kc, vc, kvd, (int)seq_q, (int)start_pos, groups,
                                   (int)n_heads, out, part, s);
     if (head_dim == 64)
-        return attn_dispatch<64>(q, qd, kc, vc, kvd, (int)seq_q, (int)start_pos, groups,
+        return attn_dispatch<64>(q, qs, qd, kc, vc, kvd, (int)seq_q, (int)start_pos, groups,
                                  (int)n_heads, out, part, s);
     return set_error(MRI_ERR_UNSUPPORTED, "attention: head_dim must be 64 or 128");
 }
@@ -639,6 +750,25 @@ mri_status launch_swiglu(const float *gate, const float *up, size_t n, float *ou
     else
         hipLaunchKernelGGL(k_swiglu, dim3(grid_for(n)), dim3(256), 0, s, gate, up, n, out);
     MRI_LAUNCHED("k_swiglu");
+    return MRI_OK;
+}
+
+mri_status launch_swiglu_rows(const float *gu, size_t rows, size_t ffn, float *out,
+                              hipStream_t s) {
+    if (!rows || !ffn) return MRI_OK;
+    if (ffn % 4 || !al16(gu) || !al16(out)) {
+        for (size_t r = 0; r < rows; ++r) {
+            mri_status st = launch_swiglu(gu + r * 2 * ffn, gu + r * 2 * ffn + ffn, ffn,
+                                          out + r * ffn, s);
+            if (st) return st;
+        }
+        return MRI_OK;
+    }
+    const size_t n4 = rows * ffn / 4;
+    hipLaunchKernelGGL(k_swiglu_rows4, dim3(grid_for(n4)), dim3(256), 0, s,
+                       reinterpret_cast<const float4 *>(gu), (int)(ffn / 4), n4,
+                       reinterpret_cast<float4 *>(out));
+    MRI_LAUNCHED("k_swiglu_rows4");
     return MRI_OK;
 }
 

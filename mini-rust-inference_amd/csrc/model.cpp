@@ -27,6 +27,9 @@ namespace {
 struct Layer {
     float *attn_norm = nullptr, *ffn_norm = nullptr;
     mri_weight_ref w[7] = {};
+    // Row concatenations [wq; wk; wv] and [wgate; wup], owned by the model
+    // (format 0 / null ptr when the parts cannot be fused).
+    mri_weight_ref qkv{}, gu{};
     bool set = false;
 };
 
@@ -39,9 +42,11 @@ struct mri_llama {
     mri_weight_ref output{};
     std::vector<Layer> layers;
     float *cos_t = nullptr, *sin_t = nullptr;  // [max_seq][hd/2]
-    // activations for up to max_seq rows
-    float *x = nullptr, *normed = nullptr, *tmp = nullptr, *q = nullptr, *k = nullptr,
-          *v = nullptr, *attn = nullptr, *gate = nullptr, *up = nullptr;
+    // activations for up to max_seq rows; qkv holds q, k and v (rows of
+    // [q | k | v] when the projection is fused, else three row-major blocks),
+    // gu likewise holds gate and up
+    float *x = nullptr, *normed = nullptr, *tmp = nullptr, *qkv = nullptr, *attn = nullptr,
+          *gu = nullptr, *act = nullptr;
     uint32_t *tok = nullptr;      // prompt ids [max_seq]
     uint32_t *gen = nullptr;      // generated ids [max_seq + 1]
     float *attn_part = nullptr;   // split-key decode attention partials
@@ -63,6 +68,12 @@ std::string fmt_err(const char *f, size_t a, size_t b = 0, size_t c = 0) {
     snprintf(buf, sizeof buf, f, a, b, c);
     return buf;
 }
+
+#define TRY(call)                              \
+    do {                                       \
+        const mri_status _st = (call);         \
+        if (_st != MRI_OK) return _st;         \
+    } while (0)
 
 mri_status dalloc(mri_llama *m, size_t bytes, void **p) {
     MRI_HIP(hipMalloc(p, bytes ? bytes : 4));
@@ -109,6 +120,52 @@ mri_status check_weight(const mri_weight_ref &w, size_t n_out, size_t k_in, cons
     }
 }
 
+void release_fused(mri_weight_ref &w) {
+    if (w.ptr && w.format == MRI_WEIGHT_INT8)
+        mri_qmatrix_destroy(static_cast<mri_qmatrix *>(const_cast<void *>(w.ptr)));
+    else if (w.ptr && w.format == MRI_WEIGHT_Q8_0)
+        mri_q8_0_matrix_destroy(static_cast<mri_q8_0_matrix *>(const_cast<void *>(w.ptr)));
+    w = mri_weight_ref{};
+}
+
+// The row concatenation of parts that share one input (q/k/v, gate/up): the
+// fused projection's output row is [part 0 | part 1 | ...] and every element
+// equals that of the separate projection, because the parts see the same
+// activations and the same activation quantization.  Q4_0 weights, mixed
+// formats and parts that are not whole 16-row tiles stay separate (*out
+// left empty).
+mri_status fuse(const mri_weight_ref *parts, int n, mri_weight_ref *out) {
+    *out = mri_weight_ref{};
+    size_t rows = 0;
+    for (int i = 0; i < n; ++i) {
+        if (parts[i].format != parts[0].format || parts[i].n_out % 16) return MRI_OK;
+        rows += parts[i].n_out;
+    }
+    void *h = nullptr;
+    if (parts[0].format == MRI_WEIGHT_INT8) {
+        const mri_qmatrix *p[3];
+        for (int i = 0; i < n; ++i) p[i] = static_cast<const mri_qmatrix *>(parts[i].ptr);
+        mri_qmatrix *f = nullptr;
+        TRY(concat_qmatrix(p, n, nullptr, &f));
+        h = f;
+    } else if (parts[0].format == MRI_WEIGHT_Q8_0) {
+        const mri_q8_0_matrix *p[3];
+        for (int i = 0; i < n; ++i) p[i] = static_cast<const mri_q8_0_matrix *>(parts[i].ptr);
+        mri_q8_0_matrix *f = nullptr;
+        TRY(concat_q8_0_matrix(p, n, nullptr, &f));
+        h = f;
+    } else {
+        return MRI_OK;
+    }
+    *out = mri_weight_ref{parts[0].format, h, rows, parts[0].k_in};
+    const hipError_t e = hipStreamSynchronize(nullptr);
+    if (e != hipSuccess) {
+        release_fused(*out);
+        return hip_error(e, "fuse");
+    }
+    return MRI_OK;
+}
+
 // out[rows, n_out] = in[rows, k_in] projected by w (forward_int8.rs:72-74).
 mri_status proj(const mri_weight_ref &w, const float *in, size_t rows, float *out,
                 hipStream_t s) {
@@ -126,35 +183,55 @@ mri_status proj(const mri_weight_ref &w, const float *in, size_t rows, float *ou
     }
 }
 
-#define TRY(call)                              \
-    do {                                       \
-        const mri_status _st = (call);         \
-        if (_st != MRI_OK) return _st;         \
-    } while (0)
-
 // TransformerBlockInt8::forward_cached (forward_int8.rs:207-216): attention
-// sublayer (:291-323) and FFN sublayer (:350-357) over the rows in m->x.
+// sublayer (:291-323) and FFN sublayer (:350-357).  On entry m->x holds the
+// block's input and m->normed its attention RMSNorm; on exit m->x holds the
+// output and m->normed its RMSNorm with next_norm (the next block's
+// attention norm, or the output norm).  Each residual add is fused with the
+// RMSNorm that follows it; the values are those of the separate steps.
 mri_status block(mri_llama *m, size_t li, size_t rows, size_t start, mri_kv_cache *c,
-                 hipStream_t s) {
+                 const float *next_norm, hipStream_t s) {
     const mri_llama_config &g = m->cfg;
     const Layer &L = m->layers[li];
     float *kc = c->k + li * c->max_seq * c->kvd, *vc = c->v + li * c->max_seq * c->kvd;
-    TRY(launch_rmsnorm(m->x, L.attn_norm, rows, g.dim, g.eps, m->normed, s));
-    TRY(proj(L.w[0], m->normed, rows, m->q, s));
-    TRY(proj(L.w[1], m->normed, rows, m->k, s));
-    TRY(proj(L.w[2], m->normed, rows, m->v, s));
-    TRY(launch_rope_qkv(m->q, m->k, m->v, rows, g.n_heads, g.n_kv_heads, m->hd, m->cos_t,
+    float *q, *k, *v;
+    size_t qs, kvs;
+    if (L.qkv.ptr) {
+        TRY(proj(L.qkv, m->normed, rows, m->qkv, s));
+        q = m->qkv;
+        k = q + m->qd;
+        v = k + m->kvd;
+        qs = kvs = m->qd + 2 * m->kvd;
+    } else {
+        q = m->qkv;
+        k = q + rows * m->qd;
+        v = k + rows * m->kvd;
+        qs = m->qd;
+        kvs = m->kvd;
+        TRY(proj(L.w[0], m->normed, rows, q, s));
+        TRY(proj(L.w[1], m->normed, rows, k, s));
+        TRY(proj(L.w[2], m->normed, rows, v, s));
+    }
+    TRY(launch_rope_qkv(q, k, v, rows, g.n_heads, g.n_kv_heads, m->hd, qs, kvs, m->cos_t,
                         m->sin_t, start, kc, vc, s));
-    TRY(launch_attention(m->q, rows, kc, vc, g.n_heads, g.n_kv_heads, m->hd, start, m->attn,
+    TRY(launch_attention(q, qs, rows, kc, vc, g.n_heads, g.n_kv_heads, m->hd, start, m->attn,
                          m->attn_part, s));
     TRY(proj(L.w[3], m->attn, rows, m->tmp, s));
-    TRY(launch_add(m->x, m->tmp, rows * g.dim, m->x, s));
-    TRY(launch_rmsnorm(m->x, L.ffn_norm, rows, g.dim, g.eps, m->normed, s));
-    TRY(proj(L.w[4], m->normed, rows, m->gate, s));
-    TRY(proj(L.w[5], m->normed, rows, m->up, s));
-    TRY(launch_swiglu(m->gate, m->up, rows * g.ffn_dim, m->gate, s));
-    TRY(proj(L.w[6], m->gate, rows, m->tmp, s));
-    return launch_add(m->x, m->tmp, rows * g.dim, m->x, s);
+    TRY(launch_add_rmsnorm(m->x, m->tmp, rows, g.dim, L.ffn_norm, g.eps, m->normed, s));
+    float *act;
+    if (L.gu.ptr) {
+        TRY(proj(L.gu, m->normed, rows, m->gu, s));
+        act = m->act;
+        TRY(launch_swiglu_rows(m->gu, rows, g.ffn_dim, act, s));
+    } else {
+        act = m->gu;
+        float *up = m->gu + rows * g.ffn_dim;
+        TRY(proj(L.w[4], m->normed, rows, act, s));
+        TRY(proj(L.w[5], m->normed, rows, up, s));
+        TRY(launch_swiglu(act, up, rows * g.ffn_dim, act, s));
+    }
+    TRY(proj(L.w[6], act, rows, m->tmp, s));
+    return launch_add_rmsnorm(m->x, m->tmp, rows, g.dim, next_norm, g.eps, m->normed, s);
 }
 
 // embed -> blocks -> rmsnorm -> output projection for `rows` token ids
@@ -162,9 +239,11 @@ mri_status block(mri_llama *m, size_t li, size_t rows, size_t start, mri_kv_cach
 mri_status run_rows(mri_llama *m, const uint32_t *tok_dev, size_t rows, size_t start,
                     mri_kv_cache *c, float *logits, hipStream_t s) {
     const mri_llama_config &g = m->cfg;
-    TRY(launch_embed(m->embd, tok_dev, rows, g.dim, m->x, s));
-    for (size_t li = 0; li < g.n_layers; ++li) TRY(block(m, li, rows, start, c, s));
-    TRY(launch_rmsnorm(m->x, m->out_norm, rows, g.dim, g.eps, m->normed, s));
+    const float *first = g.n_layers ? m->layers[0].attn_norm : m->out_norm;
+    TRY(launch_embed_rmsnorm(m->embd, tok_dev, rows, g.dim, first, g.eps, m->x, m->normed, s));
+    for (size_t li = 0; li < g.n_layers; ++li)
+        TRY(block(m, li, rows, start, c,
+                  li + 1 < g.n_layers ? m->layers[li + 1].attn_norm : m->out_norm, s));
     return proj(m->output, m->normed, rows, logits, s);
 }
 
@@ -230,10 +309,10 @@ mri_status mri_llama_create(const mri_llama_config *cfg, const float *token_embd
     if ((st = dalloc_t(m, g.vocab * g.dim, &m->embd)) || (st = dalloc_t(m, g.dim, &m->out_norm)) ||
         (st = dalloc_t(m, R * hd / 2, &m->cos_t)) || (st = dalloc_t(m, R * hd / 2, &m->sin_t)) ||
         (st = dalloc_t(m, R * g.dim, &m->x)) || (st = dalloc_t(m, R * g.dim, &m->normed)) ||
-        (st = dalloc_t(m, R * g.dim, &m->tmp)) || (st = dalloc_t(m, R * m->qd, &m->q)) ||
-        (st = dalloc_t(m, R * m->kvd, &m->k)) || (st = dalloc_t(m, R * m->kvd, &m->v)) ||
-        (st = dalloc_t(m, R * m->qd, &m->attn)) || (st = dalloc_t(m, R * g.ffn_dim, &m->gate)) ||
-        (st = dalloc_t(m, R * g.ffn_dim, &m->up)) || (st = dalloc_t(m, R, &m->tok)) ||
+        (st = dalloc_t(m, R * g.dim, &m->tmp)) ||
+        (st = dalloc_t(m, R * (m->qd + 2 * m->kvd), &m->qkv)) ||
+        (st = dalloc_t(m, R * m->qd, &m->attn)) || (st = dalloc_t(m, R * 2 * g.ffn_dim, &m->gu)) ||
+        (st = dalloc_t(m, R * g.ffn_dim, &m->act)) || (st = dalloc_t(m, R, &m->tok)) ||
         (st = dalloc_t(m, R + 1, &m->gen)) ||
         (st = dalloc_t(m, attention_part_floats(g.n_heads, hd, R), &m->attn_part)))
         return fail(st);
@@ -280,12 +359,21 @@ mri_status mri_llama_set_layer(mri_llama *m, size_t li, const float *attn_norm,
     MRI_HIP(hipMemcpy(L.attn_norm, attn_norm, g.dim * 4, hipMemcpyHostToDevice));
     MRI_HIP(hipMemcpy(L.ffn_norm, ffn_norm, g.dim * 4, hipMemcpyHostToDevice));
     for (int i = 0; i < 7; ++i) L.w[i] = w[i];
+    release_fused(L.qkv);
+    release_fused(L.gu);
+    L.set = false;
+    TRY(fuse(w, 3, &L.qkv));
+    TRY(fuse(w + 4, 2, &L.gu));
     L.set = true;
     return MRI_OK;
 }
 
 void mri_llama_destroy(mri_llama *m) {
     if (!m) return;
+    for (Layer &L : m->layers) {
+        release_fused(L.qkv);
+        release_fused(L.gu);
+    }
     for (void *p : m->allocs) (void)hipFree(p);
     if (m->logits_buf) (void)hipFree(m->logits_buf);
     delete m;

@@ -113,6 +113,22 @@ def test_llama_gqa_and_mha_head_dim_128():
     close(host(lg2), oracle.forward_cached(toks[17:], 17), 1e-4)
 
 
+def test_llama_int8_ffn_not_whole_tiles():
+    """ffn = 300 is not a multiple of 16: wq/wk/wv run as one fused
+    projection, wgate/wup as two (the fused [wgate; wup] needs whole 16-row
+    tiles).  Both layouts agree with the oracle."""
+    t = torch()
+    oracle, gpu, rng = build("int8", seed=17, ffn=300, n_layers=1)
+    toks = rng.integers(0, 300, 9).tolist()
+    cache = gpu.kv_cache()
+    lg = empty((8, 300), t.float32)
+    gpu.forward_cached(toks[:8], 0, cache, lg)
+    close(host(lg), oracle.forward_cached(toks[:8], 0), 2e-2)
+    one = empty((300,), t.float32)
+    gpu.forward_decode(toks[8], 8, cache, one)
+    close(host(one), oracle.forward_decode(toks[8], 8), 2e-2)
+
+
 def test_llama_decode_matches_prefill_rows_q8_0():
     """Per-row activation quantization: decoding token p after a prefill of
     0..p-1 gives prefill row p (the oracle's rows are bit-identical; the GPU
