@@ -336,9 +336,7 @@ mri_status mri_q8_0_matrix_from_raw_device(const uint8_t *data_dev, size_t len,
     d.n_tiles = (n_out + kTileN - 1) / kTileN;
     d.kp = round_up(k_in ? k_in : 1, kQK * kQ8ScaleGroup);
     d.device = dev;
-    const size_t P = d.kp / kChunkK, Q = d.kp / (kQK * kQ8ScaleGroup);
-    hipError_t e = hipMalloc(&d.tiles, d.n_tiles * P * 1024 + 256);
-    if (e == hipSuccess) e = hipMalloc(&d.scales, d.n_tiles * Q * kTileN * 16 + 256);
+    const hipError_t e = hipMalloc(&d.laps, d.bytes() + 256);
     if (e != hipSuccess) st = hip_error(e, "hipMalloc");
     if (!st) st = launch_repack_q8_0(data_dev, d, static_cast<hipStream_t>(stream));
     if (st) {
@@ -381,24 +379,22 @@ mri_status mri_q8_0_matrix_read_raw(const mri_q8_0_matrix *w, uint8_t *data, siz
     const Q8MatrixDev &d = w->d;
     if (len != d.n_out * d.n_blocks * kQ8Bytes)
         return set_error(MRI_ERR_INVALID_SHAPE, "read_raw: wrong length");
-    const size_t P = d.kp / kChunkK, Q = d.kp / (kQK * kQ8ScaleGroup);
-    std::vector<int8_t> tiles(d.n_tiles * P * 1024);
-    std::vector<uint16_t> sc(d.n_tiles * Q * kTileN * kQ8ScaleGroup);
+    const size_t G = d.laps_per_tile();
+    std::vector<uint8_t> laps(d.bytes());
     MRI_HIP(hipDeviceSynchronize());
-    if (!tiles.empty()) MRI_HIP(hipMemcpy(tiles.data(), d.tiles, tiles.size(), hipMemcpyDeviceToHost));
-    if (!sc.empty()) MRI_HIP(hipMemcpy(sc.data(), d.scales, sc.size() * 2, hipMemcpyDeviceToHost));
+    if (!laps.empty()) MRI_HIP(hipMemcpy(laps.data(), d.laps, laps.size(), hipMemcpyDeviceToHost));
     for (size_t n = 0; n < d.n_out; ++n) {
         const size_t T = n / kTileN, r = n % kTileN;
         for (size_t b = 0; b < d.n_blocks; ++b) {
+            const uint8_t *lap = laps.data() + (T * G + b / 8) * kQ8LapBytes;
             uint8_t *blk = data + (n * d.n_blocks + b) * kQ8Bytes;
-            const uint16_t dv = sc[((b / 8 * d.n_tiles + T) * kTileN + r) * 8 + b % 8];
-            blk[0] = (uint8_t)(dv & 0xFF);
-            blk[1] = (uint8_t)(dv >> 8);
-            const size_t p = b / 2, h = b % 2;
+            const uint8_t *dv = lap + 4096 + r * 16 + (b % 8) * 2;
+            blk[0] = dv[0];
+            blk[1] = dv[1];
+            const size_t c = (b / 2) % 4, h = b % 2;
             for (size_t g = 0; g < 4; ++g)
                 for (size_t j = 0; j < 8; ++j)
-                    blk[2 + g * 8 + j] =
-                        (uint8_t)tiles[((p * d.n_tiles + T) * 64 + g * 16 + r) * 16 + h * 8 + j];
+                    blk[2 + g * 8 + j] = lap[(c * 64 + g * 16 + r) * 16 + h * 8 + j];
         }
     }
     return MRI_OK;
@@ -408,14 +404,12 @@ size_t mri_q8_0_matrix_n_out(const mri_q8_0_matrix *w) { return w ? w->d.n_out :
 size_t mri_q8_0_matrix_k_in(const mri_q8_0_matrix *w) { return w ? w->d.k_in : 0; }
 size_t mri_q8_0_matrix_device_bytes(const mri_q8_0_matrix *w) {
     if (!w) return 0;
-    const Q8MatrixDev &d = w->d;
-    return d.n_tiles * d.kp * kTileN + d.n_tiles * (d.kp / 256) * kTileN * 16;
+    return w->d.bytes();
 }
 
 void mri_q8_0_matrix_destroy(mri_q8_0_matrix *w) {
     if (!w) return;
-    if (w->d.tiles) (void)hipFree(w->d.tiles);
-    if (w->d.scales) (void)hipFree(w->d.scales);
+    if (w->d.laps) (void)hipFree(w->d.laps);
     delete w;
 }
 
@@ -424,10 +418,10 @@ void mri_q8_0_matrix_destroy(mri_q8_0_matrix *w) {
 namespace mri {
 
 // Row concatenation of weight handles with one k_in whose n_out are whole
-// tiles (multiples of 16): in the slab-major layout, slab p of the fused
-// matrix is the parts' slab p side by side, so each part is one pitched copy
-// of its tiles (and, for Q8_0, of its scale groups).  The result is a new
-// handle; the parts are not modified.
+// tiles (multiples of 16).  The result is a new handle; the parts are not
+// modified.  INT8 (slab-major chunks): slab p of the fused matrix is the
+// parts' slab p side by side, so each part is one pitched copy.  Q8_0
+// (tile-major lap blocks): the parts' buffers one after the other.
 mri_status concat_qmatrix(const mri_qmatrix *const *parts, int n, hipStream_t s,
                           mri_qmatrix **out) {
     *out = nullptr;
@@ -471,26 +465,17 @@ mri_status concat_q8_0_matrix(const mri_q8_0_matrix *const *parts, int n, hipStr
     }
     auto *h = new mri_q8_0_matrix();
     Q8MatrixDev &d = h->d;
-    const Q8MatrixDev &d0 = parts[0]->d;
+    d = parts[0]->d;
+    d.laps = nullptr;
     d.n_out = rows;
-    d.k_in = d0.k_in;
-    d.n_blocks = d0.n_blocks;
     d.n_tiles = rows / kTileN;
-    d.kp = d0.kp;
-    d.device = d0.device;
-    const size_t P = d.kp / kChunkK, Q = d.kp / (kQK * kQ8ScaleGroup);
-    hipError_t e = hipMalloc(&d.tiles, d.n_tiles * P * 1024 + 256);
-    if (e == hipSuccess) e = hipMalloc(&d.scales, d.n_tiles * Q * kTileN * 16 + 256);
-    size_t t0 = 0;
+    // tile-major lap blocks: the fused matrix is the parts' buffers in turn
+    hipError_t e = hipMalloc(&d.laps, d.bytes() + 256);
+    size_t off = 0;
     for (int i = 0; i < n && e == hipSuccess; ++i) {
         const Q8MatrixDev &pd = parts[i]->d;
-        e = hipMemcpy2DAsync(d.tiles + t0 * 1024, d.n_tiles * 1024, pd.tiles, pd.n_tiles * 1024,
-                             pd.n_tiles * 1024, P, hipMemcpyDeviceToDevice, s);
-        if (e == hipSuccess)  // scale group q of tile T: 16 rows x 16 bytes at (q*n_tiles + T)*256
-            e = hipMemcpy2DAsync(reinterpret_cast<uint8_t *>(d.scales) + t0 * 256,
-                                 d.n_tiles * 256, pd.scales, pd.n_tiles * 256, pd.n_tiles * 256,
-                                 Q, hipMemcpyDeviceToDevice, s);
-        t0 += pd.n_tiles;
+        e = hipMemcpyAsync(d.laps + off, pd.laps, pd.bytes(), hipMemcpyDeviceToDevice, s);
+        off += pd.bytes();
     }
     if (e != hipSuccess) {
         mri_q8_0_matrix_destroy(h);

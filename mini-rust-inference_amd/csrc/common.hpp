@@ -14,15 +14,20 @@
 //    MFMA and a wave reads 1 KiB contiguous bytes per instruction.
 //    Scales: f32 [n_tiles * 16] (zero padded).
 //
-//  * Q8_0 (Q8_0WeightMatrix, q8_direct.rs:60-69) is split into quants and
-//    scales.  Quants use the same slab-major 1 KiB chunks, but lane l's 16
-//    bytes hold two 8-byte B operands of v_mfma_i32_16x16x32_i8 (one MFMA
-//    per 32-element block): bytes [8h, 8h+8) = quants [8g, 8g+8) of block
-//    2p+h of row 16T + (l % 16), g = l / 16.  Kp = K rounded up to 256.
-//    Scales stay f16 (2 bytes per block, as in GGUF) in groups of 8 blocks
-//    (4 chunks), also slab-major: group (q, T) row r at 16-byte index
-//    (q * n_tiles + T) * 16 + r holds the scales of blocks 8q .. 8q+7, so
-//    one 16-byte load gives a lane the scales of 4 consecutive chunks.
+//  * Q8_0 (Q8_0WeightMatrix, q8_direct.rs:60-69) is stored in "lap blocks"
+//    of 8 Q8_0 blocks (256 k) x 16 rows, 4352 bytes each (the raw block
+//    size, 34 bytes x 128), tile-major: lap block (T, q) of tile T and lap
+//    q = 0 .. G-1 (G = Kp / 256, Kp = K rounded up to 256) sits at byte
+//    offset (T * G + q) * 4352, so a tile's whole K is one contiguous run
+//    and a sweep reads quants and scales from the same DRAM pages.  A lap
+//    block holds:
+//     - 4 chunks of 1 KiB (c = 0..3, slab p = 4q + c) in which lane l's 16
+//       bytes hold two 8-byte B operands of v_mfma_i32_16x16x32_i8 (one MFMA
+//       per 32-element block): bytes [8h, 8h+8) = quants [8g, 8g+8) of block
+//       2p+h of row 16T + (l % 16), g = l / 16;
+//     - then 16 x 16 bytes of f16 scales (2 bytes per block, as in GGUF):
+//       row r at byte 4096 + 16 r holds the scales of blocks 8q .. 8q+7, so
+//       one 16-byte load gives a lane the scales of its 4 chunks.
 //
 //  * Activations quantized by the library are written to a per-(device,
 //    stream) scratch in [M][Kp] int8 rows (zero padded).  For Q8_0 the 64
@@ -71,14 +76,18 @@ struct QMatrixDev {
     int device = 0;
 };
 
+constexpr int kQ8LapBytes = 4352;  // one Q8_0 lap block: 4 chunks + 256 bytes of scales
+constexpr int kQ8LapK = 256;       // K elements per lap block
+
 struct Q8MatrixDev {
     size_t n_out = 0, k_in = 0;
     size_t n_blocks = 0;    // k_in / 32
     size_t n_tiles = 0;
     size_t kp = 0;          // K padded to 256
-    int8_t *tiles = nullptr;     // n_tiles * (kp/64) KiB
-    uint16_t *scales = nullptr;  // n_tiles * (kp/256) * 16 * 8 f16
+    int8_t *laps = nullptr;  // n_tiles * (kp/256) lap blocks of 4352 bytes
     int device = 0;
+    size_t laps_per_tile() const { return kp / kQ8LapK; }
+    size_t bytes() const { return n_tiles * laps_per_tile() * kQ8LapBytes; }
 };
 
 // Exact f16 -> f32 decode (v_cvt_f32_f16), the f16_to_f32 of

@@ -1,13 +1,14 @@
 // gemv_common.hpp — shared pieces of the decode GEMV kernels (M <= 4) of
-// gemv_int8.hip and gemv_q8.hip: a single sweep over the slab-major weight
-// stream with a ring of loads in flight per wave.
+// gemv_int8.hip and gemv_q8.hip: a single sweep over the weight stream with
+// a ring of loads in flight per wave.
 //
 // Work decomposition: a workgroup holds TPW tiles of 16 output channels with
-// S waves each; a tile's K chunks are split over its S waves as evenly as
-// possible (Q8_0: in whole scale groups of 4 chunks).  Because the weights
-// are stored slab-major (chunk (p, T) at (p * n_tiles + T) KiB), the waves
-// of all tiles that run together read one contiguous window of the matrix
-// that moves through memory, which is the access pattern HBM serves best.
+// S waves each; a tile's K chunks are split over its S waves (INT8: evenly;
+// Q8_0: lap blocks of 4 chunks dealt out round-robin).  INT8 weights are
+// slab-major (chunk (p, T) at (p * n_tiles + T) KiB), so the waves of all
+// tiles that run together read one contiguous, moving window; Q8_0 lap
+// blocks are tile-major with the scales inside, so each wave reads whole
+// 4 KiB runs and the scales come from the same DRAM pages as the quants.
 //
 // Ring: each wave keeps D chunk loads in flight.  Slot s holds the chunks
 // i == s (mod D) of its segment; the loop body is unrolled by D, so every
@@ -22,9 +23,9 @@
 //  * Fused prologue (one f32 row, the decode case): the S waves split the
 //    activation read, reduce max|x| through LDS, quantize (symmetric.rs:42-57;
 //    per row and per tensor coincide for one row) and write the int8 row to
-//    LDS in the weight chunk order.  The activation loads are issued before
-//    the ring's first D weight loads, so the prologue overlaps the weight
-//    stream.  Other calls copy pre-quantized rows to LDS instead.
+//    LDS in the weight chunk order.  The activation loads are issued just
+//    before the ring's first weight loads, so the prologue overlaps the
+//    weight stream.  Other calls copy pre-quantized rows to LDS instead.
 #pragma once
 
 #include <cstdlib>
@@ -99,15 +100,16 @@ __device__ inline void stage_load(const v4i *src, int n16, v4i (&xr)[XR]) {
     for (int e = 0; e < XR; ++e) xr[e] = src[min((int)threadIdx.x + S * kWave * e, n16 - 1)];
 }
 
-// The activation prologue runs in two parts around the priming of the
-// weight ring.  act_begin consumes the staged registers (the per-wave
-// max|x| of an f32 row, or the copy of int8 rows into LDS), so the wave
-// waits for its activation loads BEFORE it issues any weight load: the
-// small activation read then does not queue behind megabytes of weight
-// requests in HBM.  act_end (after the ring is primed) finishes the
-// quantization: block max through LDS, quantize_symmetric
+// The activation prologue runs after the priming of the weight ring: the
+// kernels issue the activation loads (stage_load), then the ring's first
+// weight loads, then consume the activations.  Loads return in issue order,
+// so act_begin waits for the activation loads alone while the weight loads
+// stay in flight.  act_begin consumes the staged registers (the per-wave
+// max|x| of an f32 row, or the copy of int8 rows into LDS); act_end
+// finishes the quantization: block max through LDS, quantize_symmetric
 // (symmetric.rs:42-57; per row and per tensor coincide for one row) of the
-// row held in xr into LDS (chunk-permuted when perm).
+// row held in xr into LDS (chunk-permuted when perm).  Neither waits for
+// global loads at its barriers beyond the activations'.
 template <int S, int XR, bool FUSED>
 __device__ inline void act_begin(const ActIn &in, int n16, const v4i (&xr)[XR], int8_t *s_act,
                                  float *red) {
@@ -132,7 +134,7 @@ __device__ inline void act_begin(const ActIn &in, int n16, const v4i (&xr)[XR], 
             if (i < n16) dst[i] = xr[e];
         }
     }
-    // keep the weight loads that follow behind the uses above
+    // keep the uses above after the weight loads issued before them
     __builtin_amdgcn_sched_barrier(0);
 }
 

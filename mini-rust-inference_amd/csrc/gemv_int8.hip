@@ -53,10 +53,10 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_int8(
     stage_load<NW, XR>(FUSED ? reinterpret_cast<const v4i *>(in.x)
                              : reinterpret_cast<const v4i *>(in.act),
                        n16, xr);
-    act_begin<NW, XR, FUSED>(in, n16, xr, s_act, red);
 #pragma unroll
     for (int s = 0; s < D; ++s)
         wr[s] = __builtin_nontemporal_load(wp + (size_t)min(c0 + s, last) * pitch);
+    act_begin<NW, XR, FUSED>(in, n16, xr, s_act, red);
     act_end<NW, XR, FUSED>(in, false, xr, s_act, red, sa_value, blockIdx.x == 0);
     if constexpr (FUSED) sa_ptr = nullptr;
 

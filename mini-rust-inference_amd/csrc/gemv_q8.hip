@@ -1,6 +1,6 @@
 // gemv_q8.hip — Q8_0 decode GEMV (M <= 4): matmul_q8_0_direct
-// (q8_direct.rs:229-289) on the slab-major MFMA chunks of the quants and
-// the slab-major f16 scale groups.
+// (q8_direct.rs:229-289) on the tile-major lap blocks (4 MFMA chunks of
+// quants followed by their f16 scales).
 #include "gemv_common.hpp"
 
 namespace mri {
@@ -39,8 +39,7 @@ __device__ inline void lds_barrier() {
 template <int MR, int S, int TPW, int RL, int XR, bool FUSED, bool DEBUG>
 __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     ActIn in, int M, int kp, const float *__restrict__ sa_rows,
-    const v4i *__restrict__ tiles, const v4i *__restrict__ qscales, int N,
-    int n_tiles, int G, int nb, float *__restrict__ out,
+    const v4i *__restrict__ laps, int N, int n_tiles, int G, int nb, float *__restrict__ out,
     int32_t *__restrict__ block_dots) {
     constexpr int NW = S * TPW;               // waves per workgroup
     constexpr int LR = MR == 1 ? 1 : 2;       // rows per result lane
@@ -58,10 +57,11 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     const int r = l & 15, g = l >> 4;
     const int NR = (G + S - 1) / S;           // rounds
     const int nq = tile_ok && w < G ? (G - w + S - 1) / S : 0;  // laps of this wave
-    const size_t pitch = (size_t)n_tiles * kWave;
-    const size_t spitch = (size_t)n_tiles * 16;
-    const v4i *wp = tiles + (size_t)Tc * kWave + l;
-    const v4i *sp = qscales + (size_t)Tc * 16 + r;
+    // lap block q of the tile: chunk s at v4i offset s * 64 (+ lane), its
+    // scales at 256 (+ row)
+    const v4i *wp = laps + (size_t)Tc * G * (kQ8LapBytes / 16) + l;
+    const v4i *sp = laps + (size_t)Tc * G * (kQ8LapBytes / 16) + 256 + r;
+    constexpr size_t LB = kQ8LapBytes / 16;
     const int n = T * 16 + r;
 
     // LDS: [act M*kp][red NW floats][terms 2 x TPW x (S-1) x LG x 16 x TW floats]
@@ -93,17 +93,19 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
 #pragma unroll
         for (int j = 0; j < LR; ++j) sa[j] = sa_rows[min(2 * g + j, M - 1)];
     }
-    act_begin<NW, XR, FUSED>(in, n16, xr, s_act, red);
     // prime the ring in the steady state's issue order (a lap's quants, then
-    // its scales), lap indices clamped to the tile
+    // its scales), lap indices clamped to the tile.  The activation loads
+    // were issued first, so they return first, and the prologue below waits
+    // for them alone while the ring's loads stay in flight.
 #pragma unroll
     for (int u = 0; u < RL; ++u) {
         const int q = min(min(u, max(nq - 1, 0)) * S + w, G - 1);
 #pragma unroll
         for (int s = 0; s < 4; ++s)
-            wr[u][s] = __builtin_nontemporal_load(wp + (size_t)(4 * q + s) * pitch);
-        sr[u] = sp[(size_t)q * spitch];
+            wr[u][s] = __builtin_nontemporal_load(wp + (size_t)q * LB + s * 64);
+        sr[u] = sp[(size_t)q * LB];
     }
+    act_begin<NW, XR, FUSED>(in, n16, xr, s_act, red);
     act_end<NW, XR, FUSED>(in, true, xr, s_act, red, sa[0], blockIdx.x == 0);
     float fs[LR];
 #pragma unroll
@@ -159,7 +161,7 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
 #pragma unroll
             for (int i = 0; i < 2 * LR; ++i) dt[s][i] = d[i];
             if (refill)
-                wr[U][s] = __builtin_nontemporal_load(wp + (size_t)(4 * (q + RL * S) + s) * pitch);
+                wr[U][s] = __builtin_nontemporal_load(wp + (size_t)(q + RL * S) * LB + s * 64);
         }
         float tv[LR][8];
 #pragma unroll
@@ -207,7 +209,7 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
                 }
             }
         }
-        if (refill) sr[U] = sp[(size_t)(q + RL * S) * spitch];
+        if (refill) sr[U] = sp[(size_t)(q + RL * S) * LB];
         round_end(L);
     };
 
@@ -252,14 +254,13 @@ size_t lds_q8(int s, int tpw, size_t m, size_t kp, size_t G) {
     return m * kp + (size_t)s * tpw * 16 + 2 * (size_t)tpw * (s - 1) * lg * 16 * lr * 8 * 4;
 }
 
-// Configuration by the number of 16-row tiles (measured on MI355X).  Many
-// tiles: one wave per tile over all of K, two tiles per workgroup, two laps
-// in flight; otherwise four waves per tile, with two laps in flight when
-// that leaves fewer than about 2000 waves.
+// Configuration by the number of 16-row tiles (measured on MI355X): four
+// waves per tile, with two laps in flight when that leaves fewer than
+// about 2000 waves, else one.
 CfgQ8 pick_q8(bool fused, size_t n_tiles, size_t m, size_t k, size_t kp, size_t G) {
     CfgQ8 c;
-    if (n_tiles >= 1024) { c.s = 1; c.tpw = 2; c.rl = 2; }
-    else { c.s = 4; c.rl = n_tiles * 4 >= 2048 ? 1 : 2; }
+    c.s = 4;
+    c.rl = n_tiles * 4 >= 2048 ? 1 : 2;
     const size_t threads = (size_t)c.s * c.tpw * kWave;
     const size_t nx = ceil_div(fused ? k / 4 : m * kp / 16, threads);
     if (c.s == 1) c.xr = nx <= 8 ? 8 : nx <= 24 ? 24 : 0;
@@ -268,9 +269,7 @@ CfgQ8 pick_q8(bool fused, size_t n_tiles, size_t m, size_t k, size_t kp, size_t 
     return c;
 }
 
-inline size_t groups_of(const Q8MatrixDev &w) {
-    return ((w.n_blocks + 1) / 2 + 3) / 4;  // scale groups holding real blocks
-}
+inline size_t groups_of(const Q8MatrixDev &w) { return w.laps_per_tile(); }
 
 template <int MR, int S, int TPW, int RL, int XR, bool FUSED, bool DEBUG>
 void launch_q8(ActIn in, size_t m, const float *sa_rows, const Q8MatrixDev &w,
@@ -279,8 +278,7 @@ void launch_q8(ActIn in, size_t m, const float *sa_rows, const Q8MatrixDev &w,
     hipLaunchKernelGGL((k_gemv_q8_0<MR, S, TPW, RL, XR, FUSED, DEBUG>),
                        dim3((unsigned)ceil_div(w.n_tiles, TPW)), dim3(S * TPW * kWave),
                        lds_q8(S, TPW, m, w.kp, G), st, in, (int)m, (int)w.kp, sa_rows,
-                       reinterpret_cast<const v4i *>(w.tiles),
-                       reinterpret_cast<const v4i *>(w.scales), (int)w.n_out,
+                       reinterpret_cast<const v4i *>(w.laps), (int)w.n_out,
                        (int)w.n_tiles, (int)G, (int)w.n_blocks, out, block_dots);
 }
 
@@ -291,7 +289,6 @@ void dispatch_q8(CfgQ8 c, ActIn in, size_t m, const float *sa_rows, const Q8Matr
     if (c.s == S_ && c.tpw == TPW_ && c.rl == RL_ && c.xr == XR_)                         \
         return launch_q8<MR, S_, TPW_, RL_, XR_, FUSED, DEBUG>(in, m, sa_rows, w, out,    \
                                                                block_dots, st);
-    MRI_Q8(1, 2, 2, 8) MRI_Q8(1, 2, 2, 24)
     MRI_Q8(4, 1, 1, 4) MRI_Q8(4, 1, 1, 12)
     MRI_Q8(4, 1, 2, 4) MRI_Q8(4, 1, 2, 12)
 #undef MRI_Q8
@@ -307,7 +304,7 @@ void dispatch_q8_dbg(bool dbg, CfgQ8 c, ActIn in, size_t m, const float *sa_rows
 }  // namespace
 
 bool gemv_q8_supported(bool fused, size_t m, size_t n_tiles, size_t k, size_t kp) {
-    const size_t G = ((k / kQK + 1) / 2 + 3) / 4;
+    const size_t G = kp / kQ8LapK;
     return m >= 1 && m <= (size_t)kMaxM && pick_q8(fused, n_tiles, m, k, kp, G).s > 0;
 }
 

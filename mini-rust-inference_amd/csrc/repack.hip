@@ -36,19 +36,20 @@ __global__ __launch_bounds__(kThreads) void k_pad_scales(
     if (i < np) out[i] = i < n ? scales[i] : 0.0f;
 }
 
-// One thread per 16-byte lane piece of the Q8_0 quant tiles.
+// One thread per 16-byte lane piece of the Q8_0 quants, enumerated in the
+// order of the lap blocks: piece e = (lap block, chunk c, lane).
 __global__ __launch_bounds__(kThreads) void k_repack_q8_quants(
-    const uint8_t *__restrict__ raw, size_t n, size_t nb, size_t n_tiles,
-    size_t P, int8_t *__restrict__ tiles) {
-    const size_t total = n_tiles * P * 64;
+    const uint8_t *__restrict__ raw, size_t n, size_t nb, size_t G, size_t total,
+    int8_t *__restrict__ laps) {
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
          e += stride) {
-        const size_t lane = e & 63, pt = e >> 6;
-        const size_t p = pt / n_tiles, T = pt - p * n_tiles;
+        const size_t lane = e & 63, c = (e >> 6) & 3, lb = e >> 8;
+        const size_t T = lb / G, q = lb - T * G;
+        const size_t p = 4 * q + c;
         const size_t row = T * kTileN + (lane & 15);
         const size_t g = lane >> 4;
-        int8_t *dst = tiles + e * 16;
+        int8_t *dst = laps + lb * kQ8LapBytes + (c * 64 + lane) * 16;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const size_t b = 2 * p + h;
@@ -61,18 +62,17 @@ __global__ __launch_bounds__(kThreads) void k_repack_q8_quants(
     }
 }
 
-// One thread per (tile, group of 8 blocks, row): 8 f16 scales.
+// One thread per (lap block, row): the row's 8 f16 scales of the lap.
 __global__ __launch_bounds__(kThreads) void k_repack_q8_scales(
-    const uint8_t *__restrict__ raw, size_t n, size_t nb, size_t n_tiles,
-    size_t Q, uint16_t *__restrict__ scales) {
-    const size_t total = n_tiles * Q * kTileN;
+    const uint8_t *__restrict__ raw, size_t n, size_t nb, size_t G, size_t total,
+    int8_t *__restrict__ laps) {
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
          e += stride) {
-        const size_t r = e & 15, qt = e >> 4;
-        const size_t q = qt / n_tiles, T = qt - q * n_tiles;
+        const size_t r = e & 15, lb = e >> 4;
+        const size_t T = lb / G, q = lb - T * G;
         const size_t row = T * kTileN + r;
-        uint16_t *dst = scales + e * kQ8ScaleGroup;
+        uint16_t *dst = reinterpret_cast<uint16_t *>(laps + lb * kQ8LapBytes + 4096 + r * 16);
 #pragma unroll
         for (int j = 0; j < kQ8ScaleGroup; ++j) {
             const size_t b = q * kQ8ScaleGroup + j;
@@ -115,19 +115,16 @@ mri_status launch_repack_int8(const int8_t *data, const float *scales,
 
 mri_status launch_repack_q8_0(const uint8_t *raw, Q8MatrixDev &w,
                               hipStream_t s) {
-    const size_t P = w.kp / kChunkK;
-    const size_t Q = w.kp / (kQK * kQ8ScaleGroup);
-    const size_t pieces = w.n_tiles * P * 64;
+    const size_t G = w.laps_per_tile();
+    const size_t pieces = w.n_tiles * G * 256;
     if (pieces) {
         hipLaunchKernelGGL(k_repack_q8_quants, dim3(grid_for(pieces)),
-                           dim3(kThreads), 0, s, raw, w.n_out, w.n_blocks,
-                           w.n_tiles, P, w.tiles);
+                           dim3(kThreads), 0, s, raw, w.n_out, w.n_blocks, G, pieces,
+                           w.laps);
         MRI_LAUNCHED("k_repack_q8_quants");
-    }
-    const size_t sc = w.n_tiles * Q * kTileN;
-    if (sc) {
-        hipLaunchKernelGGL(k_repack_q8_scales, dim3(grid_for(sc)), dim3(kThreads),
-                           0, s, raw, w.n_out, w.n_blocks, w.n_tiles, Q, w.scales);
+        const size_t rows = w.n_tiles * G * kTileN;
+        hipLaunchKernelGGL(k_repack_q8_scales, dim3(grid_for(rows)), dim3(kThreads), 0, s,
+                           raw, w.n_out, w.n_blocks, G, rows, w.laps);
         MRI_LAUNCHED("k_repack_q8_scales");
     }
     return MRI_OK;

@@ -2,8 +2,9 @@
 // 32-row slices) quantized matmul on CDNA4 MFMA.
 //
 // The weight stream dominates (M*K activation bytes vs N*K weight bytes), so
-// both kernels stream the slab-major 1 KiB weight chunks of one 16-row tile
-// per wave, with the activation rows read from a quantized [M][kp] buffer:
+// both kernels stream the 1 KiB weight chunks of one 16-row tile per wave
+// (INT8: slab-major chunks; Q8_0: the tile's lap blocks, quants and scales
+// together), with the activation rows read from a quantized [M][kp] buffer:
 //   * per-channel INT8: v_mfma_i32_16x16x64_i8 accumulates exact int32 dot
 //     products for 16 (m) x 16 (n) outputs; the f32 epilogue
 //     ((f32)acc * s_a) * s_w runs once at the end (int8.rs:93);
@@ -149,8 +150,7 @@ __global__ __launch_bounds__(kWave) void k_skinny_int8(
 template <int AG, int TPW, int RL, bool DEBUG>
 __global__ __launch_bounds__(TPW * kWave) void k_skinny_q8_0(
     const int8_t *__restrict__ act, int M, int kp, const float *__restrict__ sa_rows,
-    const v4i *__restrict__ tiles, const v4i *__restrict__ qscales, int N,
-    int n_tiles, int G, int nb, float *__restrict__ out,
+    const v4i *__restrict__ laps, int N, int n_tiles, int G, int nb, float *__restrict__ out,
     int32_t *__restrict__ block_dots, int ns) {
     // wave -> (tile, set of AG activation groups); the ns waves of a tile are
     // adjacent, so they share a workgroup (or neighbouring ones) and the
@@ -166,10 +166,11 @@ __global__ __launch_bounds__(TPW * kWave) void k_skinny_q8_0(
     if (T >= n_tiles) return;  // whole waves only; the kernel has no barrier
     const int l = threadIdx.x & 63;
     const int r = l & 15, g = l >> 4;
-    const size_t pitch = (size_t)n_tiles * kWave;
-    const size_t spitch = (size_t)n_tiles * 16;
-    const v4i *wp = tiles + (size_t)T * kWave + l;
-    const v4i *sp = qscales + (size_t)T * 16 + r;
+    // the tile's lap blocks: chunk c of lap q at v4i offset q * LB + c * 64
+    // (+ lane), the lap's scales at q * LB + 256 (+ row)
+    constexpr size_t LB = kQ8LapBytes / 16;
+    const v4i *wp = laps + (size_t)T * G * LB + l;
+    const v4i *sp = laps + (size_t)T * G * LB + 256 + r;
     const int n = T * 16 + r;
     const v4i *ap[AG];
     float sa[AG][4], fs[AG][4];
@@ -191,11 +192,11 @@ __global__ __launch_bounds__(TPW * kWave) void k_skinny_q8_0(
         const int q = min(u, G - 1);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            wr[u][c] = __builtin_nontemporal_load(wp + (size_t)(4 * q + c) * pitch);
+            wr[u][c] = __builtin_nontemporal_load(wp + (size_t)q * LB + c * 64);
 #pragma unroll
             for (int a = 0; a < AG; ++a) xr[u][c][a] = ap[a][(size_t)(4 * q + c) * 4];
         }
-        sr[u] = sp[(size_t)q * spitch];
+        sr[u] = sp[(size_t)q * LB];
     }
     const v4i zero = {0, 0, 0, 0};
 
@@ -216,7 +217,7 @@ __global__ __launch_bounds__(TPW * kWave) void k_skinny_q8_0(
             }
             if (refill) {
                 const size_t p = (size_t)(4 * (L + RL) + c);
-                wr[U][c] = __builtin_nontemporal_load(wp + p * pitch);
+                wr[U][c] = __builtin_nontemporal_load(wp + (size_t)(L + RL) * LB + c * 64);
 #pragma unroll
                 for (int a = 0; a < AG; ++a) xr[U][c][a] = ap[a][p * 4];
             }
@@ -246,7 +247,7 @@ __global__ __launch_bounds__(TPW * kWave) void k_skinny_q8_0(
                 }
             }
         }
-        if (refill) sr[U] = sp[(size_t)(L + RL) * spitch];
+        if (refill) sr[U] = sp[(size_t)(L + RL) * LB];
         // keep the next lap's uses of its (younger) loads below this point
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -289,14 +290,14 @@ void launch_i8(const int8_t *act, size_t m, size_t kp, const float *sa_ptr,
 template <int AG, int TPW, int RL, bool DEBUG>
 void launch_q8(const int8_t *act, size_t m, size_t kp, const float *sa_rows,
                const Q8MatrixDev &w, float *out, int32_t *block_dots, int ns, hipStream_t s) {
-    const int G = (int)(((w.n_blocks + 1) / 2 + 3) / 4);  // laps holding real blocks
+    const int G = (int)w.laps_per_tile();
     const size_t waves = w.n_tiles * (size_t)ns;
     size_t grid = (waves + TPW - 1) / TPW;
     if (ns > TPW) grid = (grid + 7) / 8 * 8;  // XCD-major mapping (whole waves past the end exit)
     hipLaunchKernelGGL((k_skinny_q8_0<AG, TPW, RL, DEBUG>),
                        dim3((unsigned)grid), dim3(TPW * kWave), 0, s,
-                       act, (int)m, (int)kp, sa_rows, reinterpret_cast<const v4i *>(w.tiles),
-                       reinterpret_cast<const v4i *>(w.scales), (int)w.n_out, (int)w.n_tiles, G,
+                       act, (int)m, (int)kp, sa_rows, reinterpret_cast<const v4i *>(w.laps),
+                       (int)w.n_out, (int)w.n_tiles, G,
                        (int)w.n_blocks, out, block_dots, ns);
 }
 
