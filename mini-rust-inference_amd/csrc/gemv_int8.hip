@@ -173,7 +173,7 @@ bool gemv_int8_supported(bool fused, size_t m, size_t n_tiles, size_t k, size_t 
 }
 
 bool gemv_fusable(size_t m, size_t k, const float *x) {
-    return m == 1 && k % 4 == 0 && x &&
+    return m == 1 && k > 0 && k % 4 == 0 && x &&
            (reinterpret_cast<uintptr_t>(x) & 15) == 0;
 }
 

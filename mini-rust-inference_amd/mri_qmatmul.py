@@ -261,6 +261,35 @@ def matmul_q8_0_direct(x, w: Q8Matrix, out, block_dots_out=None, act_scales_out=
                                        _stream(stream)))
 
 
+def bind_matmul_q8_0_direct(x, w: Q8Matrix, out, stream=None):
+    """matmul_q8_0_direct(x, w, out) with its C arguments converted once:
+    returns a callable that issues the call again on the stream current
+    now (for loops whose Python cost per call should stay small)."""
+    dims, nd = _dims(tuple(x.shape))
+    f = lib().mri_matmul_q8_0_direct
+    args = (_ptr(x), dims, nd, w.h, _ptr(out), None, None, _stream(stream))
+
+    def call():
+        rc = f(*args)
+        if rc != OK:
+            check(rc)
+    return call
+
+
+def bind_matmul_int8_from_f32(x, w: QMatrix, out, stream=None):
+    """matmul_int8_from_f32(x, w, out) with its C arguments converted once
+    (see bind_matmul_q8_0_direct)."""
+    dims, nd = _dims(tuple(x.shape))
+    f = lib().mri_matmul_int8_from_f32
+    args = (_ptr(x), dims, nd, w.h, _ptr(out), None, None, None, _stream(stream))
+
+    def call():
+        rc = f(*args)
+        if rc != OK:
+            check(rc)
+    return call
+
+
 def matmul_q4_0_dequant(x, weight_q4, n_out, k, out, stream=None, shape=None,
                         weight_len=None):
     dims, nd = _dims(tuple(x.shape) if shape is None else shape)

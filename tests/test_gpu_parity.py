@@ -362,6 +362,49 @@ def test_zero_sizes():
     M.synchronize()
 
 
+@pytest.mark.parametrize("m", [1, 3, 8])
+def test_zero_k(m):
+    """K = 0: every output is the empty sum, ((f32)0 * s_a) * s_w for INT8
+    and 0.0 for Q8_0 (no blocks), as the oracle computes it."""
+    t = torch()
+    M = mri()
+    n = 32
+    x = np.zeros((m, 0), F32)
+    xd = t.zeros((m, 0), dtype=t.float32, device="cuda")
+    w8 = M.Q8Matrix.from_raw_bytes(np.zeros(0, np.uint8), n, 0)
+    out = empty((m, n), t.float32)
+    out.fill_(7.0)
+    M.matmul_q8_0_direct(xd, w8, out)
+    assert_bits_equal(host(out), O.matmul_q8_0_direct(x, np.zeros(0, np.uint8), n, 0),
+                      "q8_0 k=0")
+    ws = np.linspace(0.5, 2.0, n).astype(F32)
+    wi = M.QMatrix.from_host(np.zeros((n, 0), np.int8), ws)
+    out2 = empty((m, n), t.float32)
+    out2.fill_(7.0)
+    M.matmul_int8_from_f32(xd, wi, out2)
+    ref = O.matmul_int8_from_f32(x, np.zeros((n, 0), np.int8), ws)[0]
+    assert_bits_equal(host(out2), ref, "int8 k=0")
+
+
+def test_bound_calls_match():
+    """The pre-bound call helpers issue the same entry points."""
+    t = torch()
+    M = mri()
+    rng = np.random.default_rng(9)
+    n, k = 272, 4096
+    raw = synth_q8_0(rng, n, k)
+    wq, ws = synth_int8_weights(rng, n, k)
+    x = dev(rng.standard_normal((1, k)).astype(F32))
+    w8, wi = M.Q8Matrix.from_raw_bytes(raw, n, k), M.QMatrix.from_host(wq, ws)
+    a, b = empty((1, n), t.float32), empty((1, n), t.float32)
+    M.matmul_q8_0_direct(x, w8, a)
+    M.bind_matmul_q8_0_direct(x, w8, b)()
+    assert_bits_equal(host(b), host(a), "bound q8_0")
+    M.matmul_int8_from_f32(x, wi, a)
+    M.bind_matmul_int8_from_f32(x, wi, b)()
+    assert_bits_equal(host(b), host(a), "bound int8")
+
+
 @pytest.mark.parametrize("m", [1, 3])
 def test_unfused_path_matches(m):
     """x at a 4-byte (not 16-byte) aligned address takes the two-kernel path
