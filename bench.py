@@ -26,7 +26,8 @@ projection shapes (M = 1), the skinny Q8_0 decode M in {4, 8, 16, 32}, the
 per-channel INT8 decode GEMV (matmul_int8_from_f32, M = 1), the INT8
 prefill GEMM over M in {128, 512, 2048} x N in {4096, 11008} on per-row
 quantized activations (matmul_int8 with per-row scales) and end to end from
-f32, the Q4_0 W4A32 decode GEMV, and the reference's rayon+AVX2
+f32, the Q4_0 W4A32 decode GEMV, the W4A8 extension's decode GEMV (Q4_0
+weights, int8 activations), and the reference's rayon+AVX2
 matmul_int8_parallel restatement on the INT8 decode shape (one core, as
 the reference: one row) and on a bounded row sample of the prefill shape
 (all cores).
@@ -206,6 +207,17 @@ def bench_q4(torch, M, T, m, n, k, steps, warmup, seed=3):
     out = torch.empty((m, n), device="cuda")
     return T.best_ms(lambda i: M.matmul_q4_0_dequant(x, raws[i], n, k, out), steps,
                      warmup, len(raws), out)[0]
+
+
+def bench_w4a8(torch, M, T, n, k, steps, warmup, seed=4):
+    """W4A8 extension: Q4_0 weights with int8 activations, M = 1."""
+    raws = [q4_raw_device(torch, n, k, seed + i) for i in range(copies_for(n * k // 32 * 18))]
+    ws = [M.Q4Matrix.from_raw_device(r, n, k) for r in raws]
+    del raws
+    x = torch.randn((1, k), device="cuda")
+    out = torch.empty((1, n), device="cuda")
+    return T.best_ms(lambda i: M.matmul_q4_0_w4a8(x, ws[i], out), steps, warmup, len(ws),
+                     out)[0]
 
 
 def bench_int8_decode(torch, M, T, n, k, steps, warmup, seed=5):
@@ -468,6 +480,12 @@ def main():
             "us": round(ms_q4 * 1e3, 2), "GB_s": round(gbs, 1),
             "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
         log(f"q4_0 decode: {ms_q4*1e3:.2f} us {gbs:.0f} GB/s")
+        ms_w4 = bench_w4a8(torch, M, T, 11008, 4096, steps2, args.warmup)
+        gbs = q4_bytes(1, 11008, 4096) / (ms_w4 * 1e-3) / 1e9
+        secondary["q4_0_w4a8_decode_1x4096x11008"] = {
+            "us": round(ms_w4 * 1e3, 2), "GB_s": round(gbs, 1),
+            "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+        log(f"q4_0 w4a8 decode: {ms_w4*1e3:.2f} us {gbs:.0f} GB/s")
 
         layer = {}
         for fmt in ("q8_0", "int8"):

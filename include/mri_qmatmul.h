@@ -171,6 +171,52 @@ mri_status mri_matmul_q4_0_dequant(const float *input, const size_t *dims,
                                    size_t weight_len, size_t n_out, size_t k,
                                    float *out, void *stream);
 
+/* ===================================================================== */
+/* Q4_0 with int8 activations (W4A8).  An extension with no counterpart   */
+/* in the reference: matmul_q8_0_direct's arithmetic                      */
+/* (src/ops/matmul/q8_direct.rs:229-289) on Q4_0 weights (quant = nibble  */
+/* - 8), for decode at half the Q8_0 weight bytes.  The reference-faithful */
+/* Q4_0 entry point remains mri_matmul_q4_0_dequant (W4A32).              */
+/* ===================================================================== */
+
+/* Nibble order of raw Q4_0 blocks: the reference's (create_q4_0_block,
+ * src/gguf/dequant.rs:706-749: element 2i = low nibble of byte i, 2i+1 =
+ * high nibble) or upstream GGML's (element i = low nibble of byte i,
+ * element i + 16 = high nibble), as in llama.cpp Q4_0 files. */
+typedef enum {
+    MRI_Q4_ORDER_INTERLEAVED = 0,
+    MRI_Q4_ORDER_GGML = 1,
+} mri_q4_order;
+
+/* Uploads raw Q4_0 blocks ([f16 d][16 bytes], 18 bytes, block (n,b) at
+ * (n*k_in/32 + b)*18) in nibble order `order`.  InvalidShape when
+ * k_in % 32 != 0 or len != n_out*(k_in/32)*18; InvalidArgument for an
+ * unknown order.  _bytes takes a host pointer, _device a device pointer. */
+typedef struct mri_q4_0_matrix mri_q4_0_matrix;
+mri_status mri_q4_0_matrix_from_raw_bytes(const uint8_t *data, size_t len,
+                                          size_t n_out, size_t k_in, int order,
+                                          mri_q4_0_matrix **out);
+mri_status mri_q4_0_matrix_from_raw_device(const uint8_t *data_dev, size_t len,
+                                           size_t n_out, size_t k_in, int order,
+                                           void *stream, mri_q4_0_matrix **out);
+size_t mri_q4_0_matrix_n_out(const mri_q4_0_matrix *w);
+size_t mri_q4_0_matrix_k_in(const mri_q4_0_matrix *w);
+size_t mri_q4_0_matrix_device_bytes(const mri_q4_0_matrix *w);
+void mri_q4_0_matrix_destroy(mri_q4_0_matrix *w);
+
+/* Per-row quantize_symmetric of `input` [m,k] (src/quant/int8/symmetric.rs:
+ * 42-57), per-block exact int32 dots with the quants, and
+ *   out[m,n] = sum over b in block order of ((f32)dot[m,n,b]*s_a[m])*d[n,b],
+ * i.e. mri_matmul_q8_0_direct on the blocks with quants nibble - 8.
+ * InvalidShape unless ndim == 2; ShapeMismatch when dims[1] != k_in;
+ * Unsupported when k_in > 12288 (the kernel stages up to four activation
+ * rows in LDS).  Optional outputs (nullable, device):
+ * block_dots_out [m, n_out, k_in/32] int32, act_scales_out [m]. */
+mri_status mri_matmul_q4_0_w4a8(const float *input, const size_t *dims, size_t ndim,
+                                const mri_q4_0_matrix *w, float *out,
+                                int32_t *block_dots_out, float *act_scales_out,
+                                void *stream);
+
 /* Waits for all work enqueued on `stream`. */
 mri_status mri_synchronize(void *stream);
 

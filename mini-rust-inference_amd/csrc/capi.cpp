@@ -21,6 +21,9 @@ struct mri_qmatrix {
 struct mri_q8_0_matrix {
     mri::Q8MatrixDev d;
 };
+struct mri_q4_0_matrix {
+    mri::Q8MatrixDev d;  // w4: Q4_0 lap blocks
+};
 
 namespace mri {
 
@@ -159,7 +162,18 @@ static mri_status run_q8(const int8_t *act, size_t m, const float *sa_rows,
                          hipStream_t s) {
     if (gemv_q8_supported(false, m, w.n_tiles, w.k_in, w.kp))
         return launch_gemv_q8_0(nullptr, act, m, sa_rows, w, out, block_dots, nullptr, s);
-    return launch_skinny_q8_0(act, m, sa_rows, w, out, block_dots, s);
+    if (!w.w4) return launch_skinny_q8_0(act, m, sa_rows, w, out, block_dots, s);
+    // W4A8 above 4 rows: the GEMV on 4-row slices
+    for (size_t r0 = 0; r0 < m; r0 += kMaxGemvRows) {
+        const size_t mm = std::min(kMaxGemvRows, m - r0);
+        if (!gemv_q8_supported(false, mm, w.n_tiles, w.k_in, w.kp))
+            return set_error(MRI_ERR_UNSUPPORTED, "matmul_q4_0_w4a8: shape not supported");
+        mri_status st = launch_gemv_q8_0(
+            nullptr, act + r0 * w.kp, mm, sa_rows + r0, w, out + r0 * w.n_out,
+            block_dots ? block_dots + r0 * w.n_out * w.n_blocks : nullptr, nullptr, s);
+        if (st) return st;
+    }
+    return MRI_OK;
 }
 
 // Returns act rows with pitch w.kp: the caller's buffer when it already has
@@ -413,6 +427,81 @@ void mri_q8_0_matrix_destroy(mri_q8_0_matrix *w) {
     delete w;
 }
 
+mri_status mri_q4_0_matrix_from_raw_device(const uint8_t *data_dev, size_t len, size_t n_out,
+                                           size_t k_in, int order, void *stream,
+                                           mri_q4_0_matrix **out) {
+    if (!out) return set_error(MRI_ERR_INVALID_ARGUMENT, "out is null");
+    *out = nullptr;
+    if (order != MRI_Q4_ORDER_INTERLEAVED && order != MRI_Q4_ORDER_GGML)
+        return set_error(MRI_ERR_INVALID_ARGUMENT, fmt("unknown Q4_0 nibble order %d", order));
+    if (k_in % kQK)
+        return set_error(MRI_ERR_INVALID_SHAPE,
+                         fmt("Q4_0 weights: k_in=%zu is not a multiple of 32", k_in));
+    const size_t expected = n_out * (k_in / kQK) * kQ4Bytes;
+    if (len != expected)
+        return set_error(MRI_ERR_INVALID_SHAPE,
+                         fmt("Q4_0 weights: data.len()=%zu != expected %zu", len, expected));
+    if (len && !data_dev) return set_error(MRI_ERR_INVALID_ARGUMENT, "data is null");
+    int dev;
+    mri_status st = current_device(&dev);
+    if (st) return st;
+    auto *h = new mri_q4_0_matrix();
+    Q8MatrixDev &d = h->d;
+    d.n_out = n_out;
+    d.k_in = k_in;
+    d.n_blocks = k_in / kQK;
+    d.n_tiles = (n_out + kTileN - 1) / kTileN;
+    d.kp = round_up(k_in ? k_in : 1, kQ8LapK);
+    d.device = dev;
+    d.w4 = true;
+    const hipError_t e = hipMalloc(&d.laps, d.bytes() + 256);
+    if (e != hipSuccess) st = hip_error(e, "hipMalloc");
+    if (!st)
+        st = launch_repack_q4_0(data_dev, order == MRI_Q4_ORDER_GGML, d,
+                                static_cast<hipStream_t>(stream));
+    if (st) {
+        mri_q4_0_matrix_destroy(h);
+        return st;
+    }
+    *out = h;
+    return MRI_OK;
+}
+
+mri_status mri_q4_0_matrix_from_raw_bytes(const uint8_t *data, size_t len, size_t n_out,
+                                          size_t k_in, int order, mri_q4_0_matrix **out) {
+    if (!out) return set_error(MRI_ERR_INVALID_ARGUMENT, "out is null");
+    *out = nullptr;
+    if (len && !data) return set_error(MRI_ERR_INVALID_ARGUMENT, "data is null");
+    int dev;
+    mri_status st = current_device(&dev);
+    if (st) return st;
+    uint8_t *dd = nullptr;
+    MRI_HIP(hipMalloc(&dd, len + 16));
+    hipError_t e = hipMemcpy(dd, data, len, hipMemcpyHostToDevice);
+    if (e != hipSuccess) st = hip_error(e, "hipMemcpy");
+    if (!st) st = mri_q4_0_matrix_from_raw_device(dd, len, n_out, k_in, order, nullptr, out);
+    if (!st) {
+        e = hipStreamSynchronize(nullptr);
+        if (e != hipSuccess) st = hip_error(e, "hipStreamSynchronize");
+    }
+    (void)hipFree(dd);
+    if (st && *out) {
+        mri_q4_0_matrix_destroy(*out);
+        *out = nullptr;
+    }
+    return st;
+}
+
+size_t mri_q4_0_matrix_n_out(const mri_q4_0_matrix *w) { return w ? w->d.n_out : 0; }
+size_t mri_q4_0_matrix_k_in(const mri_q4_0_matrix *w) { return w ? w->d.k_in : 0; }
+size_t mri_q4_0_matrix_device_bytes(const mri_q4_0_matrix *w) { return w ? w->d.bytes() : 0; }
+
+void mri_q4_0_matrix_destroy(mri_q4_0_matrix *w) {
+    if (!w) return;
+    if (w->d.laps) (void)hipFree(w->d.laps);
+    delete w;
+}
+
 }  // extern "C"
 
 namespace mri {
@@ -656,17 +745,18 @@ mri_status mri_matmul_int8_from_f32(const float *input, const size_t *dims, size
     return run_int8(act, m, scale, 0, 0.0f, d, out, acc_out, s);
 }
 
-mri_status mri_matmul_q8_0_direct(const float *input, const size_t *dims, size_t ndim,
-                                  const mri_q8_0_matrix *w, float *out,
-                                  int32_t *block_dots_out, float *act_scales_out,
-                                  void *stream) {
-    if (!w) return set_error(MRI_ERR_INVALID_ARGUMENT, "null weight handle");
+}  // extern "C"
+
+// matmul_q8_0_direct's body, shared with the W4A8 entry point (d.w4).
+static mri_status matmul_blocks(const char *name, const float *input, const size_t *dims,
+                                size_t ndim, const Q8MatrixDev &d, float *out,
+                                int32_t *block_dots_out, float *act_scales_out,
+                                void *stream) {
     if (ndim && !dims) return set_error(MRI_ERR_INVALID_ARGUMENT, "dims is null");
     if (ndim != 2)
         return set_error(MRI_ERR_INVALID_SHAPE,
-                         fmt("matmul_q8_0_direct: input must be 2-D, got %zuD (shape %s)",
-                             ndim, dims_str(dims, ndim).c_str()));
-    const Q8MatrixDev &d = w->d;
+                         fmt("%s: input must be 2-D, got %zuD (shape %s)", name, ndim,
+                             dims_str(dims, ndim).c_str()));
     const size_t m = dims[0], k = dims[1];
     if (k != d.k_in)
         return set_error(MRI_ERR_SHAPE_MISMATCH,
@@ -696,6 +786,29 @@ mri_status mri_matmul_q8_0_direct(const float *input, const size_t *dims, size_t
     if (st) return st;
     if (d.n_out == 0) return MRI_OK;
     return run_q8(act, m, sc, d, out, block_dots_out, s);
+}
+
+extern "C" {
+
+mri_status mri_matmul_q8_0_direct(const float *input, const size_t *dims, size_t ndim,
+                                  const mri_q8_0_matrix *w, float *out,
+                                  int32_t *block_dots_out, float *act_scales_out,
+                                  void *stream) {
+    if (!w) return set_error(MRI_ERR_INVALID_ARGUMENT, "null weight handle");
+    return matmul_blocks("matmul_q8_0_direct", input, dims, ndim, w->d, out, block_dots_out,
+                         act_scales_out, stream);
+}
+
+mri_status mri_matmul_q4_0_w4a8(const float *input, const size_t *dims, size_t ndim,
+                                const mri_q4_0_matrix *w, float *out,
+                                int32_t *block_dots_out, float *act_scales_out,
+                                void *stream) {
+    if (!w) return set_error(MRI_ERR_INVALID_ARGUMENT, "null weight handle");
+    if (w->d.k_in > kMaxW4a8K)
+        return set_error(MRI_ERR_UNSUPPORTED,
+                         fmt("matmul_q4_0_w4a8: k_in=%zu exceeds %zu", w->d.k_in, kMaxW4a8K));
+    return matmul_blocks("matmul_q4_0_w4a8", input, dims, ndim, w->d, out, block_dots_out,
+                         act_scales_out, stream);
 }
 
 mri_status mri_matmul_q4_0_dequant(const float *input, const size_t *dims, size_t ndim,

@@ -29,6 +29,17 @@
 //       row r at byte 4096 + 16 r holds the scales of blocks 8q .. 8q+7, so
 //       one 16-byte load gives a lane the scales of its 4 chunks.
 //
+//  * Q4_0 for the W4A8 path (an extension) uses the same lap blocks with
+//    4-bit quants, 2304 bytes each: 2 KiB of quants, then the 256 bytes of
+//    f16 scales at byte 2048.  Quant piece u (0..1) of lane l is 16 bytes at
+//    byte (u * 64 + l) * 16: u32 word 2c' + h (c' = 0..1) holds the quants
+//    of block 2p + h, p = 4q + 2u + c', that lane l's MFMA B operand needs
+//    (elements 8g .. 8g+7, g = l / 16, row 16T + l % 16): byte i has element
+//    8g + i in its low nibble and element 8g + 4 + i in its high nibble.
+//    Each nibble holds the raw GGUF nibble XOR 8, which is the 4-bit two's
+//    complement of the quant (nibble - 8), so that a nibble moved to the
+//    high half of a byte reads as the int8 16 * quant.
+//
 //  * Activations quantized by the library are written to a per-(device,
 //    stream) scratch in [M][Kp] int8 rows (zero padded).  For Q8_0 the 64
 //    bytes of each chunk are permuted to match the weight chunk:
@@ -77,17 +88,21 @@ struct QMatrixDev {
 };
 
 constexpr int kQ8LapBytes = 4352;  // one Q8_0 lap block: 4 chunks + 256 bytes of scales
+constexpr int kQ4LapBytes = 2304;  // one Q4_0 (W4A8) lap block: 2 KiB of nibbles + scales
 constexpr int kQ8LapK = 256;       // K elements per lap block
 
+// Q8_0 weights, or Q4_0 weights for the W4A8 path (w4).
 struct Q8MatrixDev {
     size_t n_out = 0, k_in = 0;
     size_t n_blocks = 0;    // k_in / 32
     size_t n_tiles = 0;
     size_t kp = 0;          // K padded to 256
-    int8_t *laps = nullptr;  // n_tiles * (kp/256) lap blocks of 4352 bytes
+    int8_t *laps = nullptr;  // n_tiles * (kp/256) lap blocks
     int device = 0;
+    bool w4 = false;
     size_t laps_per_tile() const { return kp / kQ8LapK; }
-    size_t bytes() const { return n_tiles * laps_per_tile() * kQ8LapBytes; }
+    size_t lap_bytes() const { return w4 ? kQ4LapBytes : kQ8LapBytes; }
+    size_t bytes() const { return n_tiles * laps_per_tile() * lap_bytes(); }
 };
 
 // Exact f16 -> f32 decode (v_cvt_f32_f16), the f16_to_f32 of
@@ -149,6 +164,10 @@ mri_status launch_repack_int8(const int8_t *data, const float *scales,
                               QMatrixDev &w, hipStream_t s);
 mri_status launch_repack_q8_0(const uint8_t *raw, Q8MatrixDev &w,
                               hipStream_t s);
+// Raw Q4_0 blocks (ggml_order: low nibbles = elements 0..15; else the
+// reference's interleaved order) into W4A8 lap blocks (w.w4).
+mri_status launch_repack_q4_0(const uint8_t *raw, bool ggml_order, Q8MatrixDev &w,
+                              hipStream_t s);
 
 // skinny.hip: M <= 32 rows per launch (larger M loops), one wave per tile.
 // act: [M][kp] int8 (Q8_0: chunk-permuted).  Activation scale of row m is
@@ -166,6 +185,8 @@ mri_status launch_skinny_q8_0(const int8_t *act, size_t m,
 // x (quantized in the kernel; requires gemv_fusable, M == 1; optional
 // act_q_out [k] and scale_out [1]) or as quantized rows act [m][kp] (Q8_0:
 // chunk-permuted) with their scales.
+constexpr size_t kMaxGemvRows = 4;     // rows of one GEMV launch
+constexpr size_t kMaxW4a8K = 12288;    // K of the W4A8 path (activation rows in LDS)
 bool gemv_int8_supported(bool fused, size_t m, size_t n_tiles, size_t k, size_t kp);
 bool gemv_q8_supported(bool fused, size_t m, size_t n_tiles, size_t k, size_t kp);
 bool gemv_fusable(size_t m, size_t k, const float *x);

@@ -8,7 +8,9 @@ using namespace gemv;
 namespace {
 
 // ---------------------------------------------------------------------------
-// Q8_0.  One v_mfma_i32_16x16x64_i8 per chunk computes both of its blocks:
+// Q8_0 (and, with W4, Q4_0 weights for the W4A8 path: the same computation
+// on 4-bit quants).  One v_mfma_i32_16x16x64_i8 per chunk computes both of
+// its blocks:
 // A row m = 2*row + h carries activation row `row` restricted to block
 // 2p + h (the other 8 bytes of the lane's 16 are zeroed; the weight chunk
 // keeps both blocks), so result register i of lane group g holds the exact
@@ -28,6 +30,12 @@ namespace {
 // round's remaining S-1 laps in block order.  The f32 result is therefore
 // bit-identical to the sequential reference, and only the last round's
 // terms remain to be added after the sweep.
+//
+// W4: a lap's quants are two 16-byte loads per lane instead of four; the B
+// operand of a chunk is unpacked from two u32 words by moving each nibble
+// to the high half of its byte, which gives 16 * quant as int8 (the stored
+// nibble is the quant's 4-bit two's complement), so the MFMA's int32 result
+// is 16 times the block dot and an arithmetic shift by 4 recovers it.
 // ---------------------------------------------------------------------------
 
 // Barrier for LDS traffic only: waits for this wave's LDS operations, not
@@ -36,7 +44,7 @@ __device__ inline void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-template <int MR, int S, int TPW, int RL, int XR, bool FUSED, bool DEBUG>
+template <int MR, int S, int TPW, int RL, int XR, bool FUSED, bool DEBUG, bool W4>
 __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     ActIn in, int M, int kp, const float *__restrict__ sa_rows,
     const v4i *__restrict__ laps, int N, int n_tiles, int G, int nb, float *__restrict__ out,
@@ -57,11 +65,13 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     const int r = l & 15, g = l >> 4;
     const int NR = (G + S - 1) / S;           // rounds
     const int nq = tile_ok && w < G ? (G - w + S - 1) / S : 0;  // laps of this wave
-    // lap block q of the tile: chunk s at v4i offset s * 64 (+ lane), its
-    // scales at 256 (+ row)
-    const v4i *wp = laps + (size_t)Tc * G * (kQ8LapBytes / 16) + l;
-    const v4i *sp = laps + (size_t)Tc * G * (kQ8LapBytes / 16) + 256 + r;
-    constexpr size_t LB = kQ8LapBytes / 16;
+    // lap block q of the tile: quant piece s at v4i offset s * 64 (+ lane),
+    // its scales at SO (+ row)
+    constexpr size_t LB = (W4 ? kQ4LapBytes : kQ8LapBytes) / 16;
+    constexpr int SO = W4 ? 128 : 256;
+    constexpr int NP = W4 ? 2 : 4;            // quant pieces per lap and lane
+    const v4i *wp = laps + (size_t)Tc * G * LB + l;
+    const v4i *sp = laps + (size_t)Tc * G * LB + SO + r;
     const int n = T * 16 + r;
 
     // LDS: [act M*kp][red NW floats][terms 2 x TPW x (S-1) x LG x 16 x TW floats]
@@ -101,7 +111,7 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     for (int u = 0; u < RL; ++u) {
         const int q = min(min(u, max(nq - 1, 0)) * S + w, G - 1);
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
+        for (int s = 0; s < NP; ++s)
             wr[u][s] = __builtin_nontemporal_load(wp + (size_t)q * LB + s * 64);
         sr[u] = sp[(size_t)q * LB];
     }
@@ -156,12 +166,22 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             const v4i am = {a[s].x & mlo, a[s].y & mlo, a[s].z & mhi, a[s].w & mhi};
-            const v4i d =
-                __builtin_amdgcn_mfma_i32_16x16x64_i8(am, wr[U][s], v4i{0, 0, 0, 0}, 0, 0, 0);
+            v4i bw;
+            if constexpr (W4) {
+                const v4i pc = wr[U][s >> 1];
+                const int w0 = (s & 1) ? pc.z : pc.x, w1 = (s & 1) ? pc.w : pc.y;
+                constexpr int kHi = (int)0xF0F0F0F0u;
+                bw = v4i{(w0 << 4) & kHi, w0 & kHi, (w1 << 4) & kHi, w1 & kHi};
+            } else {
+                bw = wr[U][s];
+            }
+            const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(am, bw, v4i{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
-            for (int i = 0; i < 2 * LR; ++i) dt[s][i] = d[i];
-            if (refill)
-                wr[U][s] = __builtin_nontemporal_load(wp + (size_t)(q + RL * S) * LB + s * 64);
+            for (int i = 0; i < 2 * LR; ++i) dt[s][i] = W4 ? d[i] >> 4 : d[i];
+            if (refill && (!W4 || (s & 1))) {
+                const int pi = W4 ? s >> 1 : s;
+                wr[U][pi] = __builtin_nontemporal_load(wp + (size_t)(q + RL * S) * LB + pi * 64);
+            }
         }
         float tv[LR][8];
 #pragma unroll
@@ -271,11 +291,11 @@ CfgQ8 pick_q8(bool fused, size_t n_tiles, size_t m, size_t k, size_t kp, size_t 
 
 inline size_t groups_of(const Q8MatrixDev &w) { return w.laps_per_tile(); }
 
-template <int MR, int S, int TPW, int RL, int XR, bool FUSED, bool DEBUG>
+template <int MR, int S, int TPW, int RL, int XR, bool FUSED, bool DEBUG, bool W4>
 void launch_q8(ActIn in, size_t m, const float *sa_rows, const Q8MatrixDev &w,
                float *out, int32_t *block_dots, hipStream_t st) {
     const size_t G = groups_of(w);
-    hipLaunchKernelGGL((k_gemv_q8_0<MR, S, TPW, RL, XR, FUSED, DEBUG>),
+    hipLaunchKernelGGL((k_gemv_q8_0<MR, S, TPW, RL, XR, FUSED, DEBUG, W4>),
                        dim3((unsigned)ceil_div(w.n_tiles, TPW)), dim3(S * TPW * kWave),
                        lds_q8(S, TPW, m, w.kp, G), st, in, (int)m, (int)w.kp, sa_rows,
                        reinterpret_cast<const v4i *>(w.laps), (int)w.n_out,
@@ -285,10 +305,12 @@ void launch_q8(ActIn in, size_t m, const float *sa_rows, const Q8MatrixDev &w,
 template <int MR, bool FUSED, bool DEBUG>
 void dispatch_q8(CfgQ8 c, ActIn in, size_t m, const float *sa_rows, const Q8MatrixDev &w,
                  float *out, int32_t *block_dots, hipStream_t st) {
-#define MRI_Q8(S_, TPW_, RL_, XR_)                                                        \
-    if (c.s == S_ && c.tpw == TPW_ && c.rl == RL_ && c.xr == XR_)                         \
-        return launch_q8<MR, S_, TPW_, RL_, XR_, FUSED, DEBUG>(in, m, sa_rows, w, out,    \
-                                                               block_dots, st);
+#define MRI_Q8(S_, TPW_, RL_, XR_)                                                         \
+    if (c.s == S_ && c.tpw == TPW_ && c.rl == RL_ && c.xr == XR_)                          \
+        return w.w4 ? launch_q8<MR, S_, TPW_, RL_, XR_, FUSED, DEBUG, true>(               \
+                          in, m, sa_rows, w, out, block_dots, st)                          \
+                    : launch_q8<MR, S_, TPW_, RL_, XR_, FUSED, DEBUG, false>(              \
+                          in, m, sa_rows, w, out, block_dots, st);
     MRI_Q8(4, 1, 1, 4) MRI_Q8(4, 1, 1, 12)
     MRI_Q8(4, 1, 2, 4) MRI_Q8(4, 1, 2, 12)
 #undef MRI_Q8

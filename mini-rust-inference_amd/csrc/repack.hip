@@ -62,27 +62,71 @@ __global__ __launch_bounds__(kThreads) void k_repack_q8_quants(
     }
 }
 
-// One thread per (lap block, row): the row's 8 f16 scales of the lap.
-__global__ __launch_bounds__(kThreads) void k_repack_q8_scales(
+// One thread per (lap block, row): the row's 8 f16 scales of the lap
+// (raw blocks of block_bytes, lap blocks of lap_bytes, scales at scale_off).
+__global__ __launch_bounds__(kThreads) void k_repack_scales(
     const uint8_t *__restrict__ raw, size_t n, size_t nb, size_t G, size_t total,
-    int8_t *__restrict__ laps) {
+    int block_bytes, int lap_bytes, int scale_off, int8_t *__restrict__ laps) {
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
          e += stride) {
         const size_t r = e & 15, lb = e >> 4;
         const size_t T = lb / G, q = lb - T * G;
         const size_t row = T * kTileN + r;
-        uint16_t *dst = reinterpret_cast<uint16_t *>(laps + lb * kQ8LapBytes + 4096 + r * 16);
+        uint16_t *dst =
+            reinterpret_cast<uint16_t *>(laps + lb * lap_bytes + scale_off + r * 16);
 #pragma unroll
         for (int j = 0; j < kQ8ScaleGroup; ++j) {
             const size_t b = q * kQ8ScaleGroup + j;
             uint16_t d = 0;
             if (row < n && b < nb) {
-                const uint8_t *src = raw + (row * nb + b) * kQ8Bytes;
+                const uint8_t *src = raw + (row * nb + b) * block_bytes;
                 d = (uint16_t)(src[0] | (src[1] << 8));
             }
             dst[j] = d;
         }
+    }
+}
+
+// One thread per 16-byte quant piece of the W4A8 lap blocks: piece
+// e = (lap block, u, lane).  Word 2c' + h of the piece holds block
+// b = 2p + h, p = 4q + 2u + c': byte i = element 8g + i (low nibble) and
+// element 8g + 4 + i (high nibble), each as raw nibble ^ 8.  Missing rows
+// and blocks past nb are quant 0 (stored 0).
+__global__ __launch_bounds__(kThreads) void k_repack_q4_quants(
+    const uint8_t *__restrict__ raw, size_t n, size_t nb, size_t G, size_t total,
+    int ggml, int8_t *__restrict__ laps) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += stride) {
+        const size_t lane = e & 63, u = (e >> 6) & 1, lb = e >> 7;
+        const size_t T = lb / G, q = lb - T * G;
+        const size_t row = T * kTileN + (lane & 15);
+        const int g = (int)(lane >> 4);
+        uint32_t words[4];
+#pragma unroll
+        for (int wd = 0; wd < 4; ++wd) {
+            const size_t p = 4 * q + 2 * u + (wd >> 1);
+            const size_t b = 2 * p + (wd & 1);
+            uint32_t v = 0;
+            if (row < n && b < nb) {
+                const uint8_t *qs = raw + (row * nb + b) * kQ4Bytes + 2;
+                auto nib = [&](int el) -> uint32_t {  // raw nibble of element el
+                    const int byte = ggml ? (el & 15) : (el >> 1);
+                    const int hi = ggml ? (el >> 4) : (el & 1);
+                    return (uint32_t)((qs[byte] >> (4 * hi)) & 0x0F);
+                };
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t lo = nib(8 * g + i) ^ 8u, hi = nib(8 * g + 4 + i) ^ 8u;
+                    v |= (lo | (hi << 4)) << (8 * i);
+                }
+            }
+            words[wd] = v;
+        }
+        uint32_t *dst = reinterpret_cast<uint32_t *>(laps + lb * kQ4LapBytes + (u * 64 + lane) * 16);
+#pragma unroll
+        for (int wd = 0; wd < 4; ++wd) dst[wd] = words[wd];
     }
 }
 
@@ -123,9 +167,27 @@ mri_status launch_repack_q8_0(const uint8_t *raw, Q8MatrixDev &w,
                            w.laps);
         MRI_LAUNCHED("k_repack_q8_quants");
         const size_t rows = w.n_tiles * G * kTileN;
-        hipLaunchKernelGGL(k_repack_q8_scales, dim3(grid_for(rows)), dim3(kThreads), 0, s,
-                           raw, w.n_out, w.n_blocks, G, rows, w.laps);
-        MRI_LAUNCHED("k_repack_q8_scales");
+        hipLaunchKernelGGL(k_repack_scales, dim3(grid_for(rows)), dim3(kThreads), 0, s,
+                           raw, w.n_out, w.n_blocks, G, rows, kQ8Bytes, kQ8LapBytes, 4096,
+                           w.laps);
+        MRI_LAUNCHED("k_repack_scales");
+    }
+    return MRI_OK;
+}
+
+mri_status launch_repack_q4_0(const uint8_t *raw, bool ggml_order, Q8MatrixDev &w,
+                              hipStream_t s) {
+    const size_t G = w.laps_per_tile();
+    const size_t pieces = w.n_tiles * G * 128;
+    if (pieces) {
+        hipLaunchKernelGGL(k_repack_q4_quants, dim3(grid_for(pieces)), dim3(kThreads), 0, s,
+                           raw, w.n_out, w.n_blocks, G, pieces, ggml_order ? 1 : 0, w.laps);
+        MRI_LAUNCHED("k_repack_q4_quants");
+        const size_t rows = w.n_tiles * G * kTileN;
+        hipLaunchKernelGGL(k_repack_scales, dim3(grid_for(rows)), dim3(kThreads), 0, s,
+                           raw, w.n_out, w.n_blocks, G, rows, kQ4Bytes, kQ4LapBytes, 2048,
+                           w.laps);
+        MRI_LAUNCHED("k_repack_scales");
     }
     return MRI_OK;
 }

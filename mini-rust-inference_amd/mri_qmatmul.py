@@ -55,6 +55,13 @@ _SIGS = {
     "mri_matmul_int8_from_f32": ([P, P, SZ, P, P, P, P, P, P], ST),
     "mri_matmul_q8_0_direct": ([P, P, SZ, P, P, P, P, P], ST),
     "mri_matmul_q4_0_dequant": ([P, P, SZ, P, SZ, SZ, SZ, P, P], ST),
+    "mri_q4_0_matrix_from_raw_bytes": ([P, SZ, SZ, SZ, C.c_int, C.POINTER(P)], ST),
+    "mri_q4_0_matrix_from_raw_device": ([P, SZ, SZ, SZ, C.c_int, P, C.POINTER(P)], ST),
+    "mri_q4_0_matrix_n_out": ([P], SZ),
+    "mri_q4_0_matrix_k_in": ([P], SZ),
+    "mri_q4_0_matrix_device_bytes": ([P], SZ),
+    "mri_q4_0_matrix_destroy": ([P], None),
+    "mri_matmul_q4_0_w4a8": ([P, P, SZ, P, P, P, P, P], ST),
     "mri_synchronize": ([P], ST),
 }
 
@@ -210,6 +217,51 @@ class Q8Matrix:
             pass
 
 
+Q4_ORDER_INTERLEAVED, Q4_ORDER_GGML = 0, 1
+
+
+class Q4Matrix:
+    """Q4_0 weights for the W4A8 extension (matmul_q4_0_w4a8), from raw
+    18-byte blocks in the reference's interleaved nibble order or in
+    upstream GGML's (Q4_ORDER_GGML)."""
+
+    def __init__(self, handle, n_out, k_in):
+        self.h = handle
+        self.n_out = n_out
+        self.k_in = k_in
+
+    @classmethod
+    def from_raw_bytes(cls, raw, n_out, k_in, order=Q4_ORDER_INTERLEAVED):
+        import numpy as np
+        raw = np.ascontiguousarray(raw, dtype=np.uint8)
+        h = C.c_void_p()
+        check(lib().mri_q4_0_matrix_from_raw_bytes(raw.ctypes.data_as(P), raw.size, n_out,
+                                                   k_in, order, C.byref(h)))
+        return cls(h, n_out, k_in)
+
+    @classmethod
+    def from_raw_device(cls, raw, n_out, k_in, order=Q4_ORDER_INTERLEAVED, stream=None):
+        h = C.c_void_p()
+        check(lib().mri_q4_0_matrix_from_raw_device(_ptr(raw), raw.numel(), n_out, k_in,
+                                                    order, _stream(stream), C.byref(h)))
+        return cls(h, n_out, k_in)
+
+    @property
+    def device_bytes(self):
+        return lib().mri_q4_0_matrix_device_bytes(self.h)
+
+    def close(self):
+        if self.h:
+            lib().mri_q4_0_matrix_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 # ---------------------------------------------------------------------------
 # entry points (torch device tensors in/out)
 # ---------------------------------------------------------------------------
@@ -259,6 +311,13 @@ def matmul_q8_0_direct(x, w: Q8Matrix, out, block_dots_out=None, act_scales_out=
     check(lib().mri_matmul_q8_0_direct(_ptr(x), dims, nd, w.h, _ptr(out),
                                        _ptr(block_dots_out), _ptr(act_scales_out),
                                        _stream(stream)))
+
+
+def matmul_q4_0_w4a8(x, w: Q4Matrix, out, block_dots_out=None, act_scales_out=None,
+                     stream=None, shape=None):
+    dims, nd = _dims(tuple(x.shape) if shape is None else shape)
+    check(lib().mri_matmul_q4_0_w4a8(_ptr(x), dims, nd, w.h, _ptr(out), _ptr(block_dots_out),
+                                     _ptr(act_scales_out), _stream(stream)))
 
 
 def bind_matmul_q8_0_direct(x, w: Q8Matrix, out, stream=None):

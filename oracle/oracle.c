@@ -27,6 +27,11 @@
  *                             doctest :453-470, :1246-1290
  *   orc_matmul_q4_0_dequant   sequential float32 restatement (numpy) + KATs
  *                             q4_0.rs:214-390
+ *   orc_matmul_q4_0_w4a8      (extension, no reference counterpart) equals
+ *                             orc_matmul_q8_0_direct on the same blocks
+ *                             expanded to Q8_0 (bit for bit); GGML order
+ *                             equals the interleaved order on byte-permuted
+ *                             blocks; int64 block dots (numpy)
  */
 #define _GNU_SOURCE
 #include "oracle.h"
@@ -583,5 +588,69 @@ int orc_matmul_q4_0_dequant(const float *input, const size_t *dims,
             out[mi * n_out + n] = acc;
         }
     }
+    return ORC_OK;
+}
+
+/* Quant e (0..31) of a Q4_0 block as a signed value nibble - 8, in either
+ * nibble order: ORC_Q4_INTERLEAVED (the reference's create_q4_0_block,
+ * gguf/dequant.rs:706-749 and q4_0.rs:59-68: element 2i = low nibble of byte
+ * i, 2i+1 = high nibble) or ORC_Q4_GGML (upstream GGML: element i < 16 = low
+ * nibble of byte i, element i + 16 = high nibble of byte i). */
+static int q4_quant(const uint8_t *blk, int e, int order) {
+    int byte, hi;
+    if (order == ORC_Q4_GGML) {
+        byte = e & 15;
+        hi = e >> 4;
+    } else {
+        byte = e >> 1;
+        hi = e & 1;
+    }
+    const int nib = hi ? (blk[2 + byte] >> 4) & 0x0F : blk[2 + byte] & 0x0F;
+    return nib - 8;
+}
+
+/* Q4_0 weights with int8 activations (W4A8).  An extension with no
+ * counterpart in the reference: matmul_q8_0_direct (q8_direct.rs:229-289)
+ * applied to Q4_0 blocks.  Per row, quantize_symmetric of the row
+ * (symmetric.rs:42-57); per output and block, the exact int32 dot of the
+ * int8 activations with the quants (nibble - 8), then
+ * acc += ((f32)dot * s_a) * d in block order.  Error order as
+ * matmul_q4_0_dequant: non-2-D, K mismatch, K%32, byte length. */
+int orc_matmul_q4_0_w4a8(const float *input, const size_t *dims, size_t ndim,
+                         const uint8_t *w_q4, size_t n_bytes, size_t n_out, size_t k,
+                         int order, float *out, int32_t *block_dots_out,
+                         float *act_scales_out) {
+    if (ndim != 2)
+        return fail(ORC_INVALID_SHAPE, "matmul_q4_0_w4a8: input must be 2-D, got %zuD", ndim);
+    size_t m = dims[0], k_in = dims[1];
+    if (k_in != k)
+        return fail(ORC_SHAPE_MISMATCH, "expected [%zu, %zu], got [%zu, %zu]", m, k, m, k_in);
+    if (k % ORC_QK)
+        return fail(ORC_INVALID_SHAPE, "matmul_q4_0_w4a8: k=%zu is not a multiple of 32", k);
+    size_t nb = k / ORC_QK, expected = n_out * nb * ORC_Q4_0_BLOCK_BYTES;
+    if (n_bytes != expected)
+        return fail(ORC_INVALID_SHAPE, "matmul_q4_0_w4a8: weight_q4 has %zu bytes, expected %zu",
+                    n_bytes, expected);
+    int8_t *aq = (int8_t *)malloc(k + 1);
+    for (size_t mi = 0; mi < m; mi++) {
+        float s_a = orc_quantize_symmetric(input + mi * k, k, aq);
+        if (act_scales_out) act_scales_out[mi] = s_a;
+        for (size_t ni = 0; ni < n_out; ni++) {
+            float acc = 0.0f;
+            for (size_t b = 0; b < nb; b++) {
+                const uint8_t *blk = w_q4 + (ni * nb + b) * ORC_Q4_0_BLOCK_BYTES;
+                float d = orc_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+                int32_t dot = 0;
+                for (int e = 0; e < ORC_QK; e++)
+                    dot += (int32_t)aq[b * ORC_QK + e] * q4_quant(blk, e, order);
+                if (block_dots_out) block_dots_out[(mi * n_out + ni) * nb + b] = dot;
+                float t = (float)dot * s_a;
+                t = t * d;
+                acc = acc + t;
+            }
+            out[mi * n_out + ni] = acc;
+        }
+    }
+    free(aq);
     return ORC_OK;
 }

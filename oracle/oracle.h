@@ -128,6 +128,15 @@ int orc_dequantize_q4_0(const uint8_t *data, size_t n_bytes, float *out);
 int orc_matmul_q4_0_dequant(const float *input, const size_t *dims,
                             size_t ndim, const uint8_t *w_q4, size_t n_bytes,
                             size_t n_out, size_t k, float *out);
+/* Q4_0 nibble orders: the reference's interleaved order and upstream GGML's
+ * (low nibbles = elements 0..15, high nibbles = 16..31). */
+enum { ORC_Q4_INTERLEAVED = 0, ORC_Q4_GGML = 1 };
+/* W4A8 extension (no reference counterpart): matmul_q8_0_direct
+ * (q8_direct.rs:229-289) on Q4_0 blocks, quants = nibble - 8 in `order`. */
+int orc_matmul_q4_0_w4a8(const float *input, const size_t *dims, size_t ndim,
+                         const uint8_t *w_q4, size_t n_bytes, size_t n_out, size_t k,
+                         int order, float *out, int32_t *block_dots_out,
+                         float *act_scales_out);
 
 /* ---- decoder-layer steps (llama.c) ------------------------------------- */
 /* rmsnorm, ops/norm/rmsnorm.rs: x [rows, d] -> out, weight w [d]. */

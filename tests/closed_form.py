@@ -138,6 +138,29 @@ def q4_0_split(raw: np.ndarray, n_out: int, k: int):
     return f16_bits_to_f32(d_bits), q.reshape(n_out, k)
 
 
+def q4_0_to_q8_0(raw: np.ndarray, n_out: int, k: int) -> np.ndarray:
+    """Q4_0 blocks (reference nibble order) as Q8_0 blocks: the same f16
+    scale bits, quants nibble - 8 as int8."""
+    nb = k // 32
+    blk = np.asarray(raw, dtype=np.uint8).reshape(n_out, nb, 18)
+    d_bits = blk[:, :, 0].astype(np.uint16) | (blk[:, :, 1].astype(np.uint16) << 8)
+    _, q = q4_0_split(raw, n_out, k)
+    return q8_0_pack(d_bits, q.astype(np.int8))
+
+
+def q4_0_interleaved_to_ggml(raw: np.ndarray) -> np.ndarray:
+    """Re-encode Q4_0 blocks from the reference's nibble order (element 2i =
+    low nibble of byte i) to upstream GGML's (element i = low nibble of byte
+    i, element i + 16 = its high nibble); the scale bytes are kept."""
+    blk = np.asarray(raw, dtype=np.uint8).reshape(-1, 18).copy()
+    qs = blk[:, 2:]
+    e = np.empty((blk.shape[0], 32), np.uint8)
+    e[:, 0::2] = qs & 0x0F
+    e[:, 1::2] = qs >> 4
+    blk[:, 2:] = e[:, :16] | (e[:, 16:] << 4)
+    return blk.ravel()
+
+
 def q4_0_dequant_matmul_seq(x: np.ndarray, raw: np.ndarray, n_out: int, k: int):
     """matmul_q4_0_dequant with the reference's sequential f32 sum over K."""
     x = np.asarray(x, dtype=F32)

@@ -74,6 +74,7 @@ def _sig(l):
     l.orc_create_q4_0_block.argtypes = [P, P]
     l.orc_dequantize_q4_0.argtypes = [P, SZ, P]
     l.orc_matmul_q4_0_dequant.argtypes = [P, P, SZ, P, SZ, SZ, SZ, P]
+    l.orc_matmul_q4_0_w4a8.argtypes = [P, P, SZ, P, SZ, SZ, SZ, C.c_int, P, P, P]
     l.orc_last_error.restype = C.c_char_p
     l.orc_have_avx2.restype = C.c_int
     l.orc_rmsnorm.argtypes = [P, SZ, SZ, P, C.c_float, P]
@@ -291,6 +292,26 @@ def matmul_q4_0_dequant(x, w_q4, n_out, k):
     out = np.empty((max(m, 1), max(n_out, 1)), np.float32)
     _check(lib().orc_matmul_q4_0_dequant(_p(x), _p(dims), nd, _p(w_q4), w_q4.size,
                                          n_out, k, _p(out)))
+    return out[:m, :n_out]
+
+
+Q4_INTERLEAVED, Q4_GGML = 0, 1
+
+
+def matmul_q4_0_w4a8(x, w_q4, n_out, k, order=Q4_INTERLEAVED, want_block_dots=False):
+    """W4A8 extension: returns out, or (out, block_dots[M,N,K/32], act_scales[M])."""
+    x = _c(x, np.float32)
+    w_q4 = _c(w_q4, np.uint8)
+    dims, nd = _dims(x.shape)
+    m = x.shape[0] if nd >= 1 else 1
+    out = np.empty((max(m, 1), max(n_out, 1)), np.float32)
+    bd = np.empty((max(m, 1), max(n_out, 1), max(k // 32, 1)), np.int32) if want_block_dots \
+        else None
+    sa = np.empty(max(m, 1), np.float32) if want_block_dots else None
+    _check(lib().orc_matmul_q4_0_w4a8(_p(x), _p(dims), nd, _p(w_q4), w_q4.size, n_out, k,
+                                      order, _p(out), _p(bd), _p(sa)))
+    if want_block_dots:
+        return out[:m, :n_out], bd[:m, :n_out], sa[:m]
     return out[:m, :n_out]
 
 

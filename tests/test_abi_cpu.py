@@ -80,6 +80,25 @@ def test_shape_errors_before_device_work():
                                        None)) == "InvalidArgument"
 
 
+def test_w4a8_argument_errors_before_device_work():
+    """The W4A8 extension's handle checks: nibble order, K % 32, byte count;
+    a null handle."""
+    import mri_qmatmul as M
+    lib = M.lib()
+    h = C.c_void_p()
+    buf = np.zeros(36, np.uint8)
+    p = buf.ctypes.data_as(C.c_void_p)
+    assert _status(lib.mri_q4_0_matrix_from_raw_device(p, 18, 1, 32, 2, None, C.byref(h))) \
+        == "InvalidArgument"
+    assert _status(lib.mri_q4_0_matrix_from_raw_device(p, 18, 1, 31, 0, None, C.byref(h))) \
+        == "InvalidShape"
+    assert _status(lib.mri_q4_0_matrix_from_raw_device(p, 17, 1, 32, 1, None, C.byref(h))) \
+        == "InvalidShape"
+    dims = (C.c_size_t * 2)(1, 32)
+    assert _status(lib.mri_matmul_q4_0_w4a8(None, dims, 2, None, None, None, None, None)) \
+        == "InvalidArgument"
+
+
 @pytest.mark.skipif(os.path.exists("/dev/kfd") and os.access("/dev/kfd", os.R_OK),
                     reason="a GPU is visible")
 def test_fails_loudly_without_gpu():

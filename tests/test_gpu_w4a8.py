@@ -1,0 +1,105 @@
+"""GPU parity of the W4A8 extension (include/mri_qmatmul.h,
+mri_matmul_q4_0_w4a8) against the oracle's orc_matmul_q4_0_w4a8, which is
+pinned to matmul_q8_0_direct on the expanded blocks
+(tests/test_oracle_closed_form.py).  Block dots, activation scales and the
+block-ordered f32 outputs must be bit-identical, in both nibble orders."""
+import sys
+
+import numpy as np
+import pytest
+
+import closed_form as CF
+import oracle_lib as O
+from gpu_util import F32, assert_bits_equal, bits, dev, empty, host, synth_q4_0, torch
+
+pytestmark = pytest.mark.gpu
+
+
+def mri():
+    import mri_qmatmul
+    return mri_qmatmul
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+W4A8_SHAPES = [
+    (1, 16, 32), (1, 16, 256), (1, 50, 96), (1, 1024, 4096), (1, 11008, 4096),
+    (1, 64, 11008), (1, 32000 // 8, 4096), (2, 33, 256), (3, 48, 1024), (4, 64, 4096),
+    (5, 40, 512), (9, 24, 1024), (16, 272, 4096),
+]
+
+
+@pytest.mark.parametrize("m,n,k", W4A8_SHAPES)
+@pytest.mark.parametrize("order", [0, 1])
+def test_w4a8_bit_exact(m, n, k, order):
+    say(f"matmul_q4_0_w4a8 m={m} n={n} k={k} order={order}")
+    t = torch()
+    rng = np.random.default_rng(m * 7 + n + k + order)
+    raw = synth_q4_0(rng, n, k)
+    x = rng.standard_normal((m, k)).astype(F32)
+    out0, bd0, sa0 = O.matmul_q4_0_w4a8(x, raw, n, k, order, want_block_dots=True)
+    w = mri().Q4Matrix.from_raw_bytes(raw, n, k, order)
+    out = empty((m, n), t.float32)
+    bd = empty((m, n, k // 32), t.int32)
+    sa = empty(m, t.float32)
+    mri().matmul_q4_0_w4a8(dev(x), w, out, bd, sa)
+    assert np.array_equal(bits(host(sa)), bits(sa0))
+    assert np.array_equal(host(bd), bd0)
+    assert_bits_equal(host(out), out0, "w4a8 out")
+    out2 = empty((m, n), t.float32)          # without the debug outputs
+    mri().matmul_q4_0_w4a8(dev(x), w, out2)
+    assert_bits_equal(host(out2), out0, "w4a8 out (no debug outputs)")
+
+
+def test_w4a8_ggml_file_order_matches_reference_order():
+    """The same weights uploaded from GGML-order bytes and from
+    interleaved-order bytes give the same outputs."""
+    t = torch()
+    rng = np.random.default_rng(3)
+    n, k = 96, 2048
+    raw = synth_q4_0(rng, n, k)
+    x = dev(rng.standard_normal((1, k)).astype(F32))
+    a, b = empty((1, n), t.float32), empty((1, n), t.float32)
+    mri().matmul_q4_0_w4a8(x, mri().Q4Matrix.from_raw_bytes(raw, n, k, 0), a)
+    gg = CF.q4_0_interleaved_to_ggml(raw)
+    mri().matmul_q4_0_w4a8(x, mri().Q4Matrix.from_raw_device(dev(gg), n, k, 1), b)
+    assert_bits_equal(host(b), host(a), "ggml order")
+
+
+def test_w4a8_unfused_and_device_upload():
+    """x at a 4-byte aligned address takes the quantize kernel + GEMV path;
+    weights uploaded from a device buffer."""
+    t = torch()
+    rng = np.random.default_rng(5)
+    n, k = 80, 4096
+    raw = synth_q4_0(rng, n, k)
+    x = rng.standard_normal((1, k)).astype(F32)
+    buf = dev(np.concatenate([np.zeros(1, F32), x.ravel()]))
+    xu = buf[1:].view(1, k)
+    assert xu.data_ptr() % 16 != 0
+    w = mri().Q4Matrix.from_raw_device(dev(raw), n, k)
+    out = empty((1, n), t.float32)
+    mri().matmul_q4_0_w4a8(xu, w, out)
+    assert_bits_equal(host(out), O.matmul_q4_0_w4a8(x, raw, n, k), "w4a8 unfused")
+
+
+def test_w4a8_errors():
+    t = torch()
+    M = mri()
+    rng = np.random.default_rng(1)
+    w = M.Q4Matrix.from_raw_bytes(synth_q4_0(rng, 16, 64), 16, 64)
+    out = empty((2, 16), t.float32)
+    with pytest.raises(M.MriError) as e:
+        M.matmul_q4_0_w4a8(dev(np.zeros((2, 32), F32)), w, out)
+    assert e.value.kind == "ShapeMismatch"
+    with pytest.raises(M.MriError) as e:
+        M.matmul_q4_0_w4a8(dev(np.zeros((2, 64), F32)), w, out, shape=(2, 8, 8))
+    assert e.value.kind == "InvalidShape"
+    big = M.Q4Matrix.from_raw_bytes(np.zeros(16 * (12544 // 32) * 18, np.uint8), 16, 12544)
+    with pytest.raises(M.MriError) as e:
+        M.matmul_q4_0_w4a8(dev(np.zeros((1, 12544), F32)), big, out)
+    assert e.value.kind == "Unsupported"
+    assert M.Q4Matrix.from_raw_bytes(np.zeros(18 * 16, np.uint8), 16, 32).device_bytes > 0

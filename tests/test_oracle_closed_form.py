@@ -172,6 +172,62 @@ def test_q4_0_dequant_closed_form(m, n, k, seed):
     assert np.array_equal(bits(deq), bits((np.repeat(dd, 32, 1) * q.astype(F32)).astype(F32)))
 
 
+def _q4_synth(rng, n, k):
+    raw = np.empty((n, k // 32, 18), np.uint8)
+    raw[:, :, 2:] = rng.integers(0, 256, (n, k // 32, 16))
+    d = rng.uniform(0.001, 0.05, (n, k // 32)).astype(np.float16).view(np.uint16)
+    raw[:, :, 0] = d & 0xFF
+    raw[:, :, 1] = d >> 8
+    return raw.ravel()
+
+
+@pytest.mark.parametrize("m,n,k,seed", [(1, 48, 512, 0), (3, 9, 96, 1), (5, 16, 4096, 2)])
+def test_q4_0_w4a8_is_q8_0_direct_on_expanded_blocks(m, n, k, seed):
+    """The W4A8 extension is matmul_q8_0_direct on the same blocks with
+    quants nibble - 8: bit-identical outputs, block dots and scales."""
+    rng = np.random.default_rng(seed)
+    raw4 = _q4_synth(rng, n, k)
+    x = rng.standard_normal((m, k)).astype(F32)
+    out, bd, sa = O.matmul_q4_0_w4a8(x, raw4, n, k, want_block_dots=True)
+    out8, bd8, sa8 = O.matmul_q8_0_direct(x, CF.q4_0_to_q8_0(raw4, n, k), n, k,
+                                          want_block_dots=True)
+    assert np.array_equal(bd, bd8)
+    assert np.array_equal(bits(sa), bits(sa8))
+    assert np.array_equal(bits(out), bits(out8))
+    out0, bd0, _ = CF.q8_0_direct(x, CF.q4_0_to_q8_0(raw4, n, k), n, k)
+    assert np.array_equal(bd.astype(np.int64), bd0)
+    assert np.array_equal(bits(out), bits(out0))
+
+
+def test_q4_0_w4a8_ggml_order():
+    """GGML-order blocks give the interleaved-order result of the same
+    elements."""
+    rng = np.random.default_rng(7)
+    n, k = 24, 1024
+    raw4 = _q4_synth(rng, n, k)
+    x = rng.standard_normal((2, k)).astype(F32)
+    want = O.matmul_q4_0_w4a8(x, raw4, n, k, O.Q4_INTERLEAVED)
+    gg = CF.q4_0_interleaved_to_ggml(raw4)
+    assert np.array_equal(bits(O.matmul_q4_0_w4a8(x, gg, n, k, O.Q4_GGML)), bits(want))
+    # reading GGML bytes in the interleaved order is a different matrix
+    assert not np.array_equal(bits(O.matmul_q4_0_w4a8(x, gg, n, k, O.Q4_INTERLEAVED)),
+                              bits(want))
+
+
+def test_q4_0_w4a8_errors():
+    x = np.zeros((2, 64), F32)
+    raw = np.zeros(2 * 2 * 18, np.uint8)
+    with pytest.raises(O.OracleError) as e:
+        O.matmul_q4_0_w4a8(x, raw, 2, 96)
+    assert e.value.code == 2   # K mismatch first
+    with pytest.raises(O.OracleError) as e:
+        O.matmul_q4_0_w4a8(np.zeros((2, 48), F32), raw, 2, 48)
+    assert e.value.code == 1   # K % 32
+    with pytest.raises(O.OracleError) as e:
+        O.matmul_q4_0_w4a8(x, raw[:-1], 2, 64)
+    assert e.value.code == 1   # byte length
+
+
 # ---- planted mistakes: each must be caught by the checks above ---------------
 
 def test_planted_half_even_rounding_is_caught():
