@@ -35,7 +35,8 @@ the reference: one row) and on a bounded row sample of the prefill shape
 Decoder layer (the 7B-dims LlamaModelInt8 configuration): one random-init
 layer (hidden 4096, 32 heads of 128, SwiGLU 11008, RMSNorm eps 1e-6, RoPE
 base 10000) with the output head (vocab 32000), Q8_0 weights (and per-channel
-INT8, the reference model's own format): a 512-token prefill
+INT8, the reference model's own format, and Q4_0 weights on the W4A8
+extension): a 512-token prefill
 (forward_cached) and 128 greedy decode steps (generate_greedy, token ids
 kept on the device), seeded random prompt ids.
 """
@@ -261,6 +262,8 @@ def layer_decode_bytes(fmt, ctx):
     shapes = [(d, d)] * 4 + [(f, d)] * 2 + [(d, f), (v, d)]
     if fmt == "q8_0":
         w = sum(n * (k // 32) * 34 for n, k in shapes)
+    elif fmt == "w4a8":
+        w = sum(n * (k // 32) * 18 for n, k in shapes)
     else:
         w = sum(n * k + 4 * n for n, k in shapes)
     return w + 2 * ctx * d * 4
@@ -287,6 +290,8 @@ def bench_layer(torch, M, fmt, n_prompt=512, n_steps=128, seed=21):
             raw[:, :, 0:2] = dd.view(torch.uint8).view(n, nb, 2)
             raw[:, :, 2:] = q.view(torch.uint8)
             return M.Q8Matrix.from_raw_device(raw.view(-1), n, k)
+        if fmt == "w4a8":
+            return M.Q4Matrix.from_raw_device(q4_raw_device(torch, n, k, sd[0]), n, k)
         data, scales = int8_weights_device(torch, M, n, k, sd[0])
         return M.QMatrix.from_device(data, scales)
 
@@ -488,7 +493,7 @@ def main():
         log(f"q4_0 w4a8 decode: {ms_w4*1e3:.2f} us {gbs:.0f} GB/s")
 
         layer = {}
-        for fmt in ("q8_0", "int8"):
+        for fmt in ("q8_0", "int8", "w4a8"):
             layer[fmt] = bench_layer(torch, M, fmt)
             log(f"decoder layer {fmt}: prefill 512 {layer[fmt]['prefill_512_ms']:.2f} ms, "
                 f"decode {layer[fmt]['decode_us_per_token']:.1f} us/token")

@@ -50,7 +50,10 @@ typedef struct mri_llama_config {
 typedef enum mri_weight_format {
     MRI_WEIGHT_INT8 = 0, /* const mri_qmatrix *       */
     MRI_WEIGHT_Q8_0 = 1, /* const mri_q8_0_matrix *   */
-    MRI_WEIGHT_Q4_0 = 2  /* device pointer to raw Q4_0 blocks, n_out x k_in */
+    MRI_WEIGHT_Q4_0 = 2, /* device pointer to raw Q4_0 blocks, n_out x k_in */
+    /* const mri_q4_0_matrix *: Q4_0 weights projected with int8 activations
+     * (mri_matmul_q4_0_w4a8, an extension without a reference counterpart) */
+    MRI_WEIGHT_Q4_0_W4A8 = 3
 } mri_weight_format;
 
 /* A projection weight [n_out, k_in] (GGUF "out, in" layout).  The handle or

@@ -208,9 +208,8 @@ void mri_q4_0_matrix_destroy(mri_q4_0_matrix *w);
  * 42-57), per-block exact int32 dots with the quants, and
  *   out[m,n] = sum over b in block order of ((f32)dot[m,n,b]*s_a[m])*d[n,b],
  * i.e. mri_matmul_q8_0_direct on the blocks with quants nibble - 8.
- * InvalidShape unless ndim == 2; ShapeMismatch when dims[1] != k_in;
- * Unsupported when k_in > 12288 (the kernel stages up to four activation
- * rows in LDS).  Optional outputs (nullable, device):
+ * InvalidShape unless ndim == 2; ShapeMismatch when dims[1] != k_in.
+ * Optional outputs (nullable, device):
  * block_dots_out [m, n_out, k_in/32] int32, act_scales_out [m]. */
 mri_status mri_matmul_q4_0_w4a8(const float *input, const size_t *dims, size_t ndim,
                                 const mri_q4_0_matrix *w, float *out,

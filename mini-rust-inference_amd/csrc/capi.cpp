@@ -162,18 +162,7 @@ static mri_status run_q8(const int8_t *act, size_t m, const float *sa_rows,
                          hipStream_t s) {
     if (gemv_q8_supported(false, m, w.n_tiles, w.k_in, w.kp))
         return launch_gemv_q8_0(nullptr, act, m, sa_rows, w, out, block_dots, nullptr, s);
-    if (!w.w4) return launch_skinny_q8_0(act, m, sa_rows, w, out, block_dots, s);
-    // W4A8 above 4 rows: the GEMV on 4-row slices
-    for (size_t r0 = 0; r0 < m; r0 += kMaxGemvRows) {
-        const size_t mm = std::min(kMaxGemvRows, m - r0);
-        if (!gemv_q8_supported(false, mm, w.n_tiles, w.k_in, w.kp))
-            return set_error(MRI_ERR_UNSUPPORTED, "matmul_q4_0_w4a8: shape not supported");
-        mri_status st = launch_gemv_q8_0(
-            nullptr, act + r0 * w.kp, mm, sa_rows + r0, w, out + r0 * w.n_out,
-            block_dots ? block_dots + r0 * w.n_out * w.n_blocks : nullptr, nullptr, s);
-        if (st) return st;
-    }
-    return MRI_OK;
+    return launch_skinny_q8_0(act, m, sa_rows, w, out, block_dots, s);
 }
 
 // Returns act rows with pitch w.kp: the caller's buffer when it already has
@@ -543,8 +532,10 @@ mri_status concat_qmatrix(const mri_qmatrix *const *parts, int n, hipStream_t s,
     return MRI_OK;
 }
 
-mri_status concat_q8_0_matrix(const mri_q8_0_matrix *const *parts, int n, hipStream_t s,
-                              mri_q8_0_matrix **out) {
+// Tile-major lap blocks (Q8_0 and W4A8 handles): the parts' buffers one
+// after the other.
+template <typename H, void (*Destroy)(H *)>
+mri_status concat_laps(const H *const *parts, int n, hipStream_t s, H **out) {
     *out = nullptr;
     size_t rows = 0;
     for (int i = 0; i < n; ++i) {
@@ -552,13 +543,12 @@ mri_status concat_q8_0_matrix(const mri_q8_0_matrix *const *parts, int n, hipStr
             return set_error(MRI_ERR_INVALID_SHAPE, "concat: parts must be whole tiles of one K");
         rows += parts[i]->d.n_out;
     }
-    auto *h = new mri_q8_0_matrix();
+    auto *h = new H();
     Q8MatrixDev &d = h->d;
     d = parts[0]->d;
     d.laps = nullptr;
     d.n_out = rows;
     d.n_tiles = rows / kTileN;
-    // tile-major lap blocks: the fused matrix is the parts' buffers in turn
     hipError_t e = hipMalloc(&d.laps, d.bytes() + 256);
     size_t off = 0;
     for (int i = 0; i < n && e == hipSuccess; ++i) {
@@ -567,11 +557,21 @@ mri_status concat_q8_0_matrix(const mri_q8_0_matrix *const *parts, int n, hipStr
         off += pd.bytes();
     }
     if (e != hipSuccess) {
-        mri_q8_0_matrix_destroy(h);
-        return hip_error(e, "concat_q8_0_matrix");
+        Destroy(h);
+        return hip_error(e, "concat");
     }
     *out = h;
     return MRI_OK;
+}
+
+mri_status concat_q8_0_matrix(const mri_q8_0_matrix *const *parts, int n, hipStream_t s,
+                              mri_q8_0_matrix **out) {
+    return concat_laps<mri_q8_0_matrix, mri_q8_0_matrix_destroy>(parts, n, s, out);
+}
+
+mri_status concat_q4_0_matrix(const mri_q4_0_matrix *const *parts, int n, hipStream_t s,
+                              mri_q4_0_matrix **out) {
+    return concat_laps<mri_q4_0_matrix, mri_q4_0_matrix_destroy>(parts, n, s, out);
 }
 
 }  // namespace mri
@@ -804,9 +804,6 @@ mri_status mri_matmul_q4_0_w4a8(const float *input, const size_t *dims, size_t n
                                 int32_t *block_dots_out, float *act_scales_out,
                                 void *stream) {
     if (!w) return set_error(MRI_ERR_INVALID_ARGUMENT, "null weight handle");
-    if (w->d.k_in > kMaxW4a8K)
-        return set_error(MRI_ERR_UNSUPPORTED,
-                         fmt("matmul_q4_0_w4a8: k_in=%zu exceeds %zu", w->d.k_in, kMaxW4a8K));
     return matmul_blocks("matmul_q4_0_w4a8", input, dims, ndim, w->d, out, block_dots_out,
                          act_scales_out, stream);
 }

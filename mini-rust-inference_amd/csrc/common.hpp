@@ -185,8 +185,6 @@ mri_status launch_skinny_q8_0(const int8_t *act, size_t m,
 // x (quantized in the kernel; requires gemv_fusable, M == 1; optional
 // act_q_out [k] and scale_out [1]) or as quantized rows act [m][kp] (Q8_0:
 // chunk-permuted) with their scales.
-constexpr size_t kMaxGemvRows = 4;     // rows of one GEMV launch
-constexpr size_t kMaxW4a8K = 12288;    // K of the W4A8 path (activation rows in LDS)
 bool gemv_int8_supported(bool fused, size_t m, size_t n_tiles, size_t k, size_t kp);
 bool gemv_q8_supported(bool fused, size_t m, size_t n_tiles, size_t k, size_t kp);
 bool gemv_fusable(size_t m, size_t k, const float *x);
@@ -230,6 +228,8 @@ mri_status concat_qmatrix(const mri_qmatrix *const *parts, int n, hipStream_t s,
                           mri_qmatrix **out);
 mri_status concat_q8_0_matrix(const mri_q8_0_matrix *const *parts, int n, hipStream_t s,
                               mri_q8_0_matrix **out);
+mri_status concat_q4_0_matrix(const mri_q4_0_matrix *const *parts, int n, hipStream_t s,
+                              mri_q4_0_matrix **out);
 
 // llama.hip: the decoder layer's non-matmul steps (f32 rows in HBM).
 mri_status launch_embed(const float *table, const uint32_t *tokens, size_t rows, size_t d,

@@ -115,6 +115,12 @@ mri_status check_weight(const mri_weight_ref &w, size_t n_out, size_t k_in, cons
             return set_error(MRI_ERR_INVALID_SHAPE,
                              std::string(role) + ": Q4_0 k_in must be a multiple of 32");
         return MRI_OK;
+    case MRI_WEIGHT_Q4_0_W4A8: {
+        auto *h = static_cast<const mri_q4_0_matrix *>(w.ptr);
+        if (mri_q4_0_matrix_n_out(h) != n_out || mri_q4_0_matrix_k_in(h) != k_in)
+            return set_error(MRI_ERR_INVALID_SHAPE, std::string(role) + ": handle shape differs");
+        return MRI_OK;
+    }
     default:
         return set_error(MRI_ERR_INVALID_ARGUMENT, std::string(role) + ": unknown weight format");
     }
@@ -125,15 +131,17 @@ void release_fused(mri_weight_ref &w) {
         mri_qmatrix_destroy(static_cast<mri_qmatrix *>(const_cast<void *>(w.ptr)));
     else if (w.ptr && w.format == MRI_WEIGHT_Q8_0)
         mri_q8_0_matrix_destroy(static_cast<mri_q8_0_matrix *>(const_cast<void *>(w.ptr)));
+    else if (w.ptr && w.format == MRI_WEIGHT_Q4_0_W4A8)
+        mri_q4_0_matrix_destroy(static_cast<mri_q4_0_matrix *>(const_cast<void *>(w.ptr)));
     w = mri_weight_ref{};
 }
 
 // The row concatenation of parts that share one input (q/k/v, gate/up): the
 // fused projection's output row is [part 0 | part 1 | ...] and every element
 // equals that of the separate projection, because the parts see the same
-// activations and the same activation quantization.  Q4_0 weights, mixed
-// formats and parts that are not whole 16-row tiles stay separate (*out
-// left empty).
+// activations and the same activation quantization.  W4A32 Q4_0 weights
+// (raw bytes, no handle), mixed formats and parts that are not whole 16-row
+// tiles stay separate (*out left empty).
 mri_status fuse(const mri_weight_ref *parts, int n, mri_weight_ref *out) {
     *out = mri_weight_ref{};
     size_t rows = 0;
@@ -153,6 +161,12 @@ mri_status fuse(const mri_weight_ref *parts, int n, mri_weight_ref *out) {
         for (int i = 0; i < n; ++i) p[i] = static_cast<const mri_q8_0_matrix *>(parts[i].ptr);
         mri_q8_0_matrix *f = nullptr;
         TRY(concat_q8_0_matrix(p, n, nullptr, &f));
+        h = f;
+    } else if (parts[0].format == MRI_WEIGHT_Q4_0_W4A8) {
+        const mri_q4_0_matrix *p[3];
+        for (int i = 0; i < n; ++i) p[i] = static_cast<const mri_q4_0_matrix *>(parts[i].ptr);
+        mri_q4_0_matrix *f = nullptr;
+        TRY(concat_q4_0_matrix(p, n, nullptr, &f));
         h = f;
     } else {
         return MRI_OK;
@@ -177,6 +191,9 @@ mri_status proj(const mri_weight_ref &w, const float *in, size_t rows, float *ou
     case MRI_WEIGHT_Q8_0:
         return mri_matmul_q8_0_direct(in, dims, 2, static_cast<const mri_q8_0_matrix *>(w.ptr),
                                       out, nullptr, nullptr, s);
+    case MRI_WEIGHT_Q4_0_W4A8:
+        return mri_matmul_q4_0_w4a8(in, dims, 2, static_cast<const mri_q4_0_matrix *>(w.ptr),
+                                    out, nullptr, nullptr, s);
     default:
         return mri_matmul_q4_0_dequant(in, dims, 2, static_cast<const uint8_t *>(w.ptr),
                                        w.n_out * (w.k_in / 32) * 18, w.n_out, w.k_in, out, s);

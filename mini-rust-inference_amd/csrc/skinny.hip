@@ -146,8 +146,13 @@ __global__ __launch_bounds__(kWave) void k_skinny_int8(
 // ring's loads and no data-dependent branch, so every wait leaves the
 // younger loads in flight.  Rows m >= M read row 0's activations; their
 // results are never stored.
+//
+// W4 (Q4_0 weights of the W4A8 path): a lap's quants are two 16-byte pieces
+// per lane; the 8-byte B operand of block h of chunk c is the u32 word
+// 2(c % 2) + h of piece c / 2 with each nibble moved to the high half of its
+// byte (16 * quant as int8), and the MFMA result is divided by 16 exactly.
 // ---------------------------------------------------------------------------
-template <int AG, int TPW, int RL, bool DEBUG>
+template <int AG, int TPW, int RL, bool DEBUG, bool W4>
 __global__ __launch_bounds__(TPW * kWave) void k_skinny_q8_0(
     const int8_t *__restrict__ act, int M, int kp, const float *__restrict__ sa_rows,
     const v4i *__restrict__ laps, int N, int n_tiles, int G, int nb, float *__restrict__ out,
@@ -166,11 +171,13 @@ __global__ __launch_bounds__(TPW * kWave) void k_skinny_q8_0(
     if (T >= n_tiles) return;  // whole waves only; the kernel has no barrier
     const int l = threadIdx.x & 63;
     const int r = l & 15, g = l >> 4;
-    // the tile's lap blocks: chunk c of lap q at v4i offset q * LB + c * 64
-    // (+ lane), the lap's scales at q * LB + 256 (+ row)
-    constexpr size_t LB = kQ8LapBytes / 16;
+    // the tile's lap blocks: quant piece c of lap q at v4i offset
+    // q * LB + c * 64 (+ lane), the lap's scales at q * LB + SO (+ row)
+    constexpr size_t LB = (W4 ? kQ4LapBytes : kQ8LapBytes) / 16;
+    constexpr int SO = W4 ? 128 : 256;
+    constexpr int NP = W4 ? 2 : 4;  // quant pieces per lap and lane
     const v4i *wp = laps + (size_t)T * G * LB + l;
-    const v4i *sp = laps + (size_t)T * G * LB + 256 + r;
+    const v4i *sp = laps + (size_t)T * G * LB + SO + r;
     const int n = T * 16 + r;
     const v4i *ap[AG];
     float sa[AG][4], fs[AG][4];
@@ -192,7 +199,7 @@ __global__ __launch_bounds__(TPW * kWave) void k_skinny_q8_0(
         const int q = min(u, G - 1);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            wr[u][c] = __builtin_nontemporal_load(wp + (size_t)q * LB + c * 64);
+            if (c < NP) wr[u][c] = __builtin_nontemporal_load(wp + (size_t)q * LB + c * 64);
 #pragma unroll
             for (int a = 0; a < AG; ++a) xr[u][c][a] = ap[a][(size_t)(4 * q + c) * 4];
         }
@@ -209,15 +216,32 @@ __global__ __launch_bounds__(TPW * kWave) void k_skinny_q8_0(
             v4i d[2][AG];
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const long bv = h ? hi8(wr[U][c]) : lo8(wr[U][c]);
+                long bv;
+                if constexpr (W4) {
+                    const v4i pc = wr[U][c >> 1];
+                    const int wd = (c & 1) ? (h ? pc.w : pc.z) : (h ? pc.y : pc.x);
+                    constexpr int kHi = (int)0xF0F0F0F0u;
+                    bv = (long)(((unsigned long)(unsigned)(wd & kHi) << 32) |
+                                (unsigned)((wd << 4) & kHi));
+                } else {
+                    bv = h ? hi8(wr[U][c]) : lo8(wr[U][c]);
+                }
 #pragma unroll
-                for (int a = 0; a < AG; ++a)
+                for (int a = 0; a < AG; ++a) {
                     d[h][a] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
                         h ? hi8(xr[U][c][a]) : lo8(xr[U][c][a]), bv, zero, 0, 0, 0);
+                    if constexpr (W4) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) d[h][a][i] >>= 4;
+                    }
+                }
             }
             if (refill) {
                 const size_t p = (size_t)(4 * (L + RL) + c);
-                wr[U][c] = __builtin_nontemporal_load(wp + (size_t)(L + RL) * LB + c * 64);
+                if (!W4 || (c & 1)) {
+                    const int pi = W4 ? c >> 1 : c;
+                    wr[U][pi] = __builtin_nontemporal_load(wp + (size_t)(L + RL) * LB + pi * 64);
+                }
 #pragma unroll
                 for (int a = 0; a < AG; ++a) xr[U][c][a] = ap[a][p * 4];
             }
@@ -287,18 +311,25 @@ void launch_i8(const int8_t *act, size_t m, size_t kp, const float *sa_ptr,
 }
 
 // AG activation groups per wave, ns waves per tile (AG * ns groups of 16 rows).
-template <int AG, int TPW, int RL, bool DEBUG>
-void launch_q8(const int8_t *act, size_t m, size_t kp, const float *sa_rows,
-               const Q8MatrixDev &w, float *out, int32_t *block_dots, int ns, hipStream_t s) {
+template <int AG, int TPW, int RL, bool DEBUG, bool W4>
+void launch_q8_w(const int8_t *act, size_t m, size_t kp, const float *sa_rows,
+                 const Q8MatrixDev &w, float *out, int32_t *block_dots, int ns, hipStream_t s) {
     const int G = (int)w.laps_per_tile();
     const size_t waves = w.n_tiles * (size_t)ns;
     size_t grid = (waves + TPW - 1) / TPW;
     if (ns > TPW) grid = (grid + 7) / 8 * 8;  // XCD-major mapping (whole waves past the end exit)
-    hipLaunchKernelGGL((k_skinny_q8_0<AG, TPW, RL, DEBUG>),
+    hipLaunchKernelGGL((k_skinny_q8_0<AG, TPW, RL, DEBUG, W4>),
                        dim3((unsigned)grid), dim3(TPW * kWave), 0, s,
                        act, (int)m, (int)kp, sa_rows, reinterpret_cast<const v4i *>(w.laps),
                        (int)w.n_out, (int)w.n_tiles, G,
                        (int)w.n_blocks, out, block_dots, ns);
+}
+
+template <int AG, int TPW, int RL, bool DEBUG>
+void launch_q8(const int8_t *act, size_t m, size_t kp, const float *sa_rows,
+               const Q8MatrixDev &w, float *out, int32_t *block_dots, int ns, hipStream_t s) {
+    if (w.w4) launch_q8_w<AG, TPW, RL, DEBUG, true>(act, m, kp, sa_rows, w, out, block_dots, ns, s);
+    else launch_q8_w<AG, TPW, RL, DEBUG, false>(act, m, kp, sa_rows, w, out, block_dots, ns, s);
 }
 
 }  // namespace

@@ -15,7 +15,7 @@ P = C.c_void_p
 SZ = C.c_size_t
 ST = C.c_int
 
-INT8, Q8_0, Q4_0 = 0, 1, 2
+INT8, Q8_0, Q4_0, Q4_0_W4A8 = 0, 1, 2, 3
 
 
 class Config(C.Structure):
@@ -57,11 +57,14 @@ def lib():
 
 
 def weight_ref(w):
-    """QMatrix / Q8Matrix handle, or (q4_0 device uint8 tensor, n_out, k_in)."""
+    """QMatrix / Q8Matrix / Q4Matrix (W4A8) handle, or (q4_0 device uint8
+    tensor, n_out, k_in) for the W4A32 projection."""
     if isinstance(w, Q.QMatrix):
         return WeightRef(INT8, w.h, w.n_out, w.k_in)
     if isinstance(w, Q.Q8Matrix):
         return WeightRef(Q8_0, w.h, w.n_out, w.k_in)
+    if isinstance(w, Q.Q4Matrix):
+        return WeightRef(Q4_0_W4A8, w.h, w.n_out, w.k_in)
     t, n_out, k_in = w
     return WeightRef(Q4_0, C.c_void_p(t.data_ptr()), n_out, k_in)
 

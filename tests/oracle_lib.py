@@ -371,10 +371,11 @@ def argmax(v):
 
 # ---- LlamaModelInt8 composition (model/llama/forward_int8.rs) ------------
 class Proj:
-    """One projection weight in one of the three formats: "int8"
+    """One projection weight in one of the formats: "int8"
     (QuantizedMatrix: data [N,K] int8 + scales [N], projected by
     matmul_int8_from_f32, forward_int8.rs:72-74), "q8_0" (raw Q8_0 bytes,
-    matmul_q8_0_direct) or "q4_0" (raw Q4_0 bytes, matmul_q4_0_dequant)."""
+    matmul_q8_0_direct), "q4_0" (raw Q4_0 bytes, matmul_q4_0_dequant) or
+    "w4a8" (raw Q4_0 bytes, the W4A8 extension matmul_q4_0_w4a8)."""
 
     def __init__(self, fmt, n_out, k_in, data, scales=None):
         self.fmt, self.n_out, self.k_in, self.data, self.scales = fmt, n_out, k_in, data, scales
@@ -384,6 +385,8 @@ class Proj:
             return matmul_int8_from_f32(x, self.data, self.scales)[0]
         if self.fmt == "q8_0":
             return matmul_q8_0_direct(x, self.data, self.n_out, self.k_in)
+        if self.fmt == "w4a8":
+            return matmul_q4_0_w4a8(x, self.data, self.n_out, self.k_in)
         return matmul_q4_0_dequant(x, self.data, self.n_out, self.k_in)
 
 

@@ -9,7 +9,9 @@ projections quantize their inputs to int8: a last-bit difference in an
 activation can move one element across a rounding boundary, which changes
 that element by one quantization step, so the logits of those models are
 compared to 2e-2 of their largest magnitude (a wrong head, position or
-mask moves them by O(1)) and greedy tokens by their oracle margin."""
+mask moves them by O(1)) and greedy tokens by their oracle margin.  The
+W4A8 extension quantizes its inputs the same way and is compared the same
+way."""
 import numpy as np
 import pytest
 
@@ -49,6 +51,8 @@ def build(fmt, seed=0, d=256, nh=4, nkv=2, ffn=512, vocab=300, max_seq=48, n_lay
             raw = O.quantize_q8_0(w)
             return O.Proj("q8_0", n, k, raw), Q.Q8Matrix.from_raw_bytes(raw, n, k)
         raw = O.quantize_q4_0(w)
+        if fmt == "w4a8":
+            return O.Proj("w4a8", n, k, raw), Q.Q4Matrix.from_raw_bytes(raw, n, k)
         return O.Proj("q4_0", n, k, raw), (dev(raw), n, k)
 
     o_layers, g_layers = [], []
@@ -76,15 +80,15 @@ def close(got, ref, frac):
     assert err <= frac * scale, f"max |gpu - ref| = {err:.3g} > {frac} * {scale:.3g}"
 
 
-TOL = {"q4_0": 1e-4, "q8_0": 2e-2, "int8": 2e-2}
+TOL = {"q4_0": 1e-4, "q8_0": 2e-2, "int8": 2e-2, "w4a8": 2e-2}
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "q8_0", "int8"])
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0", "int8", "w4a8"])
 def test_llama_prefill_and_decode_logits(fmt):
     """forward_cached over a prompt, then forward_decode steps (teacher
     forced: both sides see the same tokens)."""
     t = torch()
-    oracle, gpu, rng = build(fmt, seed={"q4_0": 1, "q8_0": 2, "int8": 3}[fmt])
+    oracle, gpu, rng = build(fmt, seed={"q4_0": 1, "q8_0": 2, "int8": 3, "w4a8": 4}[fmt])
     toks = rng.integers(0, 300, 24).tolist()
     cache = gpu.kv_cache()
     logits = empty((20, 300), t.float32)
@@ -148,7 +152,7 @@ def test_llama_decode_matches_prefill_rows_q8_0():
         close(host(one), host(full)[p], 2e-2)
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0", "w4a8"])
 def test_llama_generate_greedy(fmt):
     """Device-resident greedy loop: every chosen token is the oracle's
     argmax of the oracle's logits on the same (teacher-forced) prefix, or

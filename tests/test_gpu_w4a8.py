@@ -28,7 +28,8 @@ def say(msg):
 W4A8_SHAPES = [
     (1, 16, 32), (1, 16, 256), (1, 50, 96), (1, 1024, 4096), (1, 11008, 4096),
     (1, 64, 11008), (1, 32000 // 8, 4096), (2, 33, 256), (3, 48, 1024), (4, 64, 4096),
-    (5, 40, 512), (9, 24, 1024), (16, 272, 4096),
+    (5, 40, 512), (9, 24, 1024), (16, 272, 4096), (33, 48, 256), (100, 40, 1024),
+    (2, 32, 16384), (1, 48, 20480),
 ]
 
 
@@ -98,8 +99,4 @@ def test_w4a8_errors():
     with pytest.raises(M.MriError) as e:
         M.matmul_q4_0_w4a8(dev(np.zeros((2, 64), F32)), w, out, shape=(2, 8, 8))
     assert e.value.kind == "InvalidShape"
-    big = M.Q4Matrix.from_raw_bytes(np.zeros(16 * (12544 // 32) * 18, np.uint8), 16, 12544)
-    with pytest.raises(M.MriError) as e:
-        M.matmul_q4_0_w4a8(dev(np.zeros((1, 12544), F32)), big, out)
-    assert e.value.kind == "Unsupported"
     assert M.Q4Matrix.from_raw_bytes(np.zeros(18 * 16, np.uint8), 16, 32).device_bytes > 0
