@@ -152,35 +152,44 @@ __global__ __launch_bounds__(kWave) void k_skinny_int8(
 // 2(c % 2) + h of piece c / 2 with each nibble moved to the high half of its
 // byte (16 * quant as int8), and the MFMA result is divided by 16 exactly.
 // ---------------------------------------------------------------------------
-template <int AG, int TPW, int RL, bool DEBUG, bool W4>
+template <int AG, int NT, int TPW, int RL, bool DEBUG, bool W4>
 __global__ __launch_bounds__(TPW * kWave) void k_skinny_q8_0(
     const int8_t *__restrict__ act, int M, int kp, const float *__restrict__ sa_rows,
     const v4i *__restrict__ laps, int N, int n_tiles, int G, int nb, float *__restrict__ out,
     int32_t *__restrict__ block_dots, int ns) {
-    // wave -> (tile, set of AG activation groups); the ns waves of a tile are
-    // adjacent, so they share a workgroup (or neighbouring ones) and the
-    // weight chunks they all stream are fetched from HBM once.  With several
-    // workgroups per tile the grid (a multiple of 8) is taken XCD-major:
-    // workgroups are dispatched to the 8 XCDs round-robin, and consecutive
-    // indices of one XCD share its L2.
+    // wave -> (group of NT adjacent tiles, set of AG activation groups); the
+    // ns waves of a tile group are adjacent, so they share a workgroup (or
+    // neighbouring ones) and the weight chunks they all stream are fetched
+    // from HBM once.  NT > 1 spreads each activation load over NT tiles.
+    // With several workgroups per tile group the grid (a multiple of 8) is
+    // taken XCD-major: workgroups are dispatched to the 8 XCDs round-robin,
+    // and consecutive indices of one XCD share its L2.
     int blk = blockIdx.x;
     if (ns > TPW) blk = (int)(blockIdx.x % 8) * (int)(gridDim.x / 8) + (int)(blockIdx.x / 8);
     const int wv = blk * TPW + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int T = wv / ns;
-    const int a0 = (wv - T * ns) * AG;  // first activation group of the wave
-    if (T >= n_tiles) return;  // whole waves only; the kernel has no barrier
+    const int TG = wv / ns;
+    const int a0 = (wv - TG * ns) * AG;  // first activation group of the wave
+    if (TG * NT >= n_tiles) return;  // whole waves only; the kernel has no barrier
     const int l = threadIdx.x & 63;
     const int r = l & 15, g = l >> 4;
-    // the tile's lap blocks: quant piece c of lap q at v4i offset
-    // q * LB + c * 64 (+ lane), the lap's scales at q * LB + SO (+ row)
+    // the tiles' lap blocks: quant piece c of lap q at v4i offset
+    // q * LB + c * 64 (+ lane), the lap's scales at q * LB + SO (+ row);
+    // tiles past the end read the last tile and store nothing
     constexpr size_t LB = (W4 ? kQ4LapBytes : kQ8LapBytes) / 16;
     constexpr int SO = W4 ? 128 : 256;
     constexpr int NP = W4 ? 2 : 4;  // quant pieces per lap and lane
-    const v4i *wp = laps + (size_t)T * G * LB + l;
-    const v4i *sp = laps + (size_t)T * G * LB + SO + r;
-    const int n = T * 16 + r;
+    const v4i *wp[NT];
+    const v4i *sp[NT];
+    int n[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const int T = min(TG * NT + t, n_tiles - 1);
+        wp[t] = laps + (size_t)T * G * LB + l;
+        sp[t] = laps + (size_t)T * G * LB + SO + r;
+        n[t] = TG * NT + t < n_tiles ? (TG * NT + t) * 16 + r : N;
+    }
     const v4i *ap[AG];
-    float sa[AG][4], fs[AG][4];
+    float sa[AG][4], fs[AG][NT][4];
 #pragma unroll
     for (int a = 0; a < AG; ++a) {
         const int m = 16 * (a0 + a) + r;
@@ -188,22 +197,26 @@ __global__ __launch_bounds__(TPW * kWave) void k_skinny_q8_0(
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             sa[a][i] = sa_rows[min(16 * (a0 + a) + 4 * g + i, M - 1)];
-            fs[a][i] = 0.0f;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) fs[a][t][i] = 0.0f;
         }
     }
-    v4i wr[RL][4];
+    v4i wr[RL][NT][4];
     v4i xr[RL][4][AG];
-    v4i sr[RL];
+    v4i sr[RL][NT];
 #pragma unroll
     for (int u = 0; u < RL; ++u) {
         const int q = min(u, G - 1);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            if (c < NP) wr[u][c] = __builtin_nontemporal_load(wp + (size_t)q * LB + c * 64);
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+                if (c < NP) wr[u][t][c] = __builtin_nontemporal_load(wp[t] + (size_t)q * LB + c * 64);
 #pragma unroll
             for (int a = 0; a < AG; ++a) xr[u][c][a] = ap[a][(size_t)(4 * q + c) * 4];
         }
-        sr[u] = sp[(size_t)q * LB];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) sr[u][t] = sp[t][(size_t)q * LB];
     }
     const v4i zero = {0, 0, 0, 0};
 
@@ -213,26 +226,29 @@ __global__ __launch_bounds__(TPW * kWave) void k_skinny_q8_0(
         constexpr int U = decltype(slot)::value;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            v4i d[2][AG];
+            v4i d[2][AG][NT];
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                long bv;
-                if constexpr (W4) {
-                    const v4i pc = wr[U][c >> 1];
-                    const int wd = (c & 1) ? (h ? pc.w : pc.z) : (h ? pc.y : pc.x);
-                    constexpr int kHi = (int)0xF0F0F0F0u;
-                    bv = (long)(((unsigned long)(unsigned)(wd & kHi) << 32) |
-                                (unsigned)((wd << 4) & kHi));
-                } else {
-                    bv = h ? hi8(wr[U][c]) : lo8(wr[U][c]);
-                }
 #pragma unroll
-                for (int a = 0; a < AG; ++a) {
-                    d[h][a] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
-                        h ? hi8(xr[U][c][a]) : lo8(xr[U][c][a]), bv, zero, 0, 0, 0);
+                for (int t = 0; t < NT; ++t) {
+                    long bv;
                     if constexpr (W4) {
+                        const v4i pc = wr[U][t][c >> 1];
+                        const int wd = (c & 1) ? (h ? pc.w : pc.z) : (h ? pc.y : pc.x);
+                        constexpr int kHi = (int)0xF0F0F0F0u;
+                        bv = (long)(((unsigned long)(unsigned)(wd & kHi) << 32) |
+                                    (unsigned)((wd << 4) & kHi));
+                    } else {
+                        bv = h ? hi8(wr[U][t][c]) : lo8(wr[U][t][c]);
+                    }
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) d[h][a][i] >>= 4;
+                    for (int a = 0; a < AG; ++a) {
+                        d[h][a][t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+                            h ? hi8(xr[U][c][a]) : lo8(xr[U][c][a]), bv, zero, 0, 0, 0);
+                        if constexpr (W4) {
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) d[h][a][t][i] >>= 4;
+                        }
                     }
                 }
             }
@@ -240,7 +256,10 @@ __global__ __launch_bounds__(TPW * kWave) void k_skinny_q8_0(
                 const size_t p = (size_t)(4 * (L + RL) + c);
                 if (!W4 || (c & 1)) {
                     const int pi = W4 ? c >> 1 : c;
-                    wr[U][pi] = __builtin_nontemporal_load(wp + (size_t)(L + RL) * LB + pi * 64);
+#pragma unroll
+                    for (int t = 0; t < NT; ++t)
+                        wr[U][t][pi] =
+                            __builtin_nontemporal_load(wp[t] + (size_t)(L + RL) * LB + pi * 64);
                 }
 #pragma unroll
                 for (int a = 0; a < AG; ++a) xr[U][c][a] = ap[a][p * 4];
@@ -249,29 +268,36 @@ __global__ __launch_bounds__(TPW * kWave) void k_skinny_q8_0(
             for (int h = 0; h < 2; ++h) {
                 const int b = 8 * L + 2 * c + h;
                 if (!decltype(check)::value || b < nb) {
-                    const unsigned word = (unsigned)sr[U][c];
-                    const float ds = f16_bits_to_f32(h ? (word >> 16) : (word & 0xFFFFu));
 #pragma unroll
-                    for (int a = 0; a < AG; ++a) {
+                    for (int t = 0; t < NT; ++t) {
+                        const unsigned word = (unsigned)sr[U][t][c];
+                        const float ds = f16_bits_to_f32(h ? (word >> 16) : (word & 0xFFFFu));
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            float t = (float)d[h][a][i] * sa[a][i];
-                            t = t * ds;
-                            fs[a][i] = fs[a][i] + t;
-                        }
-                        if constexpr (DEBUG) {
+                        for (int a = 0; a < AG; ++a) {
 #pragma unroll
                             for (int i = 0; i < 4; ++i) {
-                                const int m = 16 * (a0 + a) + 4 * g + i;
-                                if (m < M && n < N)
-                                    block_dots[((size_t)m * N + n) * nb + b] = d[h][a][i];
+                                float tm = (float)d[h][a][t][i] * sa[a][i];
+                                tm = tm * ds;
+                                fs[a][t][i] = fs[a][t][i] + tm;
+                            }
+                            if constexpr (DEBUG) {
+#pragma unroll
+                                for (int i = 0; i < 4; ++i) {
+                                    const int m = 16 * (a0 + a) + 4 * g + i;
+                                    if (m < M && n[t] < N)
+                                        block_dots[((size_t)m * N + n[t]) * nb + b] =
+                                            d[h][a][t][i];
+                                }
                             }
                         }
                     }
                 }
             }
         }
-        if (refill) sr[U] = sp[(size_t)(L + RL) * LB];
+        if (refill) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) sr[U][t] = sp[t][(size_t)(L + RL) * LB];
+        }
         // keep the next lap's uses of its (younger) loads below this point
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -288,17 +314,26 @@ __global__ __launch_bounds__(TPW * kWave) void k_skinny_q8_0(
             if (u < rem) lap(k * RL + u, u, false, T1{});
         });
     }
-    if (n >= N) return;
 #pragma unroll
-    for (int a = 0; a < AG; ++a)
+    for (int t = 0; t < NT; ++t) {
+        if (n[t] >= N) continue;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int m = 16 * (a0 + a) + 4 * g + i;
-            if (m < M) out[(size_t)m * N + n] = fs[a][i];
-        }
+        for (int a = 0; a < AG; ++a)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = 16 * (a0 + a) + 4 * g + i;
+                if (m < M) out[(size_t)m * N + n[t]] = fs[a][t][i];
+            }
+    }
 }
 
 constexpr int kU = 8;
+
+// Prefill-sized M (one launch, ceil(M/32) waves per tile group): tiles per
+// wave and laps in flight (measured on MI355X at M = 64 .. 2048: two tiles
+// per wave run 1.4-1.5x faster than one; four are slower than two).
+constexpr int kPrefillNT = 2;
+constexpr int kPrefillRL = 2;
 
 template <int MT, int NI, int U>
 void launch_i8(const int8_t *act, size_t m, size_t kp, const float *sa_ptr,
@@ -311,25 +346,27 @@ void launch_i8(const int8_t *act, size_t m, size_t kp, const float *sa_ptr,
 }
 
 // AG activation groups per wave, ns waves per tile (AG * ns groups of 16 rows).
-template <int AG, int TPW, int RL, bool DEBUG, bool W4>
+template <int AG, int NT, int TPW, int RL, bool DEBUG, bool W4>
 void launch_q8_w(const int8_t *act, size_t m, size_t kp, const float *sa_rows,
                  const Q8MatrixDev &w, float *out, int32_t *block_dots, int ns, hipStream_t s) {
     const int G = (int)w.laps_per_tile();
-    const size_t waves = w.n_tiles * (size_t)ns;
+    const size_t waves = (w.n_tiles + NT - 1) / NT * (size_t)ns;
     size_t grid = (waves + TPW - 1) / TPW;
     if (ns > TPW) grid = (grid + 7) / 8 * 8;  // XCD-major mapping (whole waves past the end exit)
-    hipLaunchKernelGGL((k_skinny_q8_0<AG, TPW, RL, DEBUG, W4>),
+    hipLaunchKernelGGL((k_skinny_q8_0<AG, NT, TPW, RL, DEBUG, W4>),
                        dim3((unsigned)grid), dim3(TPW * kWave), 0, s,
                        act, (int)m, (int)kp, sa_rows, reinterpret_cast<const v4i *>(w.laps),
                        (int)w.n_out, (int)w.n_tiles, G,
                        (int)w.n_blocks, out, block_dots, ns);
 }
 
-template <int AG, int TPW, int RL, bool DEBUG>
+template <int AG, int NT, int TPW, int RL, bool DEBUG>
 void launch_q8(const int8_t *act, size_t m, size_t kp, const float *sa_rows,
                const Q8MatrixDev &w, float *out, int32_t *block_dots, int ns, hipStream_t s) {
-    if (w.w4) launch_q8_w<AG, TPW, RL, DEBUG, true>(act, m, kp, sa_rows, w, out, block_dots, ns, s);
-    else launch_q8_w<AG, TPW, RL, DEBUG, false>(act, m, kp, sa_rows, w, out, block_dots, ns, s);
+    if (w.w4)
+        launch_q8_w<AG, NT, TPW, RL, DEBUG, true>(act, m, kp, sa_rows, w, out, block_dots, ns, s);
+    else
+        launch_q8_w<AG, NT, TPW, RL, DEBUG, false>(act, m, kp, sa_rows, w, out, block_dots, ns, s);
 }
 
 }  // namespace
@@ -364,8 +401,10 @@ mri_status launch_skinny_q8_0(const int8_t *act, size_t m,
         // tile, four to a workgroup; the weights stream from HBM about once
         // instead of once per 32-row slice
         const int ns = (int)((m + 31) / 32);
-        if (block_dots) launch_q8<2, 4, 2, true>(act, m, kp, sa_rows, w, out, block_dots, ns, s);
-        else launch_q8<2, 4, 2, false>(act, m, kp, sa_rows, w, out, block_dots, ns, s);
+        if (block_dots)
+            launch_q8<2, kPrefillNT, 4, kPrefillRL, true>(act, m, kp, sa_rows, w, out, block_dots, ns, s);
+        else
+            launch_q8<2, kPrefillNT, 4, kPrefillRL, false>(act, m, kp, sa_rows, w, out, block_dots, ns, s);
         MRI_LAUNCHED("k_skinny_q8_0");
         return MRI_OK;
     }
@@ -378,11 +417,11 @@ mri_status launch_skinny_q8_0(const int8_t *act, size_t m,
         // one wave per tile and workgroup (measured on MI355X: splitting a
         // tile's row groups over waves, or grouping tiles, is slower)
         if (bd) {
-            if (mc <= 16) launch_q8<1, 1, 2, true>(a, mc, kp, sp, w, o, bd, 1, s);
-            else launch_q8<2, 1, 2, true>(a, mc, kp, sp, w, o, bd, 1, s);
+            if (mc <= 16) launch_q8<1, 1, 1, 2, true>(a, mc, kp, sp, w, o, bd, 1, s);
+            else launch_q8<2, 1, 1, 2, true>(a, mc, kp, sp, w, o, bd, 1, s);
         } else {
-            if (mc <= 16) launch_q8<1, 1, 3, false>(a, mc, kp, sp, w, o, bd, 1, s);
-            else launch_q8<2, 1, 2, false>(a, mc, kp, sp, w, o, bd, 1, s);
+            if (mc <= 16) launch_q8<1, 1, 1, 3, false>(a, mc, kp, sp, w, o, bd, 1, s);
+            else launch_q8<2, 1, 1, 2, false>(a, mc, kp, sp, w, o, bd, 1, s);
         }
         MRI_LAUNCHED("k_skinny_q8_0");
     }
