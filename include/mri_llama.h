@@ -80,7 +80,11 @@ mri_status mri_llama_create(const mri_llama_config *cfg, const float *token_embd
                             mri_llama **out);
 /* TransformerBlockInt8::new, forward_int8.rs:168-198: norms are host f32
  * [dim]; w[0..6] = wq [n_heads*hd, dim], wk, wv [n_kv*hd, dim],
- * wo [dim, n_heads*hd], wgate, wup [ffn, dim], wdown [dim, ffn]. */
+ * wo [dim, n_heads*hd], wgate, wup [ffn, dim], wdown [dim, ffn].  When wq,
+ * wk, wv (and wgate, wup) are handles of one format (INT8, Q8_0 or W4A8)
+ * whose n_out are multiples of 16, the model builds owned row
+ * concatenations of them here and projects once per group; outputs equal
+ * the separate projections'.  Setting a layer again replaces them. */
 mri_status mri_llama_set_layer(mri_llama *model, size_t layer, const float *attn_norm,
                                const float *ffn_norm, const mri_weight_ref w[7]);
 void mri_llama_destroy(mri_llama *model);
