@@ -216,6 +216,16 @@ mri_status mri_matmul_q4_0_w4a8(const float *input, const size_t *dims, size_t n
                                 int32_t *block_dots_out, float *act_scales_out,
                                 void *stream);
 
+/* mri_matmul_q4_0_dequant with the nibble order of weight_q4 given
+ * (mri_q4_order): MRI_Q4_ORDER_GGML reads upstream GGML blocks (llama.cpp
+ * files) with the same W4A32 arithmetic.  An option with no counterpart in
+ * the reference; InvalidArgument for an unknown order, then the same checks
+ * in the same order as mri_matmul_q4_0_dequant. */
+mri_status mri_matmul_q4_0_dequant_ordered(const float *input, const size_t *dims,
+                                           size_t ndim, const uint8_t *weight_q4,
+                                           size_t weight_len, size_t n_out, size_t k,
+                                           int order, float *out, void *stream);
+
 /* Waits for all work enqueued on `stream`. */
 mri_status mri_synchronize(void *stream);
 

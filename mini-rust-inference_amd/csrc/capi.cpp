@@ -811,6 +811,16 @@ mri_status mri_matmul_q4_0_w4a8(const float *input, const size_t *dims, size_t n
 mri_status mri_matmul_q4_0_dequant(const float *input, const size_t *dims, size_t ndim,
                                    const uint8_t *weight_q4, size_t weight_len,
                                    size_t n_out, size_t k, float *out, void *stream) {
+    return mri_matmul_q4_0_dequant_ordered(input, dims, ndim, weight_q4, weight_len, n_out, k,
+                                           MRI_Q4_ORDER_INTERLEAVED, out, stream);
+}
+
+mri_status mri_matmul_q4_0_dequant_ordered(const float *input, const size_t *dims, size_t ndim,
+                                           const uint8_t *weight_q4, size_t weight_len,
+                                           size_t n_out, size_t k, int order, float *out,
+                                           void *stream) {
+    if (order != MRI_Q4_ORDER_INTERLEAVED && order != MRI_Q4_ORDER_GGML)
+        return set_error(MRI_ERR_INVALID_ARGUMENT, fmt("unknown Q4_0 nibble order %d", order));
     if (ndim && !dims) return set_error(MRI_ERR_INVALID_ARGUMENT, "dims is null");
     if (ndim != 2)
         return set_error(MRI_ERR_INVALID_SHAPE,
@@ -850,7 +860,7 @@ mri_status mri_matmul_q4_0_dequant(const float *input, const size_t *dims, size_
                                hipMemcpyDeviceToDevice, s));
         x = static_cast<const float *>(base);
     }
-    return launch_q4_0_dequant(x, m, k, weight_q4, n_out, out, s);
+    return launch_q4_0_dequant(x, m, k, weight_q4, n_out, order == MRI_Q4_ORDER_GGML, out, s);
 }
 
 mri_status mri_synchronize(void *stream) {

@@ -218,9 +218,8 @@ mri_status launch_gemm_int8(const int8_t *act_packed, size_t m, const float *sa_
 mri_status gemm_ws_get(hipStream_t stream, size_t bytes, void **ptr);
 
 // q4_0.hip
-mri_status launch_q4_0_dequant(const float *x, size_t m, size_t k,
-                               const uint8_t *w, size_t n_out, float *out,
-                               hipStream_t s);
+mri_status launch_q4_0_dequant(const float *x, size_t m, size_t k, const uint8_t *w,
+                               size_t n_out, bool ggml_order, float *out, hipStream_t s);
 
 // capi.cpp: row concatenation of weight handles (whole 16-row tiles, one K)
 // into a new handle, for fused projections that share their input.

@@ -22,8 +22,13 @@
 // partials are added by a wave reduction.
 //
 // k_q4_0_dequant (any 2-byte aligned layout): one wave per weight row, two
-// lanes per block (8 quant bytes = 16 elements each), with the sum regrouped
-// per block as sum_b d_b * (sum_e x_e * nib_e - 8 * sum_e x_e).
+// lanes per block (16 elements each), with the sum regrouped per block as
+// sum_b d_b * (sum_e x_e * nib_e - 8 * sum_e x_e).
+//
+// GG (an option without a reference counterpart): upstream GGML's nibble
+// order, element i = low nibble of byte i and element i + 16 = its high
+// nibble (llama.cpp Q4_0 files); the lanes then read the bytes of their
+// elements and take one nibble of each.
 #include <algorithm>
 
 #include "common.hpp"
@@ -60,6 +65,17 @@ __device__ inline float nib_dot(unsigned w0, unsigned w1, const float *x) {
     return s;
 }
 
+// 16 bytes (four u32 words) against 16 activations, GGML order: element e
+// is nibble `shift` / 4 of byte e.
+__device__ inline float nib_dot_ggml(const unsigned (&wd)[4], int shift, const float *x) {
+    float s = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+        s = fmaf(x[e], (float)((wd[e >> 2] >> (8 * (e & 3) + shift)) & 0xFu), s);
+    return s;
+}
+
+template <bool GG>
 __global__ __launch_bounds__(kThreads) void k_q4_0_dequant(
     const float *__restrict__ x, int M, int K, const uint16_t *__restrict__ w,
     int N, float *__restrict__ out) {
@@ -77,9 +93,6 @@ __global__ __launch_bounds__(kThreads) void k_q4_0_dequant(
             for (int b = lane >> 1; b < nb; b += 32) {
                 const uint16_t *blk = row + (size_t)b * (kQ4Bytes / 2);
                 const float d = f16_bits_to_f32(blk[0]);
-                const uint16_t *qs = blk + 1 + half * 4;
-                const unsigned w0 = (unsigned)qs[0] | ((unsigned)qs[1] << 16);
-                const unsigned w1 = (unsigned)qs[2] | ((unsigned)qs[3] << 16);
                 const float4 *xv = reinterpret_cast<const float4 *>(xr + b * 32 + half * 16);
                 float xe[16];
 #pragma unroll
@@ -93,7 +106,20 @@ __global__ __launch_bounds__(kThreads) void k_q4_0_dequant(
                 float xs = 0.0f;
 #pragma unroll
                 for (int j = 0; j < 16; ++j) xs += xe[j];
-                const float s = nib_dot(w0, w1, xe);
+                float s;
+                if constexpr (GG) {
+                    // elements 16 half .. +15: nibble `half` of all 16 bytes
+                    unsigned wd[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        wd[i] = (unsigned)blk[1 + 2 * i] | ((unsigned)blk[2 + 2 * i] << 16);
+                    s = nib_dot_ggml(wd, 4 * half, xe);
+                } else {
+                    const uint16_t *qs = blk + 1 + half * 4;
+                    const unsigned w0 = (unsigned)qs[0] | ((unsigned)qs[1] << 16);
+                    const unsigned w1 = (unsigned)qs[2] | ((unsigned)qs[3] << 16);
+                    s = nib_dot(w0, w1, xe);
+                }
                 acc = fmaf(d, fmaf(-8.0f, xs, s), acc);
             }
             for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
@@ -102,7 +128,7 @@ __global__ __launch_bounds__(kThreads) void k_q4_0_dequant(
     }
 }
 
-template <int R>
+template <int R, bool GG>
 __global__ __launch_bounds__(kThreads) void k_q4_0_lds(const float *__restrict__ x, int M, int K,
                                                        const uint8_t *__restrict__ w, int N,
                                                        float *__restrict__ out) {
@@ -147,11 +173,26 @@ __global__ __launch_bounds__(kThreads) void k_q4_0_lds(const float *__restrict__
             for (int r = 0; r < RW; ++r) {
                 const uint8_t *blk = s_w + (size_t)(wv * RW + r) * row_bytes + b * kQ4Bytes;
                 dq[r] = f16_bits_to_f32(*reinterpret_cast<const uint16_t *>(blk));
-                const unsigned q =
-                    (unsigned)*reinterpret_cast<const uint16_t *>(blk + 2 + 4 * p) |
-                    ((unsigned)*reinterpret_cast<const uint16_t *>(blk + 4 + 4 * p) << 16);
-                lo[r] = q & 0x0F0F0F0Fu;          // elements 0, 2, 4, 6 (low nibbles)
-                hi[r] = (q >> 4) & 0x0F0F0F0Fu;   // elements 1, 3, 5, 7
+                if constexpr (GG) {
+                    // elements 8p .. 8p+7: nibble p / 2 of bytes 8 (p % 2) .. +7,
+                    // regrouped into the (even, odd) element words below
+                    const uint16_t *qs = reinterpret_cast<const uint16_t *>(blk + 2 + 8 * (p & 1));
+                    const int sh = 4 * (p >> 1);
+                    const unsigned a0 = ((unsigned)qs[0] | ((unsigned)qs[1] << 16)) >> sh;
+                    const unsigned a1 = ((unsigned)qs[2] | ((unsigned)qs[3] << 16)) >> sh;
+                    // a0 bytes = elements 0..3, a1 bytes = elements 4..7
+                    const unsigned e0 = a0 & 0x0F0F0F0Fu, e1 = a1 & 0x0F0F0F0Fu;
+                    lo[r] = (e0 & 0xFFu) | ((e0 >> 8) & 0xFF00u) | ((e1 << 16) & 0xFF0000u) |
+                            ((e1 << 8) & 0xFF000000u);          // elements 0, 2, 4, 6
+                    hi[r] = ((e0 >> 8) & 0xFFu) | ((e0 >> 16) & 0xFF00u) |
+                            ((e1 << 8) & 0xFF0000u) | (e1 & 0xFF000000u);  // 1, 3, 5, 7
+                } else {
+                    const unsigned q =
+                        (unsigned)*reinterpret_cast<const uint16_t *>(blk + 2 + 4 * p) |
+                        ((unsigned)*reinterpret_cast<const uint16_t *>(blk + 4 + 4 * p) << 16);
+                    lo[r] = q & 0x0F0F0F0Fu;          // elements 0, 2, 4, 6 (low nibbles)
+                    hi[r] = (q >> 4) & 0x0F0F0F0Fu;   // elements 1, 3, 5, 7
+                }
             }
             // d * sum_e x_e * (nib_e - 8) = d * (sum_e x_e * nib_e - 8 * sum_e x_e);
             // the activation sum is shared by the wave's rows, and the rows'
@@ -189,45 +230,52 @@ __global__ __launch_bounds__(kThreads) void k_q4_0_lds(const float *__restrict__
 
 size_t q4_lds_bytes(int r, size_t k) { return (size_t)r * (k / 32) * kQ4Bytes; }
 
-template <int R>
+template <int R, bool GG>
 mri_status launch_lds(const float *x, size_t m, size_t k, const uint8_t *w, size_t n_out,
                       float *out, hipStream_t s) {
     static bool attr_set = false;
     if (!attr_set) {
-        MRI_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_q4_0_lds<R>),
+        MRI_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_q4_0_lds<R, GG>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
         attr_set = true;
     }
-    hipLaunchKernelGGL(k_q4_0_lds<R>, dim3((unsigned)((n_out + R - 1) / R)), dim3(kThreads),
-                       q4_lds_bytes(R, k), s, x, (int)m, (int)k, w, (int)n_out, out);
+    hipLaunchKernelGGL((k_q4_0_lds<R, GG>), dim3((unsigned)((n_out + R - 1) / R)),
+                       dim3(kThreads), q4_lds_bytes(R, k), s, x, (int)m, (int)k, w, (int)n_out,
+                       out);
     MRI_LAUNCHED("k_q4_0_lds");
     return MRI_OK;
 }
 
-}  // namespace
-
-mri_status launch_q4_0_dequant(const float *x, size_t m, size_t k,
-                               const uint8_t *w, size_t n_out, float *out,
-                               hipStream_t s) {
-    if (m == 0 || n_out == 0) return MRI_OK;
+template <bool GG>
+mri_status launch_q4(const float *x, size_t m, size_t k, const uint8_t *w, size_t n_out,
+                     float *out, hipStream_t s) {
     // the staged form: 16-byte aligned rows (K % 256 == 0) and operands, and
     // at most 64 KiB of LDS per workgroup (several workgroups per CU)
     const bool al = ((uintptr_t)w & 15) == 0 && ((uintptr_t)x & 15) == 0 && k % 256 == 0;
     if (al && m <= 4 && k <= (1u << 16) && n_out <= (1u << 30)) {
         // rows per workgroup: 16, 8 or 4, as ~40 KiB of LDS allows
-        if (q4_lds_bytes(16, k) <= 40 * 1024) return launch_lds<16>(x, m, k, w, n_out, out, s);
-        if (q4_lds_bytes(8, k) <= 40 * 1024) return launch_lds<8>(x, m, k, w, n_out, out, s);
-        if (q4_lds_bytes(4, k) <= 48 * 1024) return launch_lds<4>(x, m, k, w, n_out, out, s);
+        if (q4_lds_bytes(16, k) <= 40 * 1024) return launch_lds<16, GG>(x, m, k, w, n_out, out, s);
+        if (q4_lds_bytes(8, k) <= 40 * 1024) return launch_lds<8, GG>(x, m, k, w, n_out, out, s);
+        if (q4_lds_bytes(4, k) <= 48 * 1024) return launch_lds<4, GG>(x, m, k, w, n_out, out, s);
     }
     const size_t waves = (n_out + kRowsPerWave - 1) / kRowsPerWave;
     size_t grid = (waves + (kThreads / 64) - 1) / (kThreads / 64);
     if (grid < 1) grid = 1;
     if (grid > 65535) grid = 65535;
-    hipLaunchKernelGGL(k_q4_0_dequant, dim3((unsigned)grid), dim3(kThreads), 0, s,
+    hipLaunchKernelGGL((k_q4_0_dequant<GG>), dim3((unsigned)grid), dim3(kThreads), 0, s,
                        x, (int)m, (int)k, reinterpret_cast<const uint16_t *>(w),
                        (int)n_out, out);
     MRI_LAUNCHED("k_q4_0_dequant");
     return MRI_OK;
+}
+
+}  // namespace
+
+mri_status launch_q4_0_dequant(const float *x, size_t m, size_t k, const uint8_t *w,
+                               size_t n_out, bool ggml_order, float *out, hipStream_t s) {
+    if (m == 0 || n_out == 0) return MRI_OK;
+    return ggml_order ? launch_q4<true>(x, m, k, w, n_out, out, s)
+                      : launch_q4<false>(x, m, k, w, n_out, out, s);
 }
 
 }  // namespace mri

@@ -62,6 +62,7 @@ _SIGS = {
     "mri_q4_0_matrix_device_bytes": ([P], SZ),
     "mri_q4_0_matrix_destroy": ([P], None),
     "mri_matmul_q4_0_w4a8": ([P, P, SZ, P, P, P, P, P], ST),
+    "mri_matmul_q4_0_dequant_ordered": ([P, P, SZ, P, SZ, SZ, SZ, C.c_int, P, P], ST),
     "mri_synchronize": ([P], ST),
 }
 
@@ -347,6 +348,14 @@ def bind_matmul_int8_from_f32(x, w: QMatrix, out, stream=None):
         if rc != OK:
             check(rc)
     return call
+
+
+def matmul_q4_0_dequant_ordered(x, weight_q4, n_out, k, order, out, stream=None):
+    """W4A32 on raw Q4_0 blocks in the given nibble order (Q4_ORDER_*)."""
+    dims, nd = _dims(tuple(x.shape))
+    check(lib().mri_matmul_q4_0_dequant_ordered(_ptr(x), dims, nd, _ptr(weight_q4),
+                                                weight_q4.numel(), n_out, k, order, _ptr(out),
+                                                _stream(stream)))
 
 
 def matmul_q4_0_dequant(x, weight_q4, n_out, k, out, stream=None, shape=None,

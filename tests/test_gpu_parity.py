@@ -298,6 +298,29 @@ def test_matmul_q4_0_dequant_tolerance(m, n, k):
         assert np.array_equal(host(out2), got)
 
 
+@pytest.mark.parametrize("m,n,k", [(1, 16, 32), (1, 300, 4096), (3, 20, 96), (2, 64, 11008),
+                                   (5, 7, 64), (4, 21, 256), (7, 48, 512)])
+def test_matmul_q4_0_dequant_ggml_order(m, n, k):
+    """W4A32 on GGML-order blocks: the same elements as the interleaved
+    blocks, so the result agrees with the oracle on those to the same
+    contract (both the staged and the fallback kernel)."""
+    say(f"matmul_q4_0 ggml m={m} n={n} k={k}")
+    t = torch()
+    rng = np.random.default_rng(m + n * 5 + k)
+    raw = synth_q4_0(rng, n, k)
+    x = rng.standard_normal((m, k)).astype(F32)
+    out0 = O.matmul_q4_0_dequant(x, raw, n, k)
+    out = empty((m, n), t.float32)
+    mri().matmul_q4_0_dequant_ordered(dev(x), dev(CF.q4_0_interleaved_to_ggml(raw)), n, k,
+                                      mri().Q4_ORDER_GGML, out)
+    scale = np.maximum(np.abs(out0), CF.q4_0_terms_abs_sum(x, raw, n, k))
+    err = np.abs(host(out).astype(np.float64) - out0)
+    assert np.all(err <= 1e-5 * scale), float(np.max(err / scale))
+    with pytest.raises(mri().MriError) as e:
+        mri().matmul_q4_0_dequant_ordered(dev(x), dev(raw), n, k, 7, out)
+    assert e.value.kind == "InvalidArgument"
+
+
 # ---- error behaviour (TensorError kinds and order) ------------------------------------
 
 def test_errors():
