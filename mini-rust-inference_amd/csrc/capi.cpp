@@ -27,6 +27,10 @@ struct mri_q4_0_matrix {
 
 namespace mri {
 
+const QMatrixDev &handle_dev(const mri_qmatrix *h) { return h->d; }
+const Q8MatrixDev &handle_dev(const mri_q8_0_matrix *h) { return h->d; }
+const Q8MatrixDev &handle_dev(const mri_q4_0_matrix *h) { return h->d; }
+
 static thread_local std::string g_last_error;
 
 mri_status set_error(mri_status st, const std::string &msg) {

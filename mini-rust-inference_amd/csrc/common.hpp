@@ -184,17 +184,28 @@ mri_status launch_skinny_q8_0(const int8_t *act, size_t m,
 // through a per-wave ring of loads.  Activations come either as one f32 row
 // x (quantized in the kernel; requires gemv_fusable, M == 1; optional
 // act_q_out [k] and scale_out [1]) or as quantized rows act [m][kp] (Q8_0:
-// chunk-permuted) with their scales.
+// chunk-permuted) with their scales.  norm_w (fused path only, 16-byte
+// aligned [k]): RMS-normalize x with these weights and eps before the
+// quantization.  accum: add the result to out (a residual add) instead of
+// storing it.
 bool gemv_int8_supported(bool fused, size_t m, size_t n_tiles, size_t k, size_t kp);
+// The device matrices behind the public handles (capi.cpp).
+const QMatrixDev &handle_dev(const mri_qmatrix *h);
+const Q8MatrixDev &handle_dev(const mri_q8_0_matrix *h);
+const Q8MatrixDev &handle_dev(const mri_q4_0_matrix *h);
 bool gemv_q8_supported(bool fused, size_t m, size_t n_tiles, size_t k, size_t kp);
 bool gemv_fusable(size_t m, size_t k, const float *x);
 mri_status launch_gemv_int8(const float *x, const int8_t *act, size_t m,
                             const float *sa_ptr, int sa_stride, float sa_value,
                             const QMatrixDev &w, float *out, int8_t *act_q_out,
-                            float *scale_out, int32_t *acc_out, hipStream_t s);
+                            float *scale_out, int32_t *acc_out, hipStream_t s,
+                            const float *norm_w = nullptr, float eps = 0.0f,
+                            bool accum = false);
 mri_status launch_gemv_q8_0(const float *x, const int8_t *act, size_t m,
                             const float *sa_rows, const Q8MatrixDev &w, float *out,
-                            int32_t *block_dots, float *scales_out, hipStream_t s);
+                            int32_t *block_dots, float *scales_out, hipStream_t s,
+                            const float *norm_w = nullptr, float eps = 0.0f,
+                            bool accum = false);
 
 // gemm.hip: prefill-sized M on MFMA with LDS tiles, packed activations.
 constexpr size_t kGemmMinRows = 64;

@@ -82,13 +82,20 @@ __host__ __device__ inline int split_lo(int units, int parts, int w) {
 }
 
 // Activation source of a launch: f32 rows quantized in the kernel (x != 0)
-// or int8 rows of pitch kp already quantized (act != 0).
+// or int8 rows of pitch kp already quantized (act != 0).  With norm_w (fused
+// path only) the row is first RMS-normalized, w * (x * rms_inv) with
+// rms_inv = 1 / sqrt(mean(x^2) + eps) (ops/norm/rmsnorm.rs:100-114), and the
+// normalized row is what gets quantized.  accum: the kernel adds its result
+// to out instead of storing it (the residual add, forward_int8.rs:100-121).
 struct ActIn {
     const float *x;      // [1][K] f32, 16-byte aligned, K % 4 == 0
     const int8_t *act;   // [M][kp] int8 (Q8_0: chunk-permuted), 16-byte aligned
     int K;
     int8_t *act_q_out;   // optional plain [K] int8 (INT8 fused path)
     float *scale_out;    // optional [1] (fused path)
+    const float *norm_w = nullptr;  // optional [K], 16-byte aligned (fused path)
+    float eps = 0.0f;
+    int accum = 0;
 };
 
 // Each thread stages XR 16-byte pieces of the activations in registers:
@@ -110,22 +117,45 @@ __device__ inline void stage_load(const v4i *src, int n16, v4i (&xr)[XR]) {
 // (symmetric.rs:42-57; per row and per tensor coincide for one row) of the
 // row held in xr into LDS (chunk-permuted when perm).  Neither waits for
 // global loads at its barriers beyond the activations'.
+__device__ inline float wave_sum_f(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = v + __shfl_xor(v, o);
+    return v;
+}
+
 template <int S, int XR, bool FUSED>
 __device__ inline void act_begin(const ActIn &in, int n16, const v4i (&xr)[XR], int8_t *s_act,
                                  float *red) {
     const int t = threadIdx.x;
     if constexpr (FUSED) {
         const int K4 = in.K / 4;
-        float mx = 0.0f;
+        if (in.norm_w) {  // sum of squares for the RMS norm
+            float ss = 0.0f;
 #pragma unroll
-        for (int e = 0; e < XR; ++e) {
-            if (t + S * kWave * e < K4) {
-                const float4 v = __builtin_bit_cast(float4, xr[e]);
-                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+            for (int e = 0; e < XR; ++e) {
+                if (t + S * kWave * e < K4) {
+                    const float4 v = __builtin_bit_cast(float4, xr[e]);
+                    ss = ss + v.x * v.x;
+                    ss = ss + v.y * v.y;
+                    ss = ss + v.z * v.z;
+                    ss = ss + v.w * v.w;
+                }
             }
+            ss = wave_sum_f(ss);
+            if ((t & 63) == 0) red[t >> 6] = ss;
+        } else {
+            float mx = 0.0f;
+#pragma unroll
+            for (int e = 0; e < XR; ++e) {
+                if (t + S * kWave * e < K4) {
+                    const float4 v = __builtin_bit_cast(float4, xr[e]);
+                    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)),
+                                         fmaxf(fabsf(v.z), fabsf(v.w))));
+                }
+            }
+            mx = wave_max(mx);
+            if ((t & 63) == 0) red[t >> 6] = mx;
         }
-        mx = wave_max(mx);
-        if ((t & 63) == 0) red[t >> 6] = mx;
     } else {
         v4i *dst = reinterpret_cast<v4i *>(s_act);
 #pragma unroll
@@ -138,16 +168,43 @@ __device__ inline void act_begin(const ActIn &in, int n16, const v4i (&xr)[XR], 
     __builtin_amdgcn_sched_barrier(0);
 }
 
+// wn: the norm weight pieces staged like xr (used when in.norm_w).
 template <int S, int XR, bool FUSED>
-__device__ inline void act_end(const ActIn &in, bool perm, const v4i (&xr)[XR], int8_t *s_act,
-                               const float *red, float &scale, bool writer) {
+__device__ inline void act_end(const ActIn &in, bool perm, v4i (&xr)[XR], const v4i (&wn)[XR],
+                               int8_t *s_act, float *red, float &scale, bool writer) {
     __syncthreads();
     if constexpr (FUSED) {
         const int t = threadIdx.x;
         const int K4 = in.K / 4;
         float mx = 0.0f;
+        if (in.norm_w) {
+            float ss = 0.0f;
 #pragma unroll
-        for (int s = 0; s < S; ++s) mx = fmaxf(mx, red[s]);
+            for (int s = 0; s < S; ++s) ss = ss + red[s];
+            const float mean_sq = __fdiv_rn(ss, (float)in.K);
+            const float rms_inv = __fdiv_rn(1.0f, __fsqrt_rn(mean_sq + in.eps));
+#pragma unroll
+            for (int e = 0; e < XR; ++e) {
+                if (t + S * kWave * e < K4) {
+                    const float4 v = __builtin_bit_cast(float4, xr[e]);
+                    const float4 w = __builtin_bit_cast(float4, wn[e]);
+                    const float4 y = {w.x * (v.x * rms_inv), w.y * (v.y * rms_inv),
+                                      w.z * (v.z * rms_inv), w.w * (v.w * rms_inv)};
+                    xr[e] = __builtin_bit_cast(v4i, y);
+                    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)),
+                                         fmaxf(fabsf(y.z), fabsf(y.w))));
+                }
+            }
+            mx = wave_max(mx);
+            if ((t & 63) == 0) red[S + (t >> 6)] = mx;
+            __syncthreads();
+            mx = 0.0f;
+#pragma unroll
+            for (int s = 0; s < S; ++s) mx = fmaxf(mx, red[S + s]);
+        } else {
+#pragma unroll
+            for (int s = 0; s < S; ++s) mx = fmaxf(mx, red[s]);
+        }
         scale = mx == 0.0f ? 1.0f : __fdiv_rn(mx, 127.0f);
         const float inv = __fdiv_rn(1.0f, scale);
 #pragma unroll

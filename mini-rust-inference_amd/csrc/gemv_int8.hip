@@ -53,11 +53,15 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_int8(
     stage_load<NW, XR>(FUSED ? reinterpret_cast<const v4i *>(in.x)
                              : reinterpret_cast<const v4i *>(in.act),
                        n16, xr);
+    v4i wn[XR];  // RMS norm weights (fused path with in.norm_w)
+    if constexpr (FUSED) {
+        if (in.norm_w) stage_load<NW, XR>(reinterpret_cast<const v4i *>(in.norm_w), n16, wn);
+    }
 #pragma unroll
     for (int s = 0; s < D; ++s)
         wr[s] = __builtin_nontemporal_load(wp + (size_t)min(c0 + s, last) * pitch);
     act_begin<NW, XR, FUSED>(in, n16, xr, s_act, red);
-    act_end<NW, XR, FUSED>(in, false, xr, s_act, red, sa_value, blockIdx.x == 0);
+    act_end<NW, XR, FUSED>(in, false, xr, wn, s_act, red, sa_value, blockIdx.x == 0);
     if constexpr (FUSED) sa_ptr = nullptr;
 
     auto mfma = [&](int s, int i) __attribute__((always_inline)) {
@@ -108,7 +112,8 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_int8(
             const float sa = sa_ptr ? sa_ptr[(size_t)i * sa_stride] : sa_value;
             float v = (float)acc[i] * sa;
             v = v * sw;
-            out[(size_t)i * N + n] = v;
+            float *o = out + (size_t)i * N + n;
+            *o = in.accum ? *o + v : v;
             if (acc_out) acc_out[(size_t)i * N + n] = acc[i];
         }
     }
@@ -180,11 +185,17 @@ bool gemv_fusable(size_t m, size_t k, const float *x) {
 mri_status launch_gemv_int8(const float *x, const int8_t *act, size_t m,
                             const float *sa_ptr, int sa_stride, float sa_value,
                             const QMatrixDev &w, float *out, int8_t *act_q_out,
-                            float *scale_out, int32_t *acc_out, hipStream_t st) {
+                            float *scale_out, int32_t *acc_out, hipStream_t st,
+                            const float *norm_w, float eps, bool accum) {
     if (w.n_tiles == 0 || m == 0) return MRI_OK;
     const CfgI8 c = pick_i8(x != nullptr, w.n_tiles, m, w.k_in, w.kp);
     if (c.s == 0) return set_error(MRI_ERR_INVALID_ARGUMENT, "gemv: shape not supported");
-    const ActIn in{x, act, (int)w.k_in, act_q_out, scale_out};
+    if (norm_w && (!x || (reinterpret_cast<uintptr_t>(norm_w) & 15) != 0))
+        return set_error(MRI_ERR_INVALID_ARGUMENT, "gemv: norm needs the fused path");
+    ActIn in{x, act, (int)w.k_in, act_q_out, scale_out};
+    in.norm_w = norm_w;
+    in.eps = eps;
+    in.accum = accum ? 1 : 0;
     if (x) {
         dispatch_i8<1, true>(c, in, m, nullptr, 0, 0.0f, w, out, acc_out, st);
     } else {

@@ -98,6 +98,10 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     stage_load<NW, XR>(FUSED ? reinterpret_cast<const v4i *>(in.x)
                              : reinterpret_cast<const v4i *>(in.act),
                        n16, xr);
+    v4i wn[XR];  // RMS norm weights (fused path with in.norm_w)
+    if constexpr (FUSED) {
+        if (in.norm_w) stage_load<NW, XR>(reinterpret_cast<const v4i *>(in.norm_w), n16, wn);
+    }
     float sa[LR];
     if constexpr (!FUSED) {
 #pragma unroll
@@ -116,7 +120,7 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
         sr[u] = sp[(size_t)q * LB];
     }
     act_begin<NW, XR, FUSED>(in, n16, xr, s_act, red);
-    act_end<NW, XR, FUSED>(in, true, xr, s_act, red, sa[0], blockIdx.x == 0);
+    act_end<NW, XR, FUSED>(in, true, xr, wn, s_act, red, sa[0], blockIdx.x == 0);
     float fs[LR];
 #pragma unroll
     for (int j = 0; j < LR; ++j) fs[j] = 0.0f;
@@ -255,7 +259,10 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
 #pragma unroll
     for (int j = 0; j < LR; ++j) {
         const int row = 2 * g + j;
-        if (row < M) out[(size_t)row * N + n] = fs[j];
+        if (row < M) {
+            float *o = out + (size_t)row * N + n;
+            *o = in.accum ? *o + fs[j] : fs[j];
+        }
     }
 }
 
@@ -332,11 +339,17 @@ bool gemv_q8_supported(bool fused, size_t m, size_t n_tiles, size_t k, size_t kp
 
 mri_status launch_gemv_q8_0(const float *x, const int8_t *act, size_t m,
                             const float *sa_rows, const Q8MatrixDev &w, float *out,
-                            int32_t *block_dots, float *scales_out, hipStream_t st) {
+                            int32_t *block_dots, float *scales_out, hipStream_t st,
+                            const float *norm_w, float eps, bool accum) {
     if (w.n_tiles == 0 || m == 0) return MRI_OK;
     const CfgQ8 c = pick_q8(x != nullptr, w.n_tiles, m, w.k_in, w.kp, groups_of(w));
     if (c.s == 0) return set_error(MRI_ERR_INVALID_ARGUMENT, "gemv: shape not supported");
-    const ActIn in{x, act, (int)w.k_in, nullptr, scales_out};
+    if (norm_w && (!x || (reinterpret_cast<uintptr_t>(norm_w) & 15) != 0))
+        return set_error(MRI_ERR_INVALID_ARGUMENT, "gemv: norm needs the fused path");
+    ActIn in{x, act, (int)w.k_in, nullptr, scales_out};
+    in.norm_w = norm_w;
+    in.eps = eps;
+    in.accum = accum ? 1 : 0;
     const bool dbg = block_dots != nullptr;
     if (x) {
         dispatch_q8_dbg<1, true>(dbg, c, in, m, nullptr, w, out, block_dots, st);

@@ -52,6 +52,7 @@ struct mri_llama {
     float *attn_part = nullptr;   // split-key decode attention partials
     float *logits_buf = nullptr;  // prefill logits for generation, grown on demand
     size_t logits_rows = 0;
+    int row_path = -1;            // decode rows take the folded path (-1: not yet known)
     std::vector<void *> allocs;
 };
 
@@ -200,21 +201,95 @@ mri_status proj(const mri_weight_ref &w, const float *in, size_t rows, float *ou
     }
 }
 
+// One decode row through the single-row GEMV with the RMSNorm of its input
+// (norm != 0) in the prologue and, with accum, the residual add of its
+// output in the epilogue (out += projection).  row_proj_ok: the GEMV takes
+// the weight.
+bool row_proj_ok(const mri_weight_ref &w) {
+    if (w.k_in == 0 || w.k_in % 4 || w.n_out == 0) return false;
+    switch (w.format) {
+    case MRI_WEIGHT_INT8: {
+        const QMatrixDev &d = handle_dev(static_cast<const mri_qmatrix *>(w.ptr));
+        return gemv_int8_supported(true, 1, d.n_tiles, d.k_in, d.kp);
+    }
+    case MRI_WEIGHT_Q8_0: {
+        const Q8MatrixDev &d = handle_dev(static_cast<const mri_q8_0_matrix *>(w.ptr));
+        return gemv_q8_supported(true, 1, d.n_tiles, d.k_in, d.kp);
+    }
+    case MRI_WEIGHT_Q4_0_W4A8: {
+        const Q8MatrixDev &d = handle_dev(static_cast<const mri_q4_0_matrix *>(w.ptr));
+        return gemv_q8_supported(true, 1, d.n_tiles, d.k_in, d.kp);
+    }
+    default:
+        return false;
+    }
+}
+
+mri_status row_proj(const mri_weight_ref &w, const float *in, const float *norm, float eps,
+                    bool accum, float *out, hipStream_t s) {
+    switch (w.format) {
+    case MRI_WEIGHT_INT8:
+        return launch_gemv_int8(in, nullptr, 1, nullptr, 0, 0.0f,
+                                handle_dev(static_cast<const mri_qmatrix *>(w.ptr)), out,
+                                nullptr, nullptr, nullptr, s, norm, eps, accum);
+    case MRI_WEIGHT_Q8_0:
+        return launch_gemv_q8_0(in, nullptr, 1, nullptr,
+                                handle_dev(static_cast<const mri_q8_0_matrix *>(w.ptr)), out,
+                                nullptr, nullptr, s, norm, eps, accum);
+    case MRI_WEIGHT_Q4_0_W4A8:
+        return launch_gemv_q8_0(in, nullptr, 1, nullptr,
+                                handle_dev(static_cast<const mri_q4_0_matrix *>(w.ptr)), out,
+                                nullptr, nullptr, s, norm, eps, accum);
+    default:
+        return set_error(MRI_ERR_INVALID_ARGUMENT, "row projection: unsupported format");
+    }
+}
+
+// Whether a decode row can run every projection of the model through
+// row_proj (cached until a layer changes).
+bool row_path(mri_llama *m) {
+    if (m->row_path >= 0) return m->row_path != 0;
+    bool ok = row_proj_ok(m->output);
+    for (const Layer &L : m->layers) {
+        if (L.qkv.ptr) ok = ok && row_proj_ok(L.qkv);
+        else ok = ok && row_proj_ok(L.w[0]) && row_proj_ok(L.w[1]) && row_proj_ok(L.w[2]);
+        if (L.gu.ptr) ok = ok && row_proj_ok(L.gu);
+        else ok = ok && row_proj_ok(L.w[4]) && row_proj_ok(L.w[5]);
+        ok = ok && row_proj_ok(L.w[3]) && row_proj_ok(L.w[6]);
+    }
+    m->row_path = ok ? 1 : 0;
+    return ok;
+}
+
 // TransformerBlockInt8::forward_cached (forward_int8.rs:207-216): attention
-// sublayer (:291-323) and FFN sublayer (:350-357).  On entry m->x holds the
-// block's input and m->normed its attention RMSNorm; on exit m->x holds the
-// output and m->normed its RMSNorm with next_norm (the next block's
-// attention norm, or the output norm).  Each residual add is fused with the
-// RMSNorm that follows it; the values are those of the separate steps.
+// sublayer (:291-323) and FFN sublayer (:350-357).  m->x holds the residual
+// stream.  Rows path (fold false): on entry m->normed holds the block's
+// attention RMSNorm; on exit m->normed holds the RMSNorm of the output with
+// next_norm (the next block's attention norm, or the output norm), each
+// residual add fused with the RMSNorm that follows it.  Decode row (fold):
+// each RMSNorm runs in the prologue of the projection that reads it and each
+// residual add in the epilogue of the projection that feeds it (row_proj).
+// Either way the values are those of the separate steps.
 mri_status block(mri_llama *m, size_t li, size_t rows, size_t start, mri_kv_cache *c,
-                 const float *next_norm, hipStream_t s) {
+                 const float *next_norm, bool fold, hipStream_t s) {
     const mri_llama_config &g = m->cfg;
     const Layer &L = m->layers[li];
+    // projections of a normalized row (fold: normalized in the GEMV)
+    auto in_proj = [&](const mri_weight_ref &w, const float *norm, float *out) {
+        return fold ? row_proj(w, m->x, norm, g.eps, false, out, s)
+                    : proj(w, m->normed, rows, out, s);
+    };
+    // projections whose output is added to the residual stream
+    auto out_proj = [&](const mri_weight_ref &w, const float *in, const float *norm) {
+        if (fold) return row_proj(w, in, nullptr, 0.0f, true, m->x, s);
+        TRY(proj(w, in, rows, m->tmp, s));
+        return launch_add_rmsnorm(m->x, m->tmp, rows, g.dim, norm, g.eps, m->normed, s);
+    };
     float *kc = c->k + li * c->max_seq * c->kvd, *vc = c->v + li * c->max_seq * c->kvd;
     float *q, *k, *v;
     size_t qs, kvs;
     if (L.qkv.ptr) {
-        TRY(proj(L.qkv, m->normed, rows, m->qkv, s));
+        TRY(in_proj(L.qkv, L.attn_norm, m->qkv));
         q = m->qkv;
         k = q + m->qd;
         v = k + m->kvd;
@@ -225,30 +300,28 @@ mri_status block(mri_llama *m, size_t li, size_t rows, size_t start, mri_kv_cach
         v = k + rows * m->kvd;
         qs = m->qd;
         kvs = m->kvd;
-        TRY(proj(L.w[0], m->normed, rows, q, s));
-        TRY(proj(L.w[1], m->normed, rows, k, s));
-        TRY(proj(L.w[2], m->normed, rows, v, s));
+        TRY(in_proj(L.w[0], L.attn_norm, q));
+        TRY(in_proj(L.w[1], L.attn_norm, k));
+        TRY(in_proj(L.w[2], L.attn_norm, v));
     }
     TRY(launch_rope_qkv(q, k, v, rows, g.n_heads, g.n_kv_heads, m->hd, qs, kvs, m->cos_t,
                         m->sin_t, start, kc, vc, s));
     TRY(launch_attention(q, qs, rows, kc, vc, g.n_heads, g.n_kv_heads, m->hd, start, m->attn,
                          m->attn_part, s));
-    TRY(proj(L.w[3], m->attn, rows, m->tmp, s));
-    TRY(launch_add_rmsnorm(m->x, m->tmp, rows, g.dim, L.ffn_norm, g.eps, m->normed, s));
+    TRY(out_proj(L.w[3], m->attn, L.ffn_norm));
     float *act;
     if (L.gu.ptr) {
-        TRY(proj(L.gu, m->normed, rows, m->gu, s));
+        TRY(in_proj(L.gu, L.ffn_norm, m->gu));
         act = m->act;
         TRY(launch_swiglu_rows(m->gu, rows, g.ffn_dim, act, s));
     } else {
         act = m->gu;
         float *up = m->gu + rows * g.ffn_dim;
-        TRY(proj(L.w[4], m->normed, rows, act, s));
-        TRY(proj(L.w[5], m->normed, rows, up, s));
+        TRY(in_proj(L.w[4], L.ffn_norm, act));
+        TRY(in_proj(L.w[5], L.ffn_norm, up));
         TRY(launch_swiglu(act, up, rows * g.ffn_dim, act, s));
     }
-    TRY(proj(L.w[6], act, rows, m->tmp, s));
-    return launch_add_rmsnorm(m->x, m->tmp, rows, g.dim, next_norm, g.eps, m->normed, s);
+    return out_proj(L.w[6], act, next_norm);
 }
 
 // embed -> blocks -> rmsnorm -> output projection for `rows` token ids
@@ -256,12 +329,15 @@ mri_status block(mri_llama *m, size_t li, size_t rows, size_t start, mri_kv_cach
 mri_status run_rows(mri_llama *m, const uint32_t *tok_dev, size_t rows, size_t start,
                     mri_kv_cache *c, float *logits, hipStream_t s) {
     const mri_llama_config &g = m->cfg;
+    const bool fold = rows == 1 && row_path(m);
     const float *first = g.n_layers ? m->layers[0].attn_norm : m->out_norm;
-    TRY(launch_embed_rmsnorm(m->embd, tok_dev, rows, g.dim, first, g.eps, m->x, m->normed, s));
+    if (fold) TRY(launch_embed(m->embd, tok_dev, 1, g.dim, m->x, s));
+    else TRY(launch_embed_rmsnorm(m->embd, tok_dev, rows, g.dim, first, g.eps, m->x, m->normed, s));
     for (size_t li = 0; li < g.n_layers; ++li)
         TRY(block(m, li, rows, start, c,
-                  li + 1 < g.n_layers ? m->layers[li + 1].attn_norm : m->out_norm, s));
-    return proj(m->output, m->normed, rows, logits, s);
+                  li + 1 < g.n_layers ? m->layers[li + 1].attn_norm : m->out_norm, fold, s));
+    return fold ? row_proj(m->output, m->x, m->out_norm, g.eps, false, logits, s)
+                : proj(m->output, m->normed, rows, logits, s);
 }
 
 mri_status check_run(mri_llama *m, size_t n, size_t start, mri_kv_cache *c) {
@@ -379,6 +455,7 @@ mri_status mri_llama_set_layer(mri_llama *m, size_t li, const float *attn_norm,
     release_fused(L.qkv);
     release_fused(L.gu);
     L.set = false;
+    m->row_path = -1;
     TRY(fuse(w, 3, &L.qkv));
     TRY(fuse(w + 4, 2, &L.gu));
     L.set = true;
