@@ -101,16 +101,18 @@ mri_status scratch_get(hipStream_t stream, size_t bytes, void **ptr) {
     return MRI_OK;
 }
 
-// Per-(device, stream) workspace of the stream-K GEMM.  Zeroed whenever it
-// is (re)allocated; the kernel leaves its counters zero after every call.
+// Per-(device, stream) workspaces of the kernels that count arrivals (the
+// stream-K GEMM, the one-row argmax).  Zeroed whenever they are
+// (re)allocated; the kernels leave their counters zero after every call.
 static std::mutex g_ws_mu;
-static std::map<std::pair<int, hipStream_t>, Scratch> g_ws;
+static std::map<std::pair<int, hipStream_t>, Scratch> g_ws, g_aws;
 
-mri_status gemm_ws_get(hipStream_t stream, size_t bytes, void **ptr) {
+static mri_status zeroed_ws_get(std::map<std::pair<int, hipStream_t>, Scratch> &map,
+                                hipStream_t stream, size_t bytes, void **ptr) {
     int dev = 0;
     MRI_HIP(hipGetDevice(&dev));
     std::lock_guard<std::mutex> lk(g_ws_mu);
-    Scratch &sc = g_ws[{dev, stream}];
+    Scratch &sc = map[{dev, stream}];
     if (sc.bytes < bytes) {
         const size_t want = round_up(bytes, 1u << 20);
         if (sc.ptr) {
@@ -125,6 +127,14 @@ mri_status gemm_ws_get(hipStream_t stream, size_t bytes, void **ptr) {
     }
     *ptr = sc.ptr;
     return MRI_OK;
+}
+
+mri_status gemm_ws_get(hipStream_t stream, size_t bytes, void **ptr) {
+    return zeroed_ws_get(g_ws, stream, bytes, ptr);
+}
+
+mri_status argmax_ws_get(hipStream_t stream, void **ptr) {
+    return zeroed_ws_get(g_aws, stream, kArgmaxWsBytes, ptr);
 }
 
 static inline bool aligned(const void *p, size_t a) {

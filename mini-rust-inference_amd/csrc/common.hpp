@@ -184,10 +184,17 @@ mri_status launch_skinny_q8_0(const int8_t *act, size_t m,
 // through a per-wave ring of loads.  Activations come either as one f32 row
 // x (quantized in the kernel; requires gemv_fusable, M == 1; optional
 // act_q_out [k] and scale_out [1]) or as quantized rows act [m][kp] (Q8_0:
-// chunk-permuted) with their scales.  norm_w (fused path only, 16-byte
-// aligned [k]): RMS-normalize x with these weights and eps before the
-// quantization.  accum: add the result to out (a residual add) instead of
-// storing it.
+// chunk-permuted) with their scales.  ops: the single-row extras below.
+//
+// RowOps: what the fused path (one f32 row) can do besides the projection.
+// Every pointer is 16-byte aligned and holds k floats.
+struct RowOps {
+    const float *norm_w = nullptr;  // RMS-normalize the row with these weights and eps
+    float eps = 0.0f;
+    float *x_out = nullptr;         // receives a copy of x as read
+    bool accum = false;             // out += the projection (a residual add)
+    bool any() const { return norm_w || x_out || accum; }
+};
 bool gemv_int8_supported(bool fused, size_t m, size_t n_tiles, size_t k, size_t kp);
 // The device matrices behind the public handles (capi.cpp).
 const QMatrixDev &handle_dev(const mri_qmatrix *h);
@@ -195,17 +202,16 @@ const Q8MatrixDev &handle_dev(const mri_q8_0_matrix *h);
 const Q8MatrixDev &handle_dev(const mri_q4_0_matrix *h);
 bool gemv_q8_supported(bool fused, size_t m, size_t n_tiles, size_t k, size_t kp);
 bool gemv_fusable(size_t m, size_t k, const float *x);
+bool row_ops_ok(const float *x, const RowOps &ops);
 mri_status launch_gemv_int8(const float *x, const int8_t *act, size_t m,
                             const float *sa_ptr, int sa_stride, float sa_value,
                             const QMatrixDev &w, float *out, int8_t *act_q_out,
                             float *scale_out, int32_t *acc_out, hipStream_t s,
-                            const float *norm_w = nullptr, float eps = 0.0f,
-                            bool accum = false);
+                            const RowOps &ops = RowOps{});
 mri_status launch_gemv_q8_0(const float *x, const int8_t *act, size_t m,
                             const float *sa_rows, const Q8MatrixDev &w, float *out,
                             int32_t *block_dots, float *scales_out, hipStream_t s,
-                            const float *norm_w = nullptr, float eps = 0.0f,
-                            bool accum = false);
+                            const RowOps &ops = RowOps{});
 
 // gemm.hip: prefill-sized M on MFMA with LDS tiles, packed activations.
 constexpr size_t kGemmMinRows = 64;
@@ -273,6 +279,13 @@ mri_status launch_swiglu(const float *gate, const float *up, size_t n, float *ou
 mri_status launch_swiglu_rows(const float *gu, size_t rows, size_t ffn, float *out,
                               hipStream_t s);
 mri_status launch_add(const float *a, const float *b, size_t n, float *out, hipStream_t s);
+// rows == 1 runs a split form whose blocks meet through a counter in the
+// stream's argmax workspace (argmax_ws_get: kArgmaxWsBytes, zeroed).
 mri_status launch_argmax(const float *v, size_t rows, size_t n, uint32_t *idx, hipStream_t s);
+constexpr size_t kArgmaxWsBytes = 4096;
+mri_status argmax_ws_get(hipStream_t stream, void **ptr);
+// One row: the argmax, then row idx of table ([*][d]) copied to x_out.
+mri_status launch_argmax_embed(const float *v, size_t n, uint32_t *idx, const float *table,
+                               size_t d, float *x_out, hipStream_t s);
 
 }  // namespace mri

@@ -82,11 +82,13 @@ __host__ __device__ inline int split_lo(int units, int parts, int w) {
 }
 
 // Activation source of a launch: f32 rows quantized in the kernel (x != 0)
-// or int8 rows of pitch kp already quantized (act != 0).  With norm_w (fused
-// path only) the row is first RMS-normalized, w * (x * rms_inv) with
-// rms_inv = 1 / sqrt(mean(x^2) + eps) (ops/norm/rmsnorm.rs:100-114), and the
-// normalized row is what gets quantized.  accum: the kernel adds its result
-// to out instead of storing it (the residual add, forward_int8.rs:100-121).
+// or int8 rows of pitch kp already quantized (act != 0).  Kernel instances
+// with OPS take the row operations (RowOps, in common.hpp) as well: with
+// norm_w, the fused row is RMS-normalized before it is quantized,
+// w * (x * rms_inv) with rms_inv = 1 / sqrt(mean(x^2) + eps)
+// (ops/norm/rmsnorm.rs:100-114); x_out receives a copy of the row as read;
+// accum: the kernel adds its result to out instead of storing it (the
+// residual add, forward_int8.rs:100-121).
 struct ActIn {
     const float *x;      // [1][K] f32, 16-byte aligned, K % 4 == 0
     const int8_t *act;   // [M][kp] int8 (Q8_0: chunk-permuted), 16-byte aligned
@@ -95,7 +97,12 @@ struct ActIn {
     float *scale_out;    // optional [1] (fused path)
     const float *norm_w = nullptr;  // optional [K], 16-byte aligned (fused path)
     float eps = 0.0f;
+    float *x_out = nullptr;         // optional [K], 16-byte aligned (fused path)
     int accum = 0;
+
+    ActIn(const float *x_, const int8_t *act_, int k, int8_t *aq, float *so, const RowOps &o)
+        : x(x_), act(act_), K(k), act_q_out(aq), scale_out(so), norm_w(o.norm_w), eps(o.eps),
+          x_out(o.x_out), accum(o.accum ? 1 : 0) {}
 };
 
 // Each thread stages XR 16-byte pieces of the activations in registers:
@@ -123,13 +130,19 @@ __device__ inline float wave_sum_f(float v) {
     return v;
 }
 
-template <int S, int XR, bool FUSED>
+template <int S, int XR, bool FUSED, bool OPS>
 __device__ inline void act_begin(const ActIn &in, int n16, const v4i (&xr)[XR], int8_t *s_act,
                                  float *red) {
     const int t = threadIdx.x;
     if constexpr (FUSED) {
         const int K4 = in.K / 4;
-        if (in.norm_w) {  // sum of squares for the RMS norm
+        if (OPS && in.x_out && blockIdx.x == 0) {
+#pragma unroll
+            for (int e = 0; e < XR; ++e)
+                if (t + S * kWave * e < K4)
+                    reinterpret_cast<v4i *>(in.x_out)[t + S * kWave * e] = xr[e];
+        }
+        if (OPS && in.norm_w) {  // sum of squares for the RMS norm
             float ss = 0.0f;
 #pragma unroll
             for (int e = 0; e < XR; ++e) {
@@ -169,7 +182,7 @@ __device__ inline void act_begin(const ActIn &in, int n16, const v4i (&xr)[XR], 
 }
 
 // wn: the norm weight pieces staged like xr (used when in.norm_w).
-template <int S, int XR, bool FUSED>
+template <int S, int XR, bool FUSED, bool OPS>
 __device__ inline void act_end(const ActIn &in, bool perm, v4i (&xr)[XR], const v4i (&wn)[XR],
                                int8_t *s_act, float *red, float &scale, bool writer) {
     __syncthreads();
@@ -177,7 +190,7 @@ __device__ inline void act_end(const ActIn &in, bool perm, v4i (&xr)[XR], const 
         const int t = threadIdx.x;
         const int K4 = in.K / 4;
         float mx = 0.0f;
-        if (in.norm_w) {
+        if (OPS && in.norm_w) {
             float ss = 0.0f;
 #pragma unroll
             for (int s = 0; s < S; ++s) ss = ss + red[s];

@@ -14,7 +14,7 @@ namespace {
 // ---------------------------------------------------------------------------
 // Per-channel INT8.
 // ---------------------------------------------------------------------------
-template <int NI, int S, int TPW, int D, int XR, bool FUSED>
+template <int NI, int S, int TPW, int D, int XR, bool FUSED, bool OPS>
 __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_int8(
     ActIn in, int M, int kp, const float *__restrict__ sa_ptr, int sa_stride,
     float sa_value, const v4i *__restrict__ tiles, const float *__restrict__ wscales,
@@ -53,15 +53,15 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_int8(
     stage_load<NW, XR>(FUSED ? reinterpret_cast<const v4i *>(in.x)
                              : reinterpret_cast<const v4i *>(in.act),
                        n16, xr);
-    v4i wn[XR];  // RMS norm weights (fused path with in.norm_w)
-    if constexpr (FUSED) {
+    v4i wn[XR];  // RMS norm weights (row operations)
+    if constexpr (FUSED && OPS) {
         if (in.norm_w) stage_load<NW, XR>(reinterpret_cast<const v4i *>(in.norm_w), n16, wn);
     }
 #pragma unroll
     for (int s = 0; s < D; ++s)
         wr[s] = __builtin_nontemporal_load(wp + (size_t)min(c0 + s, last) * pitch);
-    act_begin<NW, XR, FUSED>(in, n16, xr, s_act, red);
-    act_end<NW, XR, FUSED>(in, false, xr, wn, s_act, red, sa_value, blockIdx.x == 0);
+    act_begin<NW, XR, FUSED, OPS>(in, n16, xr, s_act, red);
+    act_end<NW, XR, FUSED, OPS>(in, false, xr, wn, s_act, red, sa_value, blockIdx.x == 0);
     if constexpr (FUSED) sa_ptr = nullptr;
 
     auto mfma = [&](int s, int i) __attribute__((always_inline)) {
@@ -113,7 +113,7 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_int8(
             float v = (float)acc[i] * sa;
             v = v * sw;
             float *o = out + (size_t)i * N + n;
-            *o = in.accum ? *o + v : v;
+            *o = OPS && in.accum ? *o + v : v;
             if (acc_out) acc_out[(size_t)i * N + n] = acc[i];
         }
     }
@@ -146,24 +146,24 @@ CfgI8 pick_i8(bool fused, size_t n_tiles, size_t m, size_t k, size_t kp) {
     return c;
 }
 
-template <int NI, int S, int TPW, int D, int XR, bool FUSED>
+template <int NI, int S, int TPW, int D, int XR, bool FUSED, bool OPS>
 void launch_i8(ActIn in, size_t m, const float *sa_ptr, int sa_stride, float sa_value,
                const QMatrixDev &w, float *out, int32_t *acc_out, hipStream_t st) {
-    hipLaunchKernelGGL((k_gemv_int8<NI, S, TPW, D, XR, FUSED>),
+    hipLaunchKernelGGL((k_gemv_int8<NI, S, TPW, D, XR, FUSED, OPS>),
                        dim3((unsigned)ceil_div(w.n_tiles, TPW)), dim3(S * TPW * kWave),
                        lds_i8(S, TPW, m, w.kp), st, in, (int)m, (int)w.kp, sa_ptr, sa_stride,
                        sa_value, reinterpret_cast<const v4i *>(w.tiles), w.scales,
                        (int)w.n_out, (int)w.n_tiles, (int)(w.kp / kChunkK), out, acc_out);
 }
 
-template <int NI, bool FUSED>
+template <int NI, bool FUSED, bool OPS = false>
 void dispatch_i8(CfgI8 c, ActIn in, size_t m, const float *sa_ptr, int sa_stride,
                  float sa_value, const QMatrixDev &w, float *out, int32_t *acc_out,
                  hipStream_t st) {
 #define MRI_I8(S_, TPW_, D_, XR_)                                                          \
     if (c.s == S_ && c.tpw == TPW_ && c.d == D_ && c.xr == XR_)                            \
-        return launch_i8<NI, S_, TPW_, D_, XR_, FUSED>(in, m, sa_ptr, sa_stride, sa_value, \
-                                                       w, out, acc_out, st);
+        return launch_i8<NI, S_, TPW_, D_, XR_, FUSED, OPS>(in, m, sa_ptr, sa_stride,      \
+                                                            sa_value, w, out, acc_out, st);
     MRI_I8(1, 8, 8, 4) MRI_I8(1, 8, 8, 8) MRI_I8(1, 8, 8, 12)
     MRI_I8(4, 1, 4, 4) MRI_I8(4, 1, 4, 8) MRI_I8(4, 1, 4, 12)
     MRI_I8(4, 1, 8, 4) MRI_I8(4, 1, 8, 8) MRI_I8(4, 1, 8, 12)
@@ -177,6 +177,13 @@ bool gemv_int8_supported(bool fused, size_t m, size_t n_tiles, size_t k, size_t 
     return m >= 1 && m <= (size_t)kMaxM && pick_i8(fused, n_tiles, m, k, kp).s > 0;
 }
 
+// The row operations apply to the fused path only, with aligned operands.
+bool row_ops_ok(const float *x, const RowOps &o) {
+    auto al = [](const float *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    if (!o.any()) return true;
+    return x && al(o.norm_w) && al(o.x_out);
+}
+
 bool gemv_fusable(size_t m, size_t k, const float *x) {
     return m == 1 && k > 0 && k % 4 == 0 && x &&
            (reinterpret_cast<uintptr_t>(x) & 15) == 0;
@@ -186,17 +193,16 @@ mri_status launch_gemv_int8(const float *x, const int8_t *act, size_t m,
                             const float *sa_ptr, int sa_stride, float sa_value,
                             const QMatrixDev &w, float *out, int8_t *act_q_out,
                             float *scale_out, int32_t *acc_out, hipStream_t st,
-                            const float *norm_w, float eps, bool accum) {
+                            const RowOps &ops) {
     if (w.n_tiles == 0 || m == 0) return MRI_OK;
     const CfgI8 c = pick_i8(x != nullptr, w.n_tiles, m, w.k_in, w.kp);
     if (c.s == 0) return set_error(MRI_ERR_INVALID_ARGUMENT, "gemv: shape not supported");
-    if (norm_w && (!x || (reinterpret_cast<uintptr_t>(norm_w) & 15) != 0))
-        return set_error(MRI_ERR_INVALID_ARGUMENT, "gemv: norm needs the fused path");
-    ActIn in{x, act, (int)w.k_in, act_q_out, scale_out};
-    in.norm_w = norm_w;
-    in.eps = eps;
-    in.accum = accum ? 1 : 0;
-    if (x) {
+    if (!row_ops_ok(x, ops))
+        return set_error(MRI_ERR_INVALID_ARGUMENT, "gemv: row operations need the fused path");
+    const ActIn in(x, act, (int)w.k_in, act_q_out, scale_out, ops);
+    if (ops.any()) {
+        dispatch_i8<1, true, true>(c, in, m, nullptr, 0, 0.0f, w, out, acc_out, st);
+    } else if (x) {
         dispatch_i8<1, true>(c, in, m, nullptr, 0, 0.0f, w, out, acc_out, st);
     } else {
         if (m == 1) dispatch_i8<1, false>(c, in, m, sa_ptr, sa_stride, sa_value, w, out, acc_out, st);

@@ -44,7 +44,7 @@ __device__ inline void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-template <int MR, int S, int TPW, int RL, int XR, bool FUSED, bool DEBUG, bool W4>
+template <int MR, int S, int TPW, int RL, int XR, bool FUSED, bool OPS, bool DEBUG, bool W4>
 __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     ActIn in, int M, int kp, const float *__restrict__ sa_rows,
     const v4i *__restrict__ laps, int N, int n_tiles, int G, int nb, float *__restrict__ out,
@@ -98,8 +98,8 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     stage_load<NW, XR>(FUSED ? reinterpret_cast<const v4i *>(in.x)
                              : reinterpret_cast<const v4i *>(in.act),
                        n16, xr);
-    v4i wn[XR];  // RMS norm weights (fused path with in.norm_w)
-    if constexpr (FUSED) {
+    v4i wn[XR];  // RMS norm weights (row operations)
+    if constexpr (FUSED && OPS) {
         if (in.norm_w) stage_load<NW, XR>(reinterpret_cast<const v4i *>(in.norm_w), n16, wn);
     }
     float sa[LR];
@@ -119,8 +119,8 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
             wr[u][s] = __builtin_nontemporal_load(wp + (size_t)q * LB + s * 64);
         sr[u] = sp[(size_t)q * LB];
     }
-    act_begin<NW, XR, FUSED>(in, n16, xr, s_act, red);
-    act_end<NW, XR, FUSED>(in, true, xr, wn, s_act, red, sa[0], blockIdx.x == 0);
+    act_begin<NW, XR, FUSED, OPS>(in, n16, xr, s_act, red);
+    act_end<NW, XR, FUSED, OPS>(in, true, xr, wn, s_act, red, sa[0], blockIdx.x == 0);
     float fs[LR];
 #pragma unroll
     for (int j = 0; j < LR; ++j) fs[j] = 0.0f;
@@ -261,7 +261,7 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
         const int row = 2 * g + j;
         if (row < M) {
             float *o = out + (size_t)row * N + n;
-            *o = in.accum ? *o + fs[j] : fs[j];
+            *o = OPS && in.accum ? *o + fs[j] : fs[j];
         }
     }
 }
@@ -298,25 +298,25 @@ CfgQ8 pick_q8(bool fused, size_t n_tiles, size_t m, size_t k, size_t kp, size_t 
 
 inline size_t groups_of(const Q8MatrixDev &w) { return w.laps_per_tile(); }
 
-template <int MR, int S, int TPW, int RL, int XR, bool FUSED, bool DEBUG, bool W4>
+template <int MR, int S, int TPW, int RL, int XR, bool FUSED, bool OPS, bool DEBUG, bool W4>
 void launch_q8(ActIn in, size_t m, const float *sa_rows, const Q8MatrixDev &w,
                float *out, int32_t *block_dots, hipStream_t st) {
     const size_t G = groups_of(w);
-    hipLaunchKernelGGL((k_gemv_q8_0<MR, S, TPW, RL, XR, FUSED, DEBUG, W4>),
+    hipLaunchKernelGGL((k_gemv_q8_0<MR, S, TPW, RL, XR, FUSED, OPS, DEBUG, W4>),
                        dim3((unsigned)ceil_div(w.n_tiles, TPW)), dim3(S * TPW * kWave),
                        lds_q8(S, TPW, m, w.kp, G), st, in, (int)m, (int)w.kp, sa_rows,
                        reinterpret_cast<const v4i *>(w.laps), (int)w.n_out,
                        (int)w.n_tiles, (int)G, (int)w.n_blocks, out, block_dots);
 }
 
-template <int MR, bool FUSED, bool DEBUG>
+template <int MR, bool FUSED, bool OPS, bool DEBUG>
 void dispatch_q8(CfgQ8 c, ActIn in, size_t m, const float *sa_rows, const Q8MatrixDev &w,
                  float *out, int32_t *block_dots, hipStream_t st) {
 #define MRI_Q8(S_, TPW_, RL_, XR_)                                                         \
     if (c.s == S_ && c.tpw == TPW_ && c.rl == RL_ && c.xr == XR_)                          \
-        return w.w4 ? launch_q8<MR, S_, TPW_, RL_, XR_, FUSED, DEBUG, true>(               \
+        return w.w4 ? launch_q8<MR, S_, TPW_, RL_, XR_, FUSED, OPS, DEBUG, true>(          \
                           in, m, sa_rows, w, out, block_dots, st)                          \
-                    : launch_q8<MR, S_, TPW_, RL_, XR_, FUSED, DEBUG, false>(              \
+                    : launch_q8<MR, S_, TPW_, RL_, XR_, FUSED, OPS, DEBUG, false>(         \
                           in, m, sa_rows, w, out, block_dots, st);
     MRI_Q8(4, 1, 1, 4) MRI_Q8(4, 1, 1, 12)
     MRI_Q8(4, 1, 2, 4) MRI_Q8(4, 1, 2, 12)
@@ -326,8 +326,8 @@ void dispatch_q8(CfgQ8 c, ActIn in, size_t m, const float *sa_rows, const Q8Matr
 template <int MR, bool FUSED>
 void dispatch_q8_dbg(bool dbg, CfgQ8 c, ActIn in, size_t m, const float *sa_rows,
                      const Q8MatrixDev &w, float *out, int32_t *block_dots, hipStream_t st) {
-    if (dbg) dispatch_q8<MR, FUSED, true>(c, in, m, sa_rows, w, out, block_dots, st);
-    else dispatch_q8<MR, FUSED, false>(c, in, m, sa_rows, w, out, nullptr, st);
+    if (dbg) dispatch_q8<MR, FUSED, false, true>(c, in, m, sa_rows, w, out, block_dots, st);
+    else dispatch_q8<MR, FUSED, false, false>(c, in, m, sa_rows, w, out, nullptr, st);
 }
 
 }  // namespace
@@ -340,18 +340,18 @@ bool gemv_q8_supported(bool fused, size_t m, size_t n_tiles, size_t k, size_t kp
 mri_status launch_gemv_q8_0(const float *x, const int8_t *act, size_t m,
                             const float *sa_rows, const Q8MatrixDev &w, float *out,
                             int32_t *block_dots, float *scales_out, hipStream_t st,
-                            const float *norm_w, float eps, bool accum) {
+                            const RowOps &ops) {
     if (w.n_tiles == 0 || m == 0) return MRI_OK;
     const CfgQ8 c = pick_q8(x != nullptr, w.n_tiles, m, w.k_in, w.kp, groups_of(w));
     if (c.s == 0) return set_error(MRI_ERR_INVALID_ARGUMENT, "gemv: shape not supported");
-    if (norm_w && (!x || (reinterpret_cast<uintptr_t>(norm_w) & 15) != 0))
-        return set_error(MRI_ERR_INVALID_ARGUMENT, "gemv: norm needs the fused path");
-    ActIn in{x, act, (int)w.k_in, nullptr, scales_out};
-    in.norm_w = norm_w;
-    in.eps = eps;
-    in.accum = accum ? 1 : 0;
+    if (!row_ops_ok(x, ops))
+        return set_error(MRI_ERR_INVALID_ARGUMENT, "gemv: row operations need the fused path");
+    const ActIn in(x, act, (int)w.k_in, nullptr, scales_out, ops);
     const bool dbg = block_dots != nullptr;
-    if (x) {
+    if (ops.any()) {
+        if (dbg) return set_error(MRI_ERR_INVALID_ARGUMENT, "gemv: row operations without debug outputs");
+        dispatch_q8<1, true, true, false>(c, in, m, nullptr, w, out, nullptr, st);
+    } else if (x) {
         dispatch_q8_dbg<1, true>(dbg, c, in, m, nullptr, w, out, block_dots, st);
     } else {
         if (m == 1) dispatch_q8_dbg<1, false>(dbg, c, in, m, sa_rows, w, out, block_dots, st);

@@ -556,6 +556,113 @@ __global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ v, in
     }
 }
 
+// (value, index) order of the argmax: a larger value, then a larger index
+// (the last of equal values); oi < 0 is no candidate.
+__device__ inline bool arg_better(float ov, int oi, float bv, int bi) {
+    return oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi > bi));
+}
+
+// One row split over the blocks: block b reduces its slice, stores its
+// (value, index) and counts itself; the block that counts last combines
+// the gridDim.x <= 64 candidates, writes idx[0], resets the counter, and
+// with table copies row idx of table ([*][d] f32) to x_out.  ws: the
+// counter at word 0, candidate values at words 4.., indices at 68...
+// The candidates are stored and loaded with device-scope (sc1) accesses,
+// which reach the point of coherence of all XCDs, and each block waits for
+// its stores to complete before it counts, so no cache-wide fence is needed.
+// The counter is updated at system scope, which performs the atomic past
+// every XCD's L2.
+constexpr int kArgSplit = 64;
+__global__ __launch_bounds__(256) void k_argmax_split(const float *__restrict__ v, int n,
+                                                      uint32_t *__restrict__ idx,
+                                                      const float *__restrict__ table, int d,
+                                                      float *__restrict__ x_out,
+                                                      unsigned *__restrict__ ws) {
+    __shared__ float s_v[4];
+    __shared__ int s_i[4];
+    __shared__ int s_last, s_tok;
+    unsigned *count = ws;
+    int *part_v = reinterpret_cast<int *>(ws + 4);
+    int *part_i = reinterpret_cast<int *>(ws + 4 + kArgSplit);
+    const int per = (n + (int)gridDim.x - 1) / (int)gridDim.x;
+    const int lo = (int)blockIdx.x * per, hi = min(n, lo + per);
+    float bv = -INFINITY;
+    int bi = -1;
+    // four loads in flight per thread; within a thread indices only grow,
+    // so ">=" keeps the last of equal values
+    for (int i0 = lo + (int)threadIdx.x; i0 < hi; i0 += 4 * 256) {
+        float xs[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) xs[u] = v[min(i0 + u * 256, hi - 1)];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = i0 + u * 256;
+            const float x = xs[u];
+            if (i < hi && !(x != x) && (bi < 0 || x >= bv)) {
+                bv = x;
+                bi = i;
+            }
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, kWave);
+        const int oi = __shfl_xor(bi, o, kWave);
+        if (arg_better(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if ((threadIdx.x & 63) == 0) {
+        s_v[threadIdx.x >> 6] = bv;
+        s_i[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; ++w)
+            if (arg_better(s_v[w], s_i[w], bv, bi)) {
+                bv = s_v[w];
+                bi = s_i[w];
+            }
+        __hip_atomic_store(&part_v[blockIdx.x], __float_as_int(bv), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&part_i[blockIdx.x], bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the candidate has reached the device
+        s_last = __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) ==
+                 gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    if (threadIdx.x < 64) {
+        const int b = threadIdx.x;
+        float cv = -INFINITY;
+        int ci = -1;
+        if (b < (int)gridDim.x) {
+            cv = __int_as_float(
+                __hip_atomic_load(&part_v[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+            ci = __hip_atomic_load(&part_i[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(cv, o, kWave);
+            const int oi = __shfl_xor(ci, o, kWave);
+            if (arg_better(ov, oi, cv, ci)) {
+                cv = ov;
+                ci = oi;
+            }
+        }
+        if (b == 0) {
+            idx[0] = ci < 0 ? 0u : (uint32_t)ci;
+            s_tok = ci < 0 ? 0 : ci;
+            __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+    }
+    if (!table) return;
+    __syncthreads();
+    const float *src = table + (size_t)s_tok * d;
+    for (int i = threadIdx.x; i < d; i += 256) x_out[i] = src[i];
+}
+
 // query rows per prefill workgroup: 16, else 4 when the weight rows do not fit
 template <int HD, int QB>
 size_t attn_lds(int lcap) {
@@ -784,11 +891,30 @@ mri_status launch_add(const float *a, const float *b, size_t n, float *out, hipS
     return MRI_OK;
 }
 
+static mri_status launch_argmax_split(const float *v, size_t n, uint32_t *idx,
+                                      const float *table, size_t d, float *x_out,
+                                      hipStream_t s) {
+    void *ws = nullptr;
+    mri_status st = argmax_ws_get(s, &ws);
+    if (st) return st;
+    const unsigned blocks = (unsigned)std::min<size_t>(kArgSplit, std::max<size_t>(1, n / 512));
+    hipLaunchKernelGGL(k_argmax_split, dim3(blocks), dim3(256), 0, s, v, (int)n, idx, table,
+                       (int)d, x_out, static_cast<unsigned *>(ws));
+    MRI_LAUNCHED("k_argmax_split");
+    return MRI_OK;
+}
+
 mri_status launch_argmax(const float *v, size_t rows, size_t n, uint32_t *idx, hipStream_t s) {
     if (!rows) return MRI_OK;
+    if (rows == 1) return launch_argmax_split(v, n, idx, nullptr, 0, nullptr, s);
     hipLaunchKernelGGL(k_argmax, dim3((unsigned)rows), dim3(1024), 0, s, v, (int)n, idx);
     MRI_LAUNCHED("k_argmax");
     return MRI_OK;
+}
+
+mri_status launch_argmax_embed(const float *v, size_t n, uint32_t *idx, const float *table,
+                               size_t d, float *x_out, hipStream_t s) {
+    return launch_argmax_split(v, n, idx, table, d, x_out, s);
 }
 
 }  // namespace mri

@@ -201,10 +201,10 @@ mri_status proj(const mri_weight_ref &w, const float *in, size_t rows, float *ou
     }
 }
 
-// One decode row through the single-row GEMV with the RMSNorm of its input
-// (norm != 0) in the prologue and, with accum, the residual add of its
-// output in the epilogue (out += projection).  row_proj_ok: the GEMV takes
-// the weight.
+// One decode row through the single-row GEMV, with the steps around the
+// projection that it takes over (RowOps): the RMSNorm or SwiGLU that
+// produces its input, a copy of the input row, and the residual add of its
+// output.  row_proj_ok: the GEMV takes the weight.
 bool row_proj_ok(const mri_weight_ref &w) {
     if (w.k_in == 0 || w.k_in % 4 || w.n_out == 0) return false;
     switch (w.format) {
@@ -225,21 +225,21 @@ bool row_proj_ok(const mri_weight_ref &w) {
     }
 }
 
-mri_status row_proj(const mri_weight_ref &w, const float *in, const float *norm, float eps,
-                    bool accum, float *out, hipStream_t s) {
+mri_status row_proj(const mri_weight_ref &w, const float *in, const RowOps &ops, float *out,
+                    hipStream_t s) {
     switch (w.format) {
     case MRI_WEIGHT_INT8:
         return launch_gemv_int8(in, nullptr, 1, nullptr, 0, 0.0f,
                                 handle_dev(static_cast<const mri_qmatrix *>(w.ptr)), out,
-                                nullptr, nullptr, nullptr, s, norm, eps, accum);
+                                nullptr, nullptr, nullptr, s, ops);
     case MRI_WEIGHT_Q8_0:
         return launch_gemv_q8_0(in, nullptr, 1, nullptr,
                                 handle_dev(static_cast<const mri_q8_0_matrix *>(w.ptr)), out,
-                                nullptr, nullptr, s, norm, eps, accum);
+                                nullptr, nullptr, s, ops);
     case MRI_WEIGHT_Q4_0_W4A8:
         return launch_gemv_q8_0(in, nullptr, 1, nullptr,
                                 handle_dev(static_cast<const mri_q4_0_matrix *>(w.ptr)), out,
-                                nullptr, nullptr, s, norm, eps, accum);
+                                nullptr, nullptr, s, ops);
     default:
         return set_error(MRI_ERR_INVALID_ARGUMENT, "row projection: unsupported format");
     }
@@ -267,21 +267,35 @@ bool row_path(mri_llama *m) {
 // attention RMSNorm; on exit m->normed holds the RMSNorm of the output with
 // next_norm (the next block's attention norm, or the output norm), each
 // residual add fused with the RMSNorm that follows it.  Decode row (fold):
-// each RMSNorm runs in the prologue of the projection that reads it and each
-// residual add in the epilogue of the projection that feeds it (row_proj).
-// Either way the values are those of the separate steps.
+// each RMSNorm runs in the prologue of the projection that reads it and
+// each residual add in the epilogue of the projection that feeds it
+// (row_proj); x_in is the block's input row (m->x, or the embedding row of
+// the first block, which the first projection copies into m->x).  Either
+// way the values are those of the separate steps.
 mri_status block(mri_llama *m, size_t li, size_t rows, size_t start, mri_kv_cache *c,
-                 const float *next_norm, bool fold, hipStream_t s) {
+                 const float *next_norm, bool fold, const float *x_in, hipStream_t s) {
     const mri_llama_config &g = m->cfg;
     const Layer &L = m->layers[li];
-    // projections of a normalized row (fold: normalized in the GEMV)
+    // projections of a normalized row (fold: normalized in the GEMV from
+    // xrow, the attention input and then the residual stream)
+    const float *xrow = x_in;
+    bool copy_x = fold && x_in != m->x;
     auto in_proj = [&](const mri_weight_ref &w, const float *norm, float *out) {
-        return fold ? row_proj(w, m->x, norm, g.eps, false, out, s)
-                    : proj(w, m->normed, rows, out, s);
+        if (!fold) return proj(w, m->normed, rows, out, s);
+        RowOps o;
+        o.norm_w = norm;
+        o.eps = g.eps;
+        if (copy_x) o.x_out = m->x;
+        copy_x = false;
+        return row_proj(w, xrow, o, out, s);
     };
     // projections whose output is added to the residual stream
     auto out_proj = [&](const mri_weight_ref &w, const float *in, const float *norm) {
-        if (fold) return row_proj(w, in, nullptr, 0.0f, true, m->x, s);
+        if (fold) {
+            RowOps o;
+            o.accum = true;
+            return row_proj(w, in, o, m->x, s);
+        }
         TRY(proj(w, in, rows, m->tmp, s));
         return launch_add_rmsnorm(m->x, m->tmp, rows, g.dim, norm, g.eps, m->normed, s);
     };
@@ -309,6 +323,7 @@ mri_status block(mri_llama *m, size_t li, size_t rows, size_t start, mri_kv_cach
     TRY(launch_attention(q, qs, rows, kc, vc, g.n_heads, g.n_kv_heads, m->hd, start, m->attn,
                          m->attn_part, s));
     TRY(out_proj(L.w[3], m->attn, L.ffn_norm));
+    xrow = m->x;
     float *act;
     if (L.gu.ptr) {
         TRY(in_proj(L.gu, L.ffn_norm, m->gu));
@@ -326,18 +341,31 @@ mri_status block(mri_llama *m, size_t li, size_t rows, size_t start, mri_kv_cach
 
 // embed -> blocks -> rmsnorm -> output projection for `rows` token ids
 // already on the device.
+// Where a single folded row's embedding comes from: gathered from the ids
+// on the device (kDevice), read in place at an id the host knows (kHost),
+// or already in m->x (kInX, written by the previous step's argmax).
+enum class Emb { kDevice, kHost, kInX };
+
 mri_status run_rows(mri_llama *m, const uint32_t *tok_dev, size_t rows, size_t start,
-                    mri_kv_cache *c, float *logits, hipStream_t s) {
+                    mri_kv_cache *c, float *logits, hipStream_t s, Emb emb = Emb::kDevice,
+                    uint32_t host_tok = 0) {
     const mri_llama_config &g = m->cfg;
     const bool fold = rows == 1 && row_path(m);
     const float *first = g.n_layers ? m->layers[0].attn_norm : m->out_norm;
-    if (fold) TRY(launch_embed(m->embd, tok_dev, 1, g.dim, m->x, s));
+    const float *x_in = m->x;
+    if (fold && emb == Emb::kHost) x_in = m->embd + (size_t)host_tok * g.dim;
+    else if (fold && emb == Emb::kInX) {}
+    else if (fold) TRY(launch_embed(m->embd, tok_dev, 1, g.dim, m->x, s));
     else TRY(launch_embed_rmsnorm(m->embd, tok_dev, rows, g.dim, first, g.eps, m->x, m->normed, s));
     for (size_t li = 0; li < g.n_layers; ++li)
         TRY(block(m, li, rows, start, c,
-                  li + 1 < g.n_layers ? m->layers[li + 1].attn_norm : m->out_norm, fold, s));
-    return fold ? row_proj(m->output, m->x, m->out_norm, g.eps, false, logits, s)
-                : proj(m->output, m->normed, rows, logits, s);
+                  li + 1 < g.n_layers ? m->layers[li + 1].attn_norm : m->out_norm, fold,
+                  li == 0 ? x_in : m->x, s));
+    if (!fold) return proj(m->output, m->normed, rows, logits, s);
+    RowOps o;
+    o.norm_w = m->out_norm;
+    o.eps = g.eps;
+    return row_proj(m->output, g.n_layers ? m->x : x_in, o, logits, s);
 }
 
 mri_status check_run(mri_llama *m, size_t n, size_t start, mri_kv_cache *c) {
@@ -506,6 +534,8 @@ mri_status mri_llama_forward_cached(mri_llama *m, const uint32_t *tokens, size_t
     TRY(check_tokens(m, tokens, n));
     if (!logits) return set_error(MRI_ERR_INVALID_ARGUMENT, "null logits");
     auto s = static_cast<hipStream_t>(stream);
+    if (n == 1 && row_path(m))
+        return run_rows(m, nullptr, 1, start_pos, c, logits, s, Emb::kHost, tokens[0]);
     MRI_HIP(hipMemcpyAsync(m->tok, tokens, n * sizeof(uint32_t), hipMemcpyHostToDevice, s));
     return run_rows(m, m->tok, n, start_pos, c, logits, s);
 }
@@ -542,11 +572,18 @@ mri_status mri_llama_generate_greedy(mri_llama *m, const uint32_t *prompt, size_
     const float *last = m->logits_buf + (n_prompt - 1) * V;
     if (logits_out)
         MRI_HIP(hipMemcpyAsync(logits_out, last, V * sizeof(float), hipMemcpyDeviceToDevice, s));
-    TRY(launch_argmax(last, 1, V, m->gen, s));
+    // folded decode rows: each argmax also gathers the chosen token's
+    // embedding row into m->x for the next step
+    const bool fold = row_path(m);
+    auto pick = [&](const float *lg, uint32_t *id, bool next) {
+        return fold && next ? launch_argmax_embed(lg, V, id, m->embd, m->cfg.dim, m->x, s)
+                            : launch_argmax(lg, 1, V, id, s);
+    };
+    TRY(pick(last, m->gen, n_steps > 0));
     for (size_t i = 0; i < n_steps; ++i) {
         float *lg = logits_out ? logits_out + (i + 1) * V : m->logits_buf;
-        TRY(run_rows(m, m->gen + i, 1, n_prompt + i, c, lg, s));
-        TRY(launch_argmax(lg, 1, V, m->gen + i + 1, s));
+        TRY(run_rows(m, m->gen + i, 1, n_prompt + i, c, lg, s, Emb::kInX));
+        TRY(pick(lg, m->gen + i + 1, i + 1 < n_steps));
     }
     MRI_HIP(hipMemcpyAsync(tokens_out, m->gen, (n_steps + 1) * sizeof(uint32_t),
                            hipMemcpyDeviceToHost, s));

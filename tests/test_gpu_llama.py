@@ -209,3 +209,30 @@ def test_llama_errors():
     with pytest.raises(Q.MriError) as e:
         gpu.forward_cached([1], 0, other, lg)
     assert e.value.kind == "ShapeMismatch"
+
+
+@pytest.mark.parametrize("n", [1, 5, 513, 32000, 70001])
+def test_argmax_one_row(n):
+    """One row runs the split kernel (its blocks meet through a counter that
+    every call leaves at zero): the oracle's choice on random values, ties
+    (the last wins), -0.0 against +0.0 (equal, so the last wins), NaN away
+    from element 0 (never chosen; the reference panics on NaN) and an
+    all-NaN row (0), over consecutive calls."""
+    t = torch()
+    L, _ = mods()
+    rng = np.random.default_rng(n)
+    idx = empty((1,), t.int32)
+    for trial in range(5):
+        v = rng.standard_normal(n).astype(F32)
+        if trial == 1 and n > 2:
+            v[[0, n // 2, n - 1]] = 9.0
+        elif trial == 2:
+            v[:] = -0.0
+            v[rng.integers(0, n, max(1, n // 4))] = 0.0
+        elif trial == 3 and n > 1:
+            v[1 + rng.integers(0, n - 1, max(1, n // 3))] = np.nan
+        elif trial == 4:
+            v[:] = np.nan
+        L.argmax(dev(v), idx)
+        got = int(host(idx).view(np.uint32)[0])
+        assert got == O.argmax(v), f"trial {trial}"
