@@ -99,11 +99,31 @@ struct ActIn {
     float eps = 0.0f;
     float *x_out = nullptr;         // optional [K], 16-byte aligned (fused path)
     int accum = 0;
+    const float *rope_cos = nullptr, *rope_sin = nullptr;
+    int rope_n = 0, hd = 2, seg1 = INT_MAX, seg2 = INT_MAX;
+    float *out1 = nullptr, *out2 = nullptr;
 
     ActIn(const float *x_, const int8_t *act_, int k, int8_t *aq, float *so, const RowOps &o)
         : x(x_), act(act_), K(k), act_q_out(aq), scale_out(so), norm_w(o.norm_w), eps(o.eps),
-          x_out(o.x_out), accum(o.accum ? 1 : 0) {}
+          x_out(o.x_out), accum(o.accum ? 1 : 0), rope_cos(o.rope_cos), rope_sin(o.rope_sin),
+          rope_n(o.rope_n), hd(o.hd), seg1(o.seg1), seg2(o.seg2), out1(o.out1), out2(o.out2) {}
 };
+
+// Epilogue of the row operations for output channel n of the row with value
+// v, where pv is the value of channel n ^ 1: RoPE below rope_n, as
+// rope_apply computes it (out[2i] = x0*c - x1*s, out[2i+1] = x1*c + x0*s),
+// then the store by output segment, or the residual accumulate.
+__device__ inline void row_store(const ActIn &in, float *out, int n, float v, float pv) {
+    if (n < in.rope_n) {
+        const int i = (n % in.hd) >> 1;
+        const float a = v * in.rope_cos[i], b = pv * in.rope_sin[i];
+        v = (n & 1) ? a + b : a - b;
+    }
+    float *o = n >= in.seg2 ? in.out2 + (n - in.seg2)
+             : n >= in.seg1 ? in.out1 + (n - in.seg1)
+                            : out + n;
+    *o = in.accum ? *o + v : v;
+}
 
 // Each thread stages XR 16-byte pieces of the activations in registers:
 // piece e of thread t is element t + S*64*e (index clamped, use guarded).

@@ -57,6 +57,8 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_int8(
     if constexpr (FUSED && OPS) {
         if (in.norm_w) stage_load<NW, XR>(reinterpret_cast<const v4i *>(in.norm_w), n16, wn);
     }
+    // activation loads before the ring's (they return first; see gemv_q8.hip)
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int s = 0; s < D; ++s)
         wr[s] = __builtin_nontemporal_load(wp + (size_t)min(c0 + s, last) * pitch);
@@ -104,7 +106,17 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_int8(
     }
 
     const int n = T * 16 + r;
-    if (!tile_ok || n >= N || g != 0) return;
+    if (!tile_ok) return;
+    if constexpr (OPS) {  // one row: lanes 0-15 hold channels 16T .. 16T+15
+        float v = (float)acc[0] * sa_value;
+        v = v * wscales[min(n, N - 1)];
+        const float pv = __shfl_xor(v, 1);
+        if (g != 0 || n >= N) return;
+        if (acc_out) acc_out[n] = acc[0];
+        row_store(in, out, n, v, pv);
+        return;
+    }
+    if (n >= N || g != 0) return;
     const float sw = wscales[n];
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
@@ -112,8 +124,7 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_int8(
             const float sa = sa_ptr ? sa_ptr[(size_t)i * sa_stride] : sa_value;
             float v = (float)acc[i] * sa;
             v = v * sw;
-            float *o = out + (size_t)i * N + n;
-            *o = OPS && in.accum ? *o + v : v;
+            out[(size_t)i * N + n] = v;
             if (acc_out) acc_out[(size_t)i * N + n] = acc[i];
         }
     }
@@ -181,7 +192,11 @@ bool gemv_int8_supported(bool fused, size_t m, size_t n_tiles, size_t k, size_t 
 bool row_ops_ok(const float *x, const RowOps &o) {
     auto al = [](const float *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
     if (!o.any()) return true;
-    return x && al(o.norm_w) && al(o.x_out);
+    const bool rope = o.rope_n == 0 || (o.rope_cos && o.rope_sin && o.hd >= 2 && o.hd % 2 == 0 &&
+                                        o.rope_n % 2 == 0);
+    const bool segs = (o.seg1 == INT_MAX || o.out1) && (o.seg2 == INT_MAX || o.out2) &&
+                      o.seg1 <= o.seg2 && o.seg1 >= 0;
+    return x && al(o.norm_w) && al(o.x_out) && rope && segs;
 }
 
 bool gemv_fusable(size_t m, size_t k, const float *x) {

@@ -110,7 +110,11 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     // prime the ring in the steady state's issue order (a lap's quants, then
     // its scales), lap indices clamped to the tile.  The activation loads
     // were issued first, so they return first, and the prologue below waits
-    // for them alone while the ring's loads stay in flight.
+    // for them alone while the ring's loads stay in flight.  The scheduling
+    // barrier keeps the compiler from moving activation loads after the
+    // ring's (it did with 12 pieces per thread, and the prologue then waited
+    // for weight loads).
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < RL; ++u) {
         const int q = min(min(u, max(nq - 1, 0)) * S + w, G - 1);
@@ -255,14 +259,17 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     // rounds in which this wave has no lap (the barrier count is uniform)
     for (int R = nq; R < NR; ++R) round_end(R);
 
-    if (w != 0 || !tile_ok || g >= LG || n >= N) return;
+    if (w != 0 || !tile_ok) return;
+    if constexpr (OPS) {  // one row: lanes 0-15 hold channels 16T .. 16T+15
+        const float pv = __shfl_xor(fs[0], 1);
+        if (g == 0 && n < N) row_store(in, out, n, fs[0], pv);
+        return;
+    }
+    if (g >= LG || n >= N) return;
 #pragma unroll
     for (int j = 0; j < LR; ++j) {
         const int row = 2 * g + j;
-        if (row < M) {
-            float *o = out + (size_t)row * N + n;
-            *o = OPS && in.accum ? *o + fs[j] : fs[j];
-        }
+        if (row < M) out[(size_t)row * N + n] = fs[j];
     }
 }
 

@@ -280,14 +280,17 @@ mri_status block(mri_llama *m, size_t li, size_t rows, size_t start, mri_kv_cach
     // xrow, the attention input and then the residual stream)
     const float *xrow = x_in;
     bool copy_x = fold && x_in != m->x;
-    auto in_proj = [&](const mri_weight_ref &w, const float *norm, float *out) {
-        if (!fold) return proj(w, m->normed, rows, out, s);
+    auto norm_ops = [&](const float *norm) {
         RowOps o;
         o.norm_w = norm;
         o.eps = g.eps;
         if (copy_x) o.x_out = m->x;
         copy_x = false;
-        return row_proj(w, xrow, o, out, s);
+        return o;
+    };
+    auto in_proj = [&](const mri_weight_ref &w, const float *norm, float *out) {
+        if (!fold) return proj(w, m->normed, rows, out, s);
+        return row_proj(w, xrow, norm_ops(norm), out, s);
     };
     // projections whose output is added to the residual stream
     auto out_proj = [&](const mri_weight_ref &w, const float *in, const float *norm) {
@@ -302,7 +305,37 @@ mri_status block(mri_llama *m, size_t li, size_t rows, size_t start, mri_kv_cach
     float *kc = c->k + li * c->max_seq * c->kvd, *vc = c->v + li * c->max_seq * c->kvd;
     float *q, *k, *v;
     size_t qs, kvs;
-    if (L.qkv.ptr) {
+    if (fold) {
+        // q/k/v of one row with RoPE and the KV-cache writes in the GEMV
+        // epilogue (what k_rope_qkv does for rows)
+        if (m->hd % 2 || m->hd > 128)
+            return set_error(MRI_ERR_UNSUPPORTED, "rope: head_dim must be even and <= 128");
+        const size_t half = m->hd / 2;
+        float *krow = kc + start * c->kvd, *vrow = vc + start * c->kvd;
+        RowOps o = norm_ops(L.attn_norm);
+        o.rope_cos = m->cos_t + start * half;
+        o.rope_sin = m->sin_t + start * half;
+        o.hd = (int)m->hd;
+        q = m->qkv;
+        qs = m->qd;
+        if (L.qkv.ptr) {
+            o.rope_n = (int)(m->qd + m->kvd);
+            o.seg1 = (int)m->qd;
+            o.out1 = krow;
+            o.seg2 = (int)(m->qd + m->kvd);
+            o.out2 = vrow;
+            TRY(row_proj(L.qkv, xrow, o, q, s));
+        } else {
+            RowOps ok = o, ov = o;
+            ok.x_out = ov.x_out = nullptr;  // copied by the first
+            o.rope_n = (int)m->qd;
+            TRY(row_proj(L.w[0], xrow, o, q, s));
+            ok.rope_n = (int)m->kvd;
+            TRY(row_proj(L.w[1], xrow, ok, krow, s));
+            ov.rope_n = 0;
+            TRY(row_proj(L.w[2], xrow, ov, vrow, s));
+        }
+    } else if (L.qkv.ptr) {
         TRY(in_proj(L.qkv, L.attn_norm, m->qkv));
         q = m->qkv;
         k = q + m->qd;
@@ -318,8 +351,9 @@ mri_status block(mri_llama *m, size_t li, size_t rows, size_t start, mri_kv_cach
         TRY(in_proj(L.w[1], L.attn_norm, k));
         TRY(in_proj(L.w[2], L.attn_norm, v));
     }
-    TRY(launch_rope_qkv(q, k, v, rows, g.n_heads, g.n_kv_heads, m->hd, qs, kvs, m->cos_t,
-                        m->sin_t, start, kc, vc, s));
+    if (!fold)
+        TRY(launch_rope_qkv(q, k, v, rows, g.n_heads, g.n_kv_heads, m->hd, qs, kvs, m->cos_t,
+                            m->sin_t, start, kc, vc, s));
     TRY(launch_attention(q, qs, rows, kc, vc, g.n_heads, g.n_kv_heads, m->hd, start, m->attn,
                          m->attn_part, s));
     TRY(out_proj(L.w[3], m->attn, L.ffn_norm));

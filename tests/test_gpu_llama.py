@@ -34,15 +34,25 @@ def mods():
     return L, Q
 
 
+MIXED = {"wq": "int8", "wk": "q8_0", "wv": "w4a8", "wo": "q8_0", "wgate": "w4a8", "wup": "int8",
+         "wdown": "int8", "out": "q8_0"}
+
+
 def build(fmt, seed=0, d=256, nh=4, nkv=2, ffn=512, vocab=300, max_seq=48, n_layers=2):
-    """The same random model on both sides."""
+    """The same random model on both sides (fmt "mixed": a different format
+    per projection role, MIXED)."""
     L, Q = mods()
     rng = np.random.default_rng(seed)
     hd = d // nh
     cfg = dict(dim=d, n_heads=nh, n_kv_heads=nkv, head_dim=hd, ffn=ffn, vocab=vocab,
                max_seq=max_seq, eps=1e-6, rope_base=10000.0)
 
-    def proj(n, k):
+    def proj(n, k, role="out"):
+        if fmt == "mixed":
+            return proj_fmt(MIXED[role], n, k)
+        return proj_fmt(fmt, n, k)
+
+    def proj_fmt(fmt, n, k):
         w = (rng.standard_normal((n, k)) * 0.05).astype(F32)
         if fmt == "int8":
             data, scales = O.quantize_per_channel(w, n, k)
@@ -63,7 +73,7 @@ def build(fmt, seed=0, d=256, nh=4, nkv=2, ffn=512, vocab=300, max_seq=48, n_lay
         for name, (n, k) in (("wq", (nh * hd, d)), ("wk", (nkv * hd, d)), ("wv", (nkv * hd, d)),
                              ("wo", (d, nh * hd)), ("wgate", (ffn, d)), ("wup", (ffn, d)),
                              ("wdown", (d, ffn))):
-            ol[name], gl[name] = proj(n, k)
+            ol[name], gl[name] = proj(n, k, name)
         o_layers.append(ol)
         g_layers.append(gl)
     embd = rng.standard_normal((vocab, d)).astype(F32)
@@ -80,7 +90,7 @@ def close(got, ref, frac):
     assert err <= frac * scale, f"max |gpu - ref| = {err:.3g} > {frac} * {scale:.3g}"
 
 
-TOL = {"q4_0": 1e-4, "q8_0": 2e-2, "int8": 2e-2, "w4a8": 2e-2}
+TOL = {"q4_0": 1e-4, "q8_0": 2e-2, "int8": 2e-2, "w4a8": 2e-2, "mixed": 2e-2}
 
 
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0", "int8", "w4a8"])
@@ -99,6 +109,25 @@ def test_llama_prefill_and_decode_logits(fmt):
     for p in range(20, 24):
         gpu.forward_decode(toks[p], p, cache, one)
         close(host(one), oracle.forward_decode(toks[p], p), TOL[fmt])
+
+
+def test_llama_mixed_formats():
+    """A different weight format per projection role: q/k/v and gate/up
+    cannot be concatenated, so decode rows run three q/k/v projections, each
+    with the RMSNorm prologue and its own RoPE / cache epilogue."""
+    t = torch()
+    oracle, gpu, rng = build("mixed", seed=23)
+    toks = rng.integers(0, 300, 18).tolist()
+    cache = gpu.kv_cache()
+    lg = empty((14, 300), t.float32)
+    gpu.forward_cached(toks[:14], 0, cache, lg)
+    close(host(lg), oracle.forward_cached(toks[:14], 0), 2e-2)
+    one = empty((300,), t.float32)
+    for p in range(14, 18):
+        gpu.forward_decode(toks[p], p, cache, one)
+        close(host(one), oracle.forward_decode(toks[p], p), 2e-2)
+    toks2 = gpu.generate_greedy(toks[:10], 4, gpu.kv_cache())
+    assert toks2.shape == (5,)
 
 
 def test_llama_gqa_and_mha_head_dim_128():
