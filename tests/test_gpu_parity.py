@@ -231,7 +231,7 @@ Q8_SHAPES = [
     (1, 16400, 8192), (1, 4096, 11008), (3, 2000, 4096), (1, 32000, 4096),
     (4, 48, 4096), (8, 16, 512), (16, 40, 1024), (17, 20, 64), (32, 64, 4096),
     (40, 24, 128), (33, 48, 256), (64, 80, 1024), (100, 37, 4096), (512, 96, 512),
-    (300, 4096, 256),
+    (300, 4096, 256), (2, 4096, 11008), (3, 11008, 4096), (4, 11008, 4096), (4, 64, 2048),
 ]
 
 
