@@ -265,3 +265,28 @@ def test_argmax_one_row(n):
         L.argmax(dev(v), idx)
         got = int(host(idx).view(np.uint32)[0])
         assert got == O.argmax(v), f"trial {trial}"
+
+
+@pytest.mark.parametrize("fmt", ["q8_0", "int8"])
+def test_llama_zero_layers(fmt):
+    """No decoder layers: the output projection reads the embedding row
+    (decode rows: in place, with the output RMSNorm in its prologue; the
+    greedy loop: the row its argmax gathered)."""
+    t = torch()
+    oracle, gpu, rng = build(fmt, seed=29, n_layers=0)
+    toks = rng.integers(0, 300, 8).tolist()
+    cache = gpu.kv_cache()
+    lg = empty((5, 300), t.float32)
+    gpu.forward_cached(toks[:5], 0, cache, lg)
+    close(host(lg), oracle.forward_cached(toks[:5], 0), 2e-2)
+    one = empty((300,), t.float32)
+    for p in range(5, 8):
+        gpu.forward_decode(toks[p], p, cache, one)
+        close(host(one), oracle.forward_decode(toks[p], p), 2e-2)
+    steps = 4
+    glg = empty((steps + 1, 300), t.float32)
+    got = gpu.generate_greedy(toks[:5], steps, gpu.kv_cache(), glg)
+    ref = [oracle.forward_cached(toks[:5], 0)[-1]]
+    for i in range(steps):
+        ref.append(oracle.forward_decode(int(got[i]), 5 + i))
+    close(host(glg), np.stack(ref), 2e-2)
