@@ -321,7 +321,7 @@ def bench_layer(torch, M, fmt, n_prompt=512, n_steps=128, seed=21):
         t0 = time.perf_counter()
         toks = model.generate_greedy(prompt, n_steps, cache)
         gen.append((time.perf_counter() - t0) * 1e3)
-    assert int(toks.max()) < v
+    check = layer_check(torch, model, prompt, n_steps, v)
     pre_ms, gen_ms = min(pre), min(gen)
     dec_us = (gen_ms - pre_ms) / n_steps * 1e3
     nbytes = layer_decode_bytes(fmt, n_prompt + n_steps // 2)
@@ -334,7 +334,31 @@ def bench_layer(torch, M, fmt, n_prompt=512, n_steps=128, seed=21):
             "generate_512_plus_128_ms": round(gen_ms, 3),
             "decode_bytes_per_token": nbytes,
             "decode_GB_s": round(gbs, 1), "decode_frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
-            "first_tokens": [int(t) for t in toks[:4]]}
+            "first_tokens": [int(t) for t in toks[:4]], "check": check}
+
+
+def layer_check(torch, model, prompt, n_steps, v):
+    """Checks of the timed run at full size, before its figures count:
+    every greedy token is the argmax (last of equal maxima) of its own
+    logits row, and the logits of the first decode step (the first chosen
+    token at position len(prompt)) equal row len(prompt) of one prefill over
+    the prompt and that token, within 1e-1 of the largest logit magnitude (a
+    wrong position, head or cache row moves them by O(1); activation
+    quantization moves them by a few percent at most)."""
+    import numpy as np
+    n = len(prompt)
+    lg = torch.empty((n_steps + 1, v), device="cuda")
+    toks = model.generate_greedy(prompt, n_steps, model.kv_cache(), lg)
+    g = lg.cpu().numpy()
+    for i in range(n_steps + 1):
+        r = g[i]
+        assert toks[i] == v - 1 - int(np.argmax(r[::-1])), f"step {i}: not the argmax"
+    full = torch.empty((n + 1, v), device="cuda")
+    model.forward_cached(list(prompt) + [int(toks[0])], 0, model.kv_cache(), full)
+    f = full[n].cpu().numpy()
+    rel = float(np.abs(g[1] - f).max() / np.abs(f).max())
+    assert rel <= 1e-1, f"first decode step vs prefill row: {rel}"
+    return {"greedy_tokens_are_argmax": True, "first_decode_vs_prefill_row_rel": round(rel, 5)}
 
 
 def cpu_q8_direct(raw_np, x_np, n, k, budget_s):

@@ -78,6 +78,19 @@ struct Scratch {
     void *ptr = nullptr;
     size_t bytes = 0;
 };
+int device_cus() {
+    static std::atomic<int> cus[kMaxDevices] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+    int n = cus[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return 0;
+        cus[dev].store(n, std::memory_order_relaxed);  // every thread stores the same value
+    }
+    return n;
+}
+
 static std::mutex g_scratch_mu;
 static std::map<std::pair<int, hipStream_t>, Scratch> g_scratch;
 

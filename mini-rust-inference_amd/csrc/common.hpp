@@ -55,9 +55,11 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <climits>
 #include <cstddef>
 #include <cstdint>
+#include <mutex>
 #include <string>
 
 #include "mri_qmatmul.h"
@@ -127,6 +129,35 @@ mri_status hip_error(hipError_t e, const char *what);
         hipError_t _e = hipGetLastError();                          \
         if (_e != hipSuccess) return ::mri::hip_error(_e, what);    \
     } while (0)
+
+// ---- one-time per-device set-up --------------------------------------------
+// A call site's static DeviceOnce runs its set-up (hipFuncSetAttribute, a
+// device query) once per device; concurrent first calls wait for the one
+// that runs it, later calls cost one acquire load.
+constexpr int kMaxDevices = 64;
+class DeviceOnce {
+  public:
+    template <class F>
+    hipError_t run(F &&setup) {
+        int dev = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e != hipSuccess) return e;
+        if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+        if (done_[dev].load(std::memory_order_acquire)) return hipSuccess;
+        std::lock_guard<std::mutex> g(mu_);
+        if (done_[dev].load(std::memory_order_relaxed)) return hipSuccess;
+        e = setup(dev);
+        if (e == hipSuccess) done_[dev].store(true, std::memory_order_release);
+        return e;
+    }
+
+  private:
+    std::atomic<bool> done_[kMaxDevices] = {};
+    std::mutex mu_;
+};
+
+// Number of CUs of the current device (queried once per device), or 0.
+int device_cus();
 
 // ---- per-(device, stream) scratch ----------------------------------------
 // Grow-only device buffer; growth synchronizes `stream` before freeing the

@@ -569,9 +569,9 @@ __device__ inline bool arg_better(float ov, int oi, float bv, int bi) {
 // counter at word 0, candidate values at words 4.., indices at 68...
 // The candidates are stored and loaded with device-scope (sc1) accesses,
 // which reach the point of coherence of all XCDs, and each block waits for
-// its stores to complete before it counts, so no cache-wide fence is needed.
-// The counter is updated at system scope, which performs the atomic past
-// every XCD's L2.
+// its stores to complete before it counts.  The count is an acquire-release
+// read-modify-write at system scope (performed past every XCD's L2), so the
+// candidates happen-before the last block's reads in the memory model too.
 constexpr int kArgSplit = 64;
 __global__ __launch_bounds__(256) void k_argmax_split(const float *__restrict__ v, int n,
                                                       uint32_t *__restrict__ idx,
@@ -628,7 +628,9 @@ __global__ __launch_bounds__(256) void k_argmax_split(const float *__restrict__ 
                            __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(&part_i[blockIdx.x], bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the candidate has reached the device
-        s_last = __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) ==
+        // release: publishes this block's candidate; acquire: the last block
+        // reads every candidate after it
+        s_last = __hip_atomic_fetch_add(count, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_SYSTEM) ==
                  gridDim.x - 1;
     }
     __syncthreads();
@@ -676,12 +678,11 @@ mri_status attn_launch(const float *q, int qs, int qd, const float *kc, const fl
     const int L = start_pos + seq_q;
     const int lcap = (L + 3) / 4 * 4;
     const size_t lds = attn_lds<HD, QB>(lcap);
-    static bool attr_set = false;
-    if (!attr_set) {
-        MRI_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_attention<HD, QB>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-        attr_set = true;
-    }
+    static DeviceOnce attr;
+    MRI_HIP(attr.run([](int) {
+        return hipFuncSetAttribute(reinterpret_cast<const void *>(&k_attention<HD, QB>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    }));
     const float scale = 1.0f / sqrtf((float)HD);
     hipLaunchKernelGGL((k_attention<HD, QB>), dim3((seq_q + QB - 1) / QB, n_heads), dim3(256),
                        lds, s, q, qs, qd, kc, vc, kvd, seq_q, start_pos, groups, lcap, scale, out);

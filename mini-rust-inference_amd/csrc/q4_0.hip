@@ -233,12 +233,11 @@ size_t q4_lds_bytes(int r, size_t k) { return (size_t)r * (k / 32) * kQ4Bytes; }
 template <int R, bool GG>
 mri_status launch_lds(const float *x, size_t m, size_t k, const uint8_t *w, size_t n_out,
                       float *out, hipStream_t s) {
-    static bool attr_set = false;
-    if (!attr_set) {
-        MRI_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_q4_0_lds<R, GG>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-        attr_set = true;
-    }
+    static DeviceOnce attr;
+    MRI_HIP(attr.run([](int) {
+        return hipFuncSetAttribute(reinterpret_cast<const void *>(&k_q4_0_lds<R, GG>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    }));
     hipLaunchKernelGGL((k_q4_0_lds<R, GG>), dim3((unsigned)((n_out + R - 1) / R)),
                        dim3(kThreads), q4_lds_bytes(R, k), s, x, (int)m, (int)k, w, (int)n_out,
                        out);

@@ -139,7 +139,8 @@ def test_matmul_int8_bit_exact(m, n, k):
 
 @pytest.mark.parametrize("m,n,k", [(512, 11008, 4096), (300, 200, 1024), (2048, 512, 4096),
                                    (64, 4096, 11008), (128, 4096, 4096), (512, 4096, 11008),
-                                   (2048, 8192, 4096)])
+                                   (2048, 8192, 4096), (128, 11008, 4096), (512, 4096, 4096),
+                                   (2048, 4096, 4096), (2048, 11008, 4096)])
 def test_matmul_int8_prefill_closed_form(m, n, k):
     """Prefill-sized matmul_int8 (int8.rs:61-98) at full shapes: the int32
     accumulators against an exact float64 matmul (|sum| <= 127^2 * K < 2^53)
@@ -232,6 +233,9 @@ Q8_SHAPES = [
     (4, 48, 4096), (8, 16, 512), (16, 40, 1024), (17, 20, 64), (32, 64, 4096),
     (40, 24, 128), (33, 48, 256), (64, 80, 1024), (100, 37, 4096), (512, 96, 512),
     (300, 4096, 256), (2, 4096, 11008), (3, 11008, 4096), (4, 11008, 4096), (4, 64, 2048),
+    # the benchmarked decode shapes: [1,4096]x[4096,4096] and [4096,11008], and the
+    # batched decode rows M = 8, 16, 32 at N = 11008
+    (1, 11008, 4096), (1, 4096, 4096), (8, 11008, 4096), (16, 11008, 4096), (32, 11008, 4096),
 ]
 
 
