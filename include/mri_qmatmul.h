@@ -41,7 +41,7 @@ typedef enum mri_status {
     MRI_ERR_SHAPE_MISMATCH = 2,   /* TensorError::ShapeMismatch */
     MRI_ERR_INVALID_ARGUMENT = 3, /* null pointer / bad handle (no Rust analogue: borrowck) */
     MRI_ERR_HIP = 4,              /* HIP runtime error (allocation, launch) */
-    MRI_ERR_UNSUPPORTED = 5       /* device is not gfx950 */
+    MRI_ERR_UNSUPPORTED = 5       /* device is not gfx950, or a size beyond a fixed limit */
 } mri_status;
 
 /* Thread-local message for the last non-OK status on this thread
@@ -159,6 +159,22 @@ mri_status mri_matmul_q8_0_direct(const float *input, const size_t *dims,
                                   size_t ndim, const mri_q8_0_matrix *w,
                                   float *out, int32_t *block_dots_out,
                                   float *act_scales_out, void *stream);
+
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): mri_matmul_q8_0_direct with the same arguments, checks
+ * and results, but its quantized activation rows and scales (m * K' + 4 * m
+ * bytes, K' = k_in rounded up to 256, 0 at m = 1) are staged in a fixed
+ * device array of MRI_NOALLOC_SCRATCH_BYTES per device instead of the
+ * library's grow-on-demand scratch; it calls no hipMalloc / hipFree.  Larger
+ * inputs return MRI_ERR_UNSUPPORTED.  All calls on one device share that
+ * array: calls that overlap in time on one device (different streams or
+ * threads) race and must be serialized by the caller. */
+#define MRI_NOALLOC_SCRATCH_BYTES (4 << 20)
+mri_status mri_matmul_q8_0_direct_noalloc(const float *input, const size_t *dims,
+                                          size_t ndim, const mri_q8_0_matrix *w,
+                                          float *out, int32_t *block_dots_out,
+                                          float *act_scales_out, void *stream);
 
 /* matmul_q4_0_dequant, src/ops/matmul/q4_0.rs:94-181 (W4A32): weight_q4 is
  * a DEVICE pointer to raw Q4_0 blocks ([f16 d][16 bytes], 18 bytes, element

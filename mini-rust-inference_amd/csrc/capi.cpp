@@ -774,11 +774,30 @@ mri_status mri_matmul_int8_from_f32(const float *input, const size_t *dims, size
 
 }  // extern "C"
 
-// matmul_q8_0_direct's body, shared with the W4A8 entry point (d.w4).
+// Staging of the no-allocation entry point (quantized activation rows and
+// their scales): one copy per device, held until the process ends.  Host
+// code uses the address hipGetSymbolAddress gives for the current device,
+// never the array's own name.
+static __device__ __align__(256) uint8_t scratch[MRI_NOALLOC_SCRATCH_BYTES];
+
+static mri_status noalloc_scratch(void **ptr) {
+    static DeviceOnce once;
+    static void *addr[kMaxDevices] = {};
+    int dev = 0;
+    MRI_HIP(hipGetDevice(&dev));
+    MRI_HIP(once.run([](int d) {
+        return hipGetSymbolAddress(&addr[d], HIP_SYMBOL(scratch));
+    }));
+    *ptr = addr[dev];  // published by the once's release
+    return MRI_OK;
+}
+
+// matmul_q8_0_direct's body, shared with the W4A8 entry point (d.w4) and
+// the no-allocation variant (fixed: staging in the file's device array).
 static mri_status matmul_blocks(const char *name, const float *input, const size_t *dims,
                                 size_t ndim, const Q8MatrixDev &d, float *out,
                                 int32_t *block_dots_out, float *act_scales_out,
-                                void *stream) {
+                                void *stream, bool fixed = false) {
     if (ndim && !dims) return set_error(MRI_ERR_INVALID_ARGUMENT, "dims is null");
     if (ndim != 2)
         return set_error(MRI_ERR_INVALID_SHAPE,
@@ -804,7 +823,16 @@ static mri_status matmul_blocks(const char *name, const float *input, const size
     const size_t o_act = cv.take(m * d.kp);
     const size_t o_sc = cv.take(m * sizeof(float));
     void *base = nullptr;
-    st = scratch_get(s, cv.off, &base);
+    if (fixed) {
+        if (cv.off > MRI_NOALLOC_SCRATCH_BYTES)
+            return set_error(MRI_ERR_UNSUPPORTED,
+                             fmt("%s: %zu rows of K = %zu need %zu bytes of staging, more than "
+                                 "the %d of the no-allocation entry point",
+                                 name, m, k, cv.off, MRI_NOALLOC_SCRATCH_BYTES));
+        st = noalloc_scratch(&base);
+    } else {
+        st = scratch_get(s, cv.off, &base);
+    }
     if (st) return st;
     auto *b = static_cast<uint8_t *>(base);
     int8_t *act = reinterpret_cast<int8_t *>(b + o_act);
@@ -824,6 +852,15 @@ mri_status mri_matmul_q8_0_direct(const float *input, const size_t *dims, size_t
     if (!w) return set_error(MRI_ERR_INVALID_ARGUMENT, "null weight handle");
     return matmul_blocks("matmul_q8_0_direct", input, dims, ndim, w->d, out, block_dots_out,
                          act_scales_out, stream);
+}
+
+mri_status mri_matmul_q8_0_direct_noalloc(const float *input, const size_t *dims, size_t ndim,
+                                          const mri_q8_0_matrix *w, float *out,
+                                          int32_t *block_dots_out, float *act_scales_out,
+                                          void *stream) {
+    if (!w) return set_error(MRI_ERR_INVALID_ARGUMENT, "null weight handle");
+    return matmul_blocks("matmul_q8_0_direct_noalloc", input, dims, ndim, w->d, out,
+                         block_dots_out, act_scales_out, stream, true);
 }
 
 mri_status mri_matmul_q4_0_w4a8(const float *input, const size_t *dims, size_t ndim,

@@ -54,6 +54,7 @@ _SIGS = {
     "mri_matmul_int8_rows": ([P, SZ, P, P, SZ, P, P, P], ST),
     "mri_matmul_int8_from_f32": ([P, P, SZ, P, P, P, P, P, P], ST),
     "mri_matmul_q8_0_direct": ([P, P, SZ, P, P, P, P, P], ST),
+    "mri_matmul_q8_0_direct_noalloc": ([P, P, SZ, P, P, P, P, P], ST),
     "mri_matmul_q4_0_dequant": ([P, P, SZ, P, SZ, SZ, SZ, P, P], ST),
     "mri_q4_0_matrix_from_raw_bytes": ([P, SZ, SZ, SZ, C.c_int, C.POINTER(P)], ST),
     "mri_q4_0_matrix_from_raw_device": ([P, SZ, SZ, SZ, C.c_int, P, C.POINTER(P)], ST),
@@ -312,6 +313,20 @@ def matmul_q8_0_direct(x, w: Q8Matrix, out, block_dots_out=None, act_scales_out=
     check(lib().mri_matmul_q8_0_direct(_ptr(x), dims, nd, w.h, _ptr(out),
                                        _ptr(block_dots_out), _ptr(act_scales_out),
                                        _stream(stream)))
+
+
+def matmul_q8_0_direct_noalloc(x, w: Q8Matrix, out, block_dots_out=None, act_scales_out=None,
+                               stream=None, shape=None):
+    """matmul_q8_0_direct staged in the library's fixed per-device array
+    (NOALLOC_SCRATCH_BYTES): no device allocation; overlapping calls on one
+    device race."""
+    dims, nd = _dims(tuple(x.shape) if shape is None else shape)
+    check(lib().mri_matmul_q8_0_direct_noalloc(_ptr(x), dims, nd, w.h, _ptr(out),
+                                               _ptr(block_dots_out), _ptr(act_scales_out),
+                                               _stream(stream)))
+
+
+NOALLOC_SCRATCH_BYTES = 4 << 20  # MRI_NOALLOC_SCRATCH_BYTES
 
 
 def matmul_q4_0_w4a8(x, w: Q4Matrix, out, block_dots_out=None, act_scales_out=None,
