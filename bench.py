@@ -6,8 +6,9 @@ Headline workload (one "step" = one call of the hot path):
   synthetic data: quants ~U[-127, 127], f16 block scales ~U(0.001, 0.01),
   x ~ N(0, 1).  Enough device copies of the weights (>= 384 MB, more than
   the 256 MB Infinity Cache) are used in rotation so that the weight stream
-  comes from HBM.  The output of the first call is checked bit-for-bit
-  against the oracle before timing.
+  comes from HBM.  The first call is checked against the oracle before
+  timing: int32 block dots bit for bit, f32 outputs within
+  1e-5 * max(|ref|, sum_b |t_b|).
 
 value = algorithmic bytes per call / mean call time (GB/s), with
         algorithmic bytes = Q8_0 weight bytes (34 B per 32 weights)
@@ -192,10 +193,19 @@ def bench_q8(torch, M, T, m, n, k, steps, warmup, check=False, seed=1):
     if check:
         import numpy as np
         import oracle_lib as O
-        M.matmul_q8_0_direct(x, ws[0], out)
-        ref = O.matmul_q8_0_direct(x.cpu().numpy(), raw.cpu().numpy(), n, k)
-        if not np.array_equal(out.cpu().numpy().view(np.uint32), ref.view(np.uint32)):
-            raise SystemExit("bench: Q8_0 output differs from the oracle")
+        dots = torch.empty((m, n, k // 32), dtype=torch.int32, device="cuda")
+        M.matmul_q8_0_direct(x, ws[0], out, dots)
+        raw_np = raw.cpu().numpy()
+        ref, bd, sa = O.matmul_q8_0_direct(x.cpu().numpy(), raw_np, n, k, want_block_dots=True)
+        if not np.array_equal(dots.cpu().numpy(), bd):
+            raise SystemExit("bench: Q8_0 block dots differ from the oracle")
+        # f32 contract: |gpu - ref| <= 1e-5 * max(|ref|, sum_b |t_b|)
+        dsc = raw_np.reshape(n, k // 32, 34)[:, :, :2].copy().view(np.float16)[:, :, 0]
+        terms = np.einsum("mnb,nb->mn", np.abs(bd).astype(np.float64),
+                          np.abs(dsc.astype(np.float64))) * np.abs(sa.astype(np.float64))[:, None]
+        err = np.abs(out.cpu().numpy().astype(np.float64) - ref)
+        if not np.all(err <= 1e-5 * np.maximum(np.abs(ref), terms)):
+            raise SystemExit("bench: Q8_0 output outside the 1e-5 contract")
     call = lambda i: M.matmul_q8_0_direct(x, ws[i], out)  # noqa: E731
     bound = [M.bind_matmul_q8_0_direct(x, w, out) for w in ws]
     ms, ms_graph, ms_host = T.best_ms(call, steps, warmup, nrot, out, lambda i: bound[i]())

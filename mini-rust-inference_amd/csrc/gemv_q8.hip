@@ -23,13 +23,14 @@ namespace {
 // (4 chunks = 8 blocks) dealt out round-robin: in round R wave w takes lap
 // R*S + w, so each round covers S consecutive laps.  Per lap a wave runs
 // the MFMAs of its chunks (each followed by the refill of its ring slot
-// with the chunk RL laps ahead) and forms the eight terms
-// t_b = ((f32)dot_b * s_a) * d_b (q8_direct.rs:281).  Wave 0 adds its own
-// terms to the running sum at once; the other waves leave theirs in LDS.
-// Every round ends with an LDS-only barrier, after which wave 0 adds the
-// round's remaining S-1 laps in block order.  The f32 result is therefore
-// bit-identical to the sequential reference, and only the last round's
-// terms remain to be added after the sweep.
+// with the chunk RL laps ahead) and adds the eight terms
+// t_b = ((f32)dot_b * s_a) * d_b (q8_direct.rs:281) to its own running
+// f32 sum, in block order.  After the sweep the S wave sums of a tile are
+// added through LDS in wave order (one barrier), so the result is
+// deterministic; it differs from the reference's single left-to-right sum
+// only in f32 rounding, within 1e-5 * max(|out|, sum_b |t_b|).  The int32
+// block dots are exact.  (Keeping the reference's order needed an LDS
+// barrier per round and measured ~0.3 us slower at [1,4096]x[4096,11008].)
 //
 // W4: a lap's quants are two 16-byte loads per lane instead of four; the B
 // operand of a chunk is unpacked from two u32 words by moving each nibble
@@ -37,12 +38,6 @@ namespace {
 // nibble is the quant's 4-bit two's complement), so the MFMA's int32 result
 // is 16 times the block dot and an arithmetic shift by 4 recovers it.
 // ---------------------------------------------------------------------------
-
-// Barrier for LDS traffic only: waits for this wave's LDS operations, not
-// for its outstanding global loads (the ring stays in flight).
-__device__ inline void lds_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
 
 template <int MR, int S, int TPW, int RL, int XR, bool FUSED, bool OPS, bool DEBUG, bool W4>
 __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
@@ -52,7 +47,6 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     constexpr int NW = S * TPW;               // waves per workgroup
     constexpr int LR = MR == 1 ? 1 : 2;       // rows per result lane
     constexpr int LG = (MR + 1) / 2;          // lane groups holding results
-    constexpr int TW = 8 * LR;                // terms per result lane per lap
     static_assert(!FUSED || MR == 1, "the fused prologue quantizes one row");
     extern __shared__ v4i s_lds[];
     const int wl = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -63,7 +57,6 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     const int Tc = tile_ok ? T : n_tiles - 1; // address of a missing tile
     const int l = threadIdx.x & 63;
     const int r = l & 15, g = l >> 4;
-    const int NR = (G + S - 1) / S;           // rounds
     const int nq = tile_ok && w < G ? (G - w + S - 1) / S : 0;  // laps of this wave
     // lap block q of the tile: quant piece s at v4i offset s * 64 (+ lane),
     // its scales at SO (+ row)
@@ -74,13 +67,12 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     const v4i *sp = laps + (size_t)Tc * G * LB + SO + r;
     const int n = T * 16 + r;
 
-    // LDS: [act M*kp][red NW floats][terms 2 x TPW x (S-1) x LG x 16 x TW floats]
+    // LDS: [act M*kp][red NW floats][wave sums TPW x (S-1) x LG x 16 x LR floats]
     int8_t *s_act = reinterpret_cast<int8_t *>(s_lds);
     float *red = reinterpret_cast<float *>(s_act + (size_t)M * kp);
-    float *terms = red + 4 * NW;
-    auto tslot = [&](int par, int ww) {  // terms of wave ww >= 1 in round parity par, this lane
-        return terms +
-               ((((size_t)(par * TPW + tw_) * (S - 1) + (ww - 1)) * LG + (g < LG ? g : 0)) * 16 + r) * TW;
+    float *sums = red + 4 * NW;
+    auto sslot = [&](int ww) {  // sums of wave ww >= 1 of this tile, this lane
+        return sums + ((((size_t)tw_ * (S - 1) + (ww - 1)) * LG + (g < LG ? g : 0)) * 16 + r) * LR;
     };
 
     // A operand: lane (r, g) reads activation row r/2 (16 bytes of lane
@@ -129,38 +121,6 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
 #pragma unroll
     for (int j = 0; j < LR; ++j) fs[j] = 0.0f;
 
-    // End of round R: wave 0 adds laps R*S+1 .. R*S+S-1 (those that exist)
-    // in block order.
-    auto round_end = [&](int R) __attribute__((always_inline)) {
-        if constexpr (S > 1) {
-            lds_barrier();
-            if (w == 0) {
-                float4 tv[S - 1][TW / 4];
-#pragma unroll
-                for (int ww = 1; ww < S; ++ww) {
-                    const float4 *src = reinterpret_cast<const float4 *>(tslot(R & 1, ww));
-#pragma unroll
-                    for (int i = 0; i < TW / 4; ++i) tv[ww - 1][i] = src[i];
-                }
-#pragma unroll
-                for (int ww = 1; ww < S; ++ww) {
-                    const int cnt = min(nb - 8 * (R * S + ww), 8);  // valid blocks of the lap
-#pragma unroll
-                    for (int j = 0; j < LR; ++j) {
-#pragma unroll
-                        for (int i = 0; i < 8; ++i) {
-                            const float4 v4 = tv[ww - 1][(8 * j + i) / 4];
-                            const int e = i & 3;
-                            const float t = e == 0 ? v4.x : e == 1 ? v4.y : e == 2 ? v4.z : v4.w;
-                            const float f = fs[j] + t;
-                            fs[j] = i < cnt ? f : fs[j];
-                        }
-                    }
-                }
-            }
-        }
-    };
-
     // Lap L of this wave (round L, lap index L*S + w) in ring slot U.
     // REFILL: lap L + RL exists and is loaded into the slot; CHECK: skip
     // padding blocks past nb (only the tile's last lap can hold them).
@@ -205,21 +165,12 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
                 }
             }
         }
-        if (w == 0) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int b = 8 * q + i;
-                if (!decltype(check)::value || b < nb) {
+        for (int i = 0; i < 8; ++i) {
+            const int b = 8 * q + i;
+            if (!decltype(check)::value || b < nb) {
 #pragma unroll
-                    for (int j = 0; j < LR; ++j) fs[j] = fs[j] + tv[j][i];
-                }
-            }
-        } else if (g < LG) {
-            float4 *dst = reinterpret_cast<float4 *>(tslot(L & 1, w));
-#pragma unroll
-            for (int j = 0; j < LR; ++j) {
-                dst[2 * j] = float4{tv[j][0], tv[j][1], tv[j][2], tv[j][3]};
-                dst[2 * j + 1] = float4{tv[j][4], tv[j][5], tv[j][6], tv[j][7]};
+                for (int j = 0; j < LR; ++j) fs[j] = fs[j] + tv[j][i];
             }
         }
         if constexpr (DEBUG) {
@@ -238,7 +189,6 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
             }
         }
         if (refill) sr[U] = sp[(size_t)(q + RL * S) * LB];
-        round_end(L);
     };
 
     using T1 = std::true_type;
@@ -256,9 +206,21 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
             if (u < rem) lap(k * RL + u, u, false, T1{});
         });
     }
-    // rounds in which this wave has no lap (the barrier count is uniform)
-    for (int R = nq; R < NR; ++R) round_end(R);
-
+    // the wave sums of the tile, added in wave order
+    if constexpr (S > 1) {
+        if (w != 0 && g < LG) {
+#pragma unroll
+            for (int j = 0; j < LR; ++j) sslot(w)[j] = fs[j];
+        }
+        __syncthreads();
+        if (w == 0 && g < LG) {
+            const int sw = min(S, G);  // waves past G hold no lap
+            for (int ww = 1; ww < sw; ++ww) {
+#pragma unroll
+                for (int j = 0; j < LR; ++j) fs[j] = fs[j] + sslot(ww)[j];
+            }
+        }
+    }
     if (w != 0 || !tile_ok) return;
     if constexpr (OPS) {  // one row: lanes 0-15 hold channels 16T .. 16T+15
         const float pv = __shfl_xor(fs[0], 1);
@@ -285,20 +247,30 @@ size_t lds_q8(int s, int tpw, size_t m, size_t kp, size_t G) {
     (void)G;
     const size_t mr = (size_t)mr_of(m);
     const size_t lr = mr == 1 ? 1 : 2, lg = (mr + 1) / 2;
-    return m * kp + (size_t)s * tpw * 16 + 2 * (size_t)tpw * (s - 1) * lg * 16 * lr * 8 * 4;
+    return m * kp + (size_t)s * tpw * 16 + (size_t)tpw * (s - 1) * lg * 16 * lr * 4;
 }
 
-// Configuration by the number of 16-row tiles (measured on MI355X): four
-// waves per tile, with two laps in flight when that leaves fewer than
-// about 2000 waves, else one.
+// Activation pieces per thread of the instances with S waves per tile.
+inline int xr_small(int s) { return 16 / s; }
+inline int xr_large(int s) { return 48 / s; }
+
+// Configuration by the number of 16-row tiles (measured on MI355X at
+// K = 4096 and 11008): four waves per tile and one lap in flight per wave
+// from 512 tiles up; below, more waves per tile (8 at K <= 4096, 16 above)
+// with two laps in flight, so that the launch still has >= 2048 waves.
 CfgQ8 pick_q8(bool fused, size_t n_tiles, size_t m, size_t k, size_t kp, size_t G) {
     CfgQ8 c;
-    c.s = 4;
-    c.rl = n_tiles * 4 >= 2048 ? 1 : 2;
+    if (n_tiles >= 512) {
+        c.s = 4;
+        c.rl = 1;
+    } else {
+        c.s = G > 16 ? 16 : 8;
+        c.rl = 2;
+    }
     const size_t threads = (size_t)c.s * c.tpw * kWave;
     const size_t nx = ceil_div(fused ? k / 4 : m * kp / 16, threads);
-    if (c.s == 1) c.xr = nx <= 8 ? 8 : nx <= 24 ? 24 : 0;
-    else c.xr = nx <= 4 ? 4 : nx <= 12 ? 12 : 0;
+    const size_t xs = (size_t)xr_small(c.s), xl = (size_t)xr_large(c.s);
+    c.xr = nx <= xs ? (int)xs : nx <= xl ? (int)xl : 0;
     if (c.xr == 0 || lds_q8(c.s, c.tpw, m, kp, G) > kMaxLds) c.s = 0;
     return c;
 }
@@ -326,7 +298,8 @@ void dispatch_q8(CfgQ8 c, ActIn in, size_t m, const float *sa_rows, const Q8Matr
                     : launch_q8<MR, S_, TPW_, RL_, XR_, FUSED, OPS, DEBUG, false>(         \
                           in, m, sa_rows, w, out, block_dots, st);
     MRI_Q8(4, 1, 1, 4) MRI_Q8(4, 1, 1, 12)
-    MRI_Q8(4, 1, 2, 4) MRI_Q8(4, 1, 2, 12)
+    MRI_Q8(8, 1, 2, 2) MRI_Q8(8, 1, 2, 6)
+    MRI_Q8(16, 1, 2, 1) MRI_Q8(16, 1, 2, 3)
 #undef MRI_Q8
 }
 

@@ -69,3 +69,30 @@ def synth_int8_weights(rng, n, k):
     import oracle_lib as O
     w = (rng.standard_normal((n, k)) * 0.02).astype(F32)
     return O.quantize_per_channel(w, n, k)
+
+
+def q8_terms_abs_sum(bd, sa, d):
+    """sum_b |t_b| in float64 for the block terms t_b = ((f32)dot_b * s_a) * d_b
+    of matmul_q8_0_direct (q8_direct.rs:281): bd [M, N, nb] block dots,
+    sa [M] activation scales, d [N, nb] block scales; returns [M, N]."""
+    bd = np.abs(np.asarray(bd, np.float64))
+    d = np.abs(np.asarray(d, np.float64))
+    sa = np.abs(np.asarray(sa, np.float64))
+    return np.einsum("mnb,nb->mn", bd, d) * sa[:, None]
+
+
+def assert_q8_close(got, exp, terms_abs, what="", rel=1e-5):
+    """The Q8_0 f32 contract: |got - exp| <= rel * max(|exp|, sum_b |t_b|)
+    per element (the block terms may be added in another order than the
+    reference's left-to-right sum)."""
+    got = np.asarray(got, np.float64)
+    exp = np.asarray(exp, np.float64)
+    assert got.shape == exp.shape, (what, got.shape, exp.shape)
+    bound = rel * np.maximum(np.abs(exp), terms_abs)
+    bad = np.flatnonzero((np.abs(got - exp) > bound).ravel())
+    if bad.size:
+        i = bad[0]
+        raise AssertionError(
+            f"{what}: {bad.size} of {got.size} values outside {rel} * max(|ref|, sum|t_b|); "
+            f"first at {np.unravel_index(i, got.shape)}: got {got.ravel()[i]!r} expected "
+            f"{exp.ravel()[i]!r} (bound {bound.ravel()[i]:.3g})")

@@ -1,8 +1,11 @@
 """GPU parity: the HIP kernels through the C ABI vs the CPU oracle.
 
 Integer results (quantized activations, int32 accumulators, block dots) and
-the per-channel / Q8_0 f32 outputs must be bit-identical; Q4_0 (W4A32)
-outputs are within 1e-5 * max(|ref|, sum_k |x_k w_k|).
+the per-channel INT8 f32 outputs must be bit-identical.  Q8_0 f32 outputs
+are within 1e-5 * max(|ref|, sum_b |t_b|) of the reference's left-to-right
+block sum (the decode GEMV, M <= 4, adds per-wave partial sums); above four
+rows, where the kernel keeps the reference's order, they are bit-identical.
+Q4_0 (W4A32) outputs are within 1e-5 * max(|ref|, sum_k |x_k w_k|).
 """
 import sys
 
@@ -11,8 +14,8 @@ import pytest
 
 import closed_form as CF
 import oracle_lib as O
-from gpu_util import (F32, assert_bits_equal, bits, dev, empty, host, synth_int8_weights,
-                      synth_q4_0, synth_q8_0, torch)
+from gpu_util import (F32, assert_bits_equal, assert_q8_close, bits, dev, empty, host,
+                      q8_terms_abs_sum, synth_int8_weights, synth_q4_0, synth_q8_0, torch)
 
 pytestmark = pytest.mark.gpu
 
@@ -239,8 +242,17 @@ Q8_SHAPES = [
 ]
 
 
+def q8_check(got, out0, bd0, sa0, raw, n, k, what):
+    """Q8_0 f32 outputs against the oracle: within the contract, and bit for
+    bit above four rows (the kernels there keep the reference's order)."""
+    d, _ = CF.q8_0_split(raw, n, k)
+    assert_q8_close(got, out0, q8_terms_abs_sum(bd0, sa0, d), what)
+    if got.shape[0] > 4:
+        assert_bits_equal(got, out0, what)
+
+
 @pytest.mark.parametrize("m,n,k", Q8_SHAPES)
-def test_matmul_q8_0_direct_bit_exact(m, n, k):
+def test_matmul_q8_0_direct_parity(m, n, k):
     say(f"matmul_q8_0_direct m={m} n={n} k={k}")
     t = torch()
     rng = np.random.default_rng(m * 11 + n + k)
@@ -254,10 +266,10 @@ def test_matmul_q8_0_direct_bit_exact(m, n, k):
     mri().matmul_q8_0_direct(dev(x), w, out, bd, sa)
     assert np.array_equal(bits(host(sa)), bits(sa0))
     assert np.array_equal(host(bd), bd0)
-    assert_bits_equal(host(out), out0, "q8_0 out")
+    q8_check(host(out), out0, bd0, sa0, raw, n, k, "q8_0 out")
     out2 = empty((m, n), t.float32)        # without the debug outputs
     mri().matmul_q8_0_direct(dev(x), w, out2)
-    assert_bits_equal(host(out2), out0, "q8_0 out (no debug outputs)")
+    assert_bits_equal(host(out2), host(out), "q8_0 out (no debug outputs)")
 
 
 def test_q8_0_reference_encoder_weights():
@@ -268,11 +280,11 @@ def test_q8_0_reference_encoder_weights():
     wf = (rng.standard_normal((24, 256)) * 0.05).astype(F32)
     raw = O.quantize_q8_0(wf)
     x = rng.standard_normal((3, 256)).astype(F32)
-    out0 = O.matmul_q8_0_direct(x, raw, 24, 256)
+    out0, bd0, sa0 = O.matmul_q8_0_direct(x, raw, 24, 256, want_block_dots=True)
     w = mri().Q8Matrix.from_raw_bytes(raw, 24, 256)
     out = empty((3, 24), t.float32)
     mri().matmul_q8_0_direct(dev(x), w, out)
-    assert_bits_equal(host(out), out0, "q8_0 encoder weights")
+    q8_check(host(out), out0, bd0, sa0, raw, 24, 256, "q8_0 encoder weights")
 
 
 # ---- Q4_0 ----------------------------------------------------------------------------
@@ -435,7 +447,8 @@ def test_bound_calls_match():
 @pytest.mark.parametrize("m", [1, 3])
 def test_unfused_path_matches(m):
     """x at a 4-byte (not 16-byte) aligned address takes the two-kernel path
-    (quantize kernel + GEMV); both paths must agree bit-for-bit."""
+    (quantize kernel + GEMV): Q8_0 within the contract of the oracle and bit
+    for bit equal to the fused path; INT8 bit for bit."""
     t = torch()
     rng = np.random.default_rng(21 + m)
     n, k = 48, 4096
@@ -445,11 +458,14 @@ def test_unfused_path_matches(m):
     buf = dev(np.concatenate([np.zeros(1, F32), x.ravel()]))
     xu = buf[1:].view(m, k)                       # misaligned by 4 bytes
     assert xu.data_ptr() % 16 != 0
-    out0 = O.matmul_q8_0_direct(x, raw, n, k)
+    out0, bd0, sa0 = O.matmul_q8_0_direct(x, raw, n, k, want_block_dots=True)
     w8 = mri().Q8Matrix.from_raw_bytes(raw, n, k)
     out = empty((m, n), t.float32)
     mri().matmul_q8_0_direct(xu, w8, out)
-    assert_bits_equal(host(out), out0, "q8_0 unfused")
+    q8_check(host(out), out0, bd0, sa0, raw, n, k, "q8_0 unfused")
+    fused = empty((m, n), t.float32)
+    mri().matmul_q8_0_direct(dev(x), w8, fused)
+    assert_bits_equal(host(out), host(fused), "q8_0 unfused vs fused")
     ref, aq0, sa0, acc0 = O.matmul_int8_from_f32(x, wq, ws)
     wi = mri().QMatrix.from_host(wq, ws)
     out2, aq, sa = empty((m, n), t.float32), empty((m, k), t.int8), empty(1, t.float32)

@@ -1,8 +1,10 @@
 """GPU parity of the W4A8 extension (include/mri_qmatmul.h,
 mri_matmul_q4_0_w4a8) against the oracle's orc_matmul_q4_0_w4a8, which is
 pinned to matmul_q8_0_direct on the expanded blocks
-(tests/test_oracle_closed_form.py).  Block dots, activation scales and the
-block-ordered f32 outputs must be bit-identical, in both nibble orders."""
+(tests/test_oracle_closed_form.py).  Block dots and activation scales must
+be bit-identical, in both nibble orders; f32 outputs are within
+1e-5 * max(|ref|, sum_b |t_b|) of the block-ordered sum (the decode GEMV,
+M <= 4, adds per-wave partial sums) and bit-identical above four rows."""
 import sys
 
 import numpy as np
@@ -10,7 +12,8 @@ import pytest
 
 import closed_form as CF
 import oracle_lib as O
-from gpu_util import F32, assert_bits_equal, bits, dev, empty, host, synth_q4_0, torch
+from gpu_util import (F32, assert_bits_equal, assert_q8_close, bits, dev, empty, host,
+                      q8_terms_abs_sum, synth_q4_0, torch)
 
 pytestmark = pytest.mark.gpu
 
@@ -49,10 +52,13 @@ def test_w4a8_bit_exact(m, n, k, order):
     mri().matmul_q4_0_w4a8(dev(x), w, out, bd, sa)
     assert np.array_equal(bits(host(sa)), bits(sa0))
     assert np.array_equal(host(bd), bd0)
-    assert_bits_equal(host(out), out0, "w4a8 out")
+    d, _ = CF.q4_0_split(raw, n, k)
+    assert_q8_close(host(out), out0, q8_terms_abs_sum(bd0, sa0, d), "w4a8 out")
+    if m > 4:  # the kernels above four rows keep the reference's order
+        assert_bits_equal(host(out), out0, "w4a8 out")
     out2 = empty((m, n), t.float32)          # without the debug outputs
     mri().matmul_q4_0_w4a8(dev(x), w, out2)
-    assert_bits_equal(host(out2), out0, "w4a8 out (no debug outputs)")
+    assert_bits_equal(host(out2), host(out), "w4a8 out (no debug outputs)")
 
 
 def test_w4a8_ggml_file_order_matches_reference_order():
@@ -84,7 +90,9 @@ def test_w4a8_unfused_and_device_upload():
     w = mri().Q4Matrix.from_raw_device(dev(raw), n, k)
     out = empty((1, n), t.float32)
     mri().matmul_q4_0_w4a8(xu, w, out)
-    assert_bits_equal(host(out), O.matmul_q4_0_w4a8(x, raw, n, k), "w4a8 unfused")
+    out0, bd0, sa0 = O.matmul_q4_0_w4a8(x, raw, n, k, want_block_dots=True)
+    d, _ = CF.q4_0_split(raw, n, k)
+    assert_q8_close(host(out), out0, q8_terms_abs_sum(bd0, sa0, d), "w4a8 unfused")
 
 
 def test_w4a8_errors():
