@@ -470,6 +470,26 @@ def main():
     log(f"q8_0 decode [1,{k}]x[{k},{n}]: {ms*1e3:.2f} us/call, {value:.0f} GB/s")
 
     secondary = {}
+    # the one-kernel read ceiling at the headline's size, same rotation
+    rbytes = nbytes // 16 * 16
+    bufs = [torch.empty(rbytes, dtype=torch.uint8, device="cuda") for _ in range(nrot)]
+    for b_ in bufs:
+        b_.fill_(1)
+    import ctypes
+    f_rd = M.lib().mri_hbm_read
+    st_rd = M._stream(None)
+    a_rd = [(ctypes.c_void_p(b_.data_ptr()), rbytes, None, st_rd) for b_ in bufs]
+    ms_rd = T.per_call_ms(lambda i: f_rd(*a_rd[i]), args.steps, args.warmup, nrot)
+    del bufs
+    gbs_rd = rbytes / (ms_rd * 1e-3) / 1e9
+    secondary["hbm_read_ceiling"] = {
+        "bytes": rbytes, "us": round(ms_rd * 1e3, 2), "GB_s": round(gbs_rd, 1),
+        "frac_of_hbm_peak": round(gbs_rd / HBM_PEAK_GBS, 4),
+        "gemv_frac_of_read_ceiling": round(value / gbs_rd, 4),
+        "what": "one plain streaming-read kernel over the same number of bytes, same "
+                "rotation and timing (mri_hbm_read)"}
+    log(f"plain read of {rbytes} B: {ms_rd*1e3:.2f} us, {gbs_rd:.0f} GB/s "
+        f"(GEMV at {value / gbs_rd:.3f} of it)")
     if not args.no_secondary:
         steps2 = max(20, args.steps // 2)
         sweep = {}

@@ -245,6 +245,13 @@ mri_status mri_matmul_q4_0_dequant_ordered(const float *input, const size_t *dim
 /* Waits for all work enqueued on `stream`. */
 mri_status mri_synchronize(void *stream);
 
+/* Diagnostic, no counterpart in the reference: one kernel that streams
+ * `bytes` (rounded down to 16) of device memory at p (16-byte aligned) and
+ * discards them, i.e. the ceiling a one-kernel read of that size reaches on
+ * this device, next to which the benchmark reports the decode GEMVs.  sink
+ * (nullable, device) is never written for ordinary data. */
+mri_status mri_hbm_read(const void *p, size_t bytes, int32_t *sink, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

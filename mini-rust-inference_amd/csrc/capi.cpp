@@ -927,6 +927,12 @@ mri_status mri_matmul_q4_0_dequant_ordered(const float *input, const size_t *dim
     return launch_q4_0_dequant(x, m, k, weight_q4, n_out, order == MRI_Q4_ORDER_GGML, out, s);
 }
 
+mri_status mri_hbm_read(const void *p, size_t bytes, int32_t *sink, void *stream) {
+    if (bytes && !p) return set_error(MRI_ERR_INVALID_ARGUMENT, "p is null");
+    if (!aligned(p, 16)) return set_error(MRI_ERR_INVALID_ARGUMENT, "p is not 16-byte aligned");
+    return launch_hbm_read(p, bytes, sink, static_cast<hipStream_t>(stream));
+}
+
 mri_status mri_synchronize(void *stream) {
     MRI_HIP(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
     return MRI_OK;

@@ -191,6 +191,10 @@ mri_status launch_dot_i8(const int8_t *a, const int8_t *b, size_t n,
                          int32_t *out, hipStream_t s);
 size_t quantize_partials_count(size_t n);
 
+// hbm_read.hip: a plain streaming read of `bytes` (16-byte aligned) device
+// bytes; sink (nullable) is written only in a case that does not occur.
+mri_status launch_hbm_read(const void *p, size_t bytes, int32_t *sink, hipStream_t s);
+
 // repack.hip
 mri_status launch_repack_int8(const int8_t *data, const float *scales,
                               QMatrixDev &w, hipStream_t s);

@@ -1,0 +1,45 @@
+// hbm_read.hip — a plain streaming read of device memory, the measured
+// ceiling of a one-kernel HBM read at a given size (a diagnostic for the
+// benchmark: the decode GEMVs are bounded by it, not by the datasheet peak).
+#include <algorithm>
+
+#include "common.hpp"
+
+namespace mri {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// Grid-stride over n16 16-byte vectors, four loads in flight per thread;
+// the values are folded into one word that is stored only if it equals a
+// value the data never produce in practice, so the loads cannot be dropped.
+__global__ __launch_bounds__(256) void k_hbm_read(const v4i *__restrict__ p, size_t n16,
+                                                  int *__restrict__ sink) {
+    int acc = 0;
+    const size_t stride = (size_t)gridDim.x * 256;
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    for (; i + 3 * stride < n16; i += 4 * stride) {
+        const v4i a = __builtin_nontemporal_load(p + i);
+        const v4i b = __builtin_nontemporal_load(p + i + stride);
+        const v4i c = __builtin_nontemporal_load(p + i + 2 * stride);
+        const v4i d = __builtin_nontemporal_load(p + i + 3 * stride);
+        acc ^= a.x ^ b.y ^ c.z ^ d.w;
+    }
+    for (; i < n16; i += stride) acc ^= p[i].x;
+    if (acc == 0x5a5a5a5a && sink) *sink = acc;
+}
+
+}  // namespace
+
+mri_status launch_hbm_read(const void *p, size_t bytes, int32_t *sink, hipStream_t s) {
+    const size_t n16 = bytes / 16;
+    if (n16 == 0) return MRI_OK;
+    const int cus = device_cus();
+    const unsigned grid = (unsigned)std::max(1, 16 * (cus > 0 ? cus : 256));
+    hipLaunchKernelGGL(k_hbm_read, dim3(grid), dim3(256), 0, s, static_cast<const v4i *>(p), n16,
+                       reinterpret_cast<int *>(sink));
+    MRI_LAUNCHED("k_hbm_read");
+    return MRI_OK;
+}
+
+}  // namespace mri

@@ -65,6 +65,7 @@ _SIGS = {
     "mri_matmul_q4_0_w4a8": ([P, P, SZ, P, P, P, P, P], ST),
     "mri_matmul_q4_0_dequant_ordered": ([P, P, SZ, P, SZ, SZ, SZ, C.c_int, P, P], ST),
     "mri_synchronize": ([P], ST),
+    "mri_hbm_read": ([P, SZ, P, P], ST),
 }
 
 # Every symbol the header declares (checked by the CPU test suite).
@@ -387,3 +388,10 @@ def synchronize(stream=None):
 
 def version() -> str:
     return lib().mri_version().decode()
+
+
+def hbm_read(buf, nbytes=None, stream=None):
+    """One kernel that reads nbytes of the device tensor buf (diagnostic:
+    the one-kernel HBM read ceiling at that size)."""
+    n = buf.numel() * buf.element_size() if nbytes is None else nbytes
+    check(lib().mri_hbm_read(C.c_void_p(buf.data_ptr()), n, None, _stream(stream)))
