@@ -531,6 +531,22 @@ def main():
                     "us_from_f32": round(ms_f * 1e3, 2), "TOPS_from_f32": round(tops_f, 1)}
                 log(f"int8 prefill M={mm} N={nn}: {ms_r*1e3:.1f} us {tops:.0f} TOPS "
                     f"(from f32 {ms_f*1e3:.1f} us)")
+        # the int8 MFMA ceiling on this device with random operands and no
+        # memory traffic (the power state of real data), next to the GEMM
+        src = torch.randint(-127, 128, (32768,), dtype=torch.int8, device="cuda")
+        M.mfma_i8_peak(src, 200)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        ops_pk = sum(M.mfma_i8_peak(src, 4000)[0] for _ in range(5))
+        e1.record()
+        torch.cuda.synchronize()
+        tops_pk = ops_pk / (e0.elapsed_time(e1) * 1e-3) / 1e12
+        prefill["mfma_i8_ceiling"] = {
+            "TOPS": round(tops_pk, 1), "frac_of_int8_peak": round(tops_pk / INT8_PEAK_TOPS, 4),
+            "what": "v_mfma_i32_32x32x32_i8 only, random operands in registers, 8 waves per "
+                    "CU, no memory traffic (mri_mfma_i8_peak)"}
+        log(f"int8 MFMA ceiling (random operands, no memory): {tops_pk:.0f} TOPS")
         secondary["int8_prefill_gemm"] = prefill
 
         ms_q4 = bench_q4(torch, M, T, 1, 11008, 4096, steps2, args.warmup)

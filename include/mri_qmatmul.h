@@ -252,6 +252,15 @@ mri_status mri_synchronize(void *stream);
  * (nullable, device) is never written for ordinary data. */
 mri_status mri_hbm_read(const void *p, size_t bytes, int32_t *sink, void *stream);
 
+/* Diagnostic, no counterpart in the reference: the int8 MFMA ceiling of
+ * this device with operands of real data.  One workgroup of 8 waves per CU
+ * (*n_cus receives the CU count) loads 32 KiB of int8 operands from src
+ * (device, 16-byte aligned) once and runs iters x 8 v_mfma_i32_32x32x32_i8
+ * per wave (2 * 32768 * 8 * iters int ops per wave) with no other memory
+ * traffic; the benchmark times it beside the prefill GEMM. */
+mri_status mri_mfma_i8_peak(const int8_t *src, int iters, int32_t *sink, int *n_cus,
+                            void *stream);
+
 #ifdef __cplusplus
 }
 #endif

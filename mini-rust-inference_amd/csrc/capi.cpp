@@ -933,6 +933,15 @@ mri_status mri_hbm_read(const void *p, size_t bytes, int32_t *sink, void *stream
     return launch_hbm_read(p, bytes, sink, static_cast<hipStream_t>(stream));
 }
 
+mri_status mri_mfma_i8_peak(const int8_t *src, int iters, int32_t *sink, int *n_cus,
+                            void *stream) {
+    if (!src) return set_error(MRI_ERR_INVALID_ARGUMENT, "src is null");
+    if (!aligned(src, 16)) return set_error(MRI_ERR_INVALID_ARGUMENT, "src is not 16-byte aligned");
+    if (iters < 1) return set_error(MRI_ERR_INVALID_ARGUMENT, "iters < 1");
+    if (n_cus) *n_cus = device_cus();
+    return launch_mfma_peak(src, iters, sink, static_cast<hipStream_t>(stream));
+}
+
 mri_status mri_synchronize(void *stream) {
     MRI_HIP(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
     return MRI_OK;

@@ -194,6 +194,9 @@ size_t quantize_partials_count(size_t n);
 // hbm_read.hip: a plain streaming read of `bytes` (16-byte aligned) device
 // bytes; sink (nullable) is written only in a case that does not occur.
 mri_status launch_hbm_read(const void *p, size_t bytes, int32_t *sink, hipStream_t s);
+// One workgroup of 8 waves per CU, each running 8 * iters int8 32x32x32
+// MFMAs on operands loaded once from src (32 KiB of int8).
+mri_status launch_mfma_peak(const int8_t *src, int iters, int32_t *sink, hipStream_t s);
 
 // repack.hip
 mri_status launch_repack_int8(const int8_t *data, const float *scales,

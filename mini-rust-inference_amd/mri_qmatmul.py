@@ -66,6 +66,7 @@ _SIGS = {
     "mri_matmul_q4_0_dequant_ordered": ([P, P, SZ, P, SZ, SZ, SZ, C.c_int, P, P], ST),
     "mri_synchronize": ([P], ST),
     "mri_hbm_read": ([P, SZ, P, P], ST),
+    "mri_mfma_i8_peak": ([P, C.c_int, P, C.POINTER(C.c_int), P], ST),
 }
 
 # Every symbol the header declares (checked by the CPU test suite).
@@ -395,3 +396,12 @@ def hbm_read(buf, nbytes=None, stream=None):
     the one-kernel HBM read ceiling at that size)."""
     n = buf.numel() * buf.element_size() if nbytes is None else nbytes
     check(lib().mri_hbm_read(C.c_void_p(buf.data_ptr()), n, None, _stream(stream)))
+
+
+def mfma_i8_peak(src, iters, stream=None):
+    """Enqueues the int8 MFMA ceiling kernel on operands src (torch int8,
+    >= 32 KiB on the device); returns (int ops per launch, CUs)."""
+    n = C.c_int(0)
+    check(lib().mri_mfma_i8_peak(C.c_void_p(src.data_ptr()), int(iters), None, C.byref(n),
+                                 _stream(stream)))
+    return 2 * 32768 * 8 * int(iters) * 8 * n.value, n.value
