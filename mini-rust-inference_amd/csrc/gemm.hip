@@ -236,27 +236,83 @@ __global__ __launch_bounds__(WM * WN * kWave) void k_gemm_int8(
 
     // epilogue: lane l, register r of tile (i, j) holds row
     // m0 + 32*(wm*TM + i) + 8*(r/4) + 4*(l/32) + r%4 and column
-    // n = 16*T0 + 32*(wn*TN + j) + l%32
+    // n = 16*T0 + 32*(wn*TN + j) + l%32.  The scales are loaded first: a
+    // global load issued after output stores would wait for those stores
+    // (one in-order counter covers both).
+    float sw[TN], sa[TM][16];
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        const int n = 16 * T0 + 32 * (wn * TN + j) + (l & 31);
-        if (n >= N) continue;
-        const float sw = wscales[n];
+    for (int j = 0; j < TN; ++j) sw[j] = wscales[min(16 * T0 + 32 * (wn * TN + j) + (l & 31), N - 1)];
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = m0 + 32 * (wm * TM + i) + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
-                if (m < M) {
-                    const float sa = sa_ptr ? sa_ptr[(size_t)m * sa_stride] : sa_value;
-                    float v = (float)acc[i][j][r] * sa;
-                    v = v * sw;
-                    out[(size_t)m * N + n] = v;
-                    if (acc_out) acc_out[(size_t)m * N + n] = acc[i][j][r];
+        for (int r = 0; r < 16; ++r) {
+            const int m = min(m0 + 32 * (wm * TM + i) + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3), M - 1);
+            sa[i][r] = sa_ptr ? sa_ptr[(size_t)m * sa_stride] : sa_value;
+        }
+    if (acc_out) {  // with the int32 accumulators: element stores
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int n = 16 * T0 + 32 * (wn * TN + j) + (l & 31);
+            if (n >= N) continue;
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = m0 + 32 * (wm * TM + i) + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+                    if (m < M) {
+                        float v = (float)acc[i][j][r] * sa[i][r];
+                        v = v * sw[j];
+                        out[(size_t)m * N + n] = v;
+                        acc_out[(size_t)m * N + n] = acc[i][j][r];
+                    }
                 }
             }
         }
+        return;
     }
+    // f32 outputs only: the tile is staged in LDS (the ring is free: every
+    // wave's loads have landed and the barrier ends all reads of it) and
+    // written row by row, 16 contiguous bytes per lane, which measured
+    // ~6 us faster than element stores at M = 512, N = 11008.
+    constexpr int PITCH = BN + 4;  // floats per staged row (pads the banks)
+    float *st = reinterpret_cast<float *>(s_buf);
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int rt = 32 * (wm * TM + i) + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+                float v = (float)acc[i][j][r] * sa[i][r];
+                st[rt * PITCH + 32 * (wn * TN + j) + (l & 31)] = v * sw[j];
+            }
+    __syncthreads();
+    constexpr int V = BN / 4;  // 16-byte vectors per row
+    const int n0 = 16 * T0;
+    const bool vec = (N & 3) == 0 && ((size_t)out & 15) == 0;
+    for (int e = t; e < BM * V; e += NW * kWave) {
+        const int rt = e / V, c4 = e - rt * V;
+        const int m = m0 + rt, n = n0 + 4 * c4;
+        if (m >= M || n >= N) continue;
+        typedef float v4f __attribute__((ext_vector_type(4)));
+        const v4f v = *reinterpret_cast<const v4f *>(st + rt * PITCH + 4 * c4);
+        float *dst = out + (size_t)m * N + n;
+        if (vec && n + 4 <= N) {
+            *reinterpret_cast<v4f *>(dst) = v;
+        } else {
+            const float vv[4] = {v.x, v.y, v.z, v.w};
+            for (int q = 0; q < 4 && n + q < N; ++q) dst[q] = vv[q];
+        }
+    }
+}
+
+// Dynamic LDS of k_gemm_int8: the ring, or the staged output tile.
+template <int BM, int BN, int NSA, int NSB>
+constexpr size_t gemm_lds_bytes() {
+    constexpr size_t ring = ((size_t)NSA * (BM / 32) + (size_t)NSB * (BN / 32)) * 2 * 1024;
+    constexpr size_t stage = (size_t)BM * (BN + 4) * 4;
+    return ring > stage ? ring : stage;
 }
 
 // ---------------------------------------------------------------------------
@@ -654,7 +710,7 @@ template <int BM, int BN, int WM, int WN, int NSA, int NSB>
 mri_status launch(const int8_t *act_packed, size_t m, const float *sa_ptr, int sa_stride,
                   float sa_value, const QMatrixDev &w, float *out, int32_t *acc_out,
                   hipStream_t s) {
-    constexpr size_t lds = ((size_t)NSA * (BM / 32) + (size_t)NSB * (BN / 32)) * 2 * 1024;
+    constexpr size_t lds = gemm_lds_bytes<BM, BN, NSA, NSB>();
     static DeviceOnce attr;  // the attribute belongs to the function
     MRI_HIP(attr.run([&](int) {
         return hipFuncSetAttribute(
