@@ -436,6 +436,9 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device copy, 20 times (the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
+    ap.add_argument("--profile-gemm", default="",
+                    help="only run matmul_int8 20 times at each comma-separated MxKxN shape "
+                         "(random int8 operands; a workload for rocprofv3 counter passes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -459,6 +462,21 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_read": src.numel() * 4, "copy_bytes_written":
                           dst.numel() * 4, "launches": 20}), flush=True)
+        return
+
+    if args.profile_gemm:
+        for spec in args.profile_gemm.split(","):
+            mm, kk, nn = (int(v) for v in spec.split("x"))
+            g = torch.Generator(device="cuda").manual_seed(1)
+            wq = torch.randint(-127, 128, (nn, kk), dtype=torch.int8, device="cuda", generator=g)
+            wsc = torch.rand(nn, device="cuda", generator=g) * 1e-3
+            w = M.QMatrix.from_device(wq, wsc)
+            a = torch.randint(-127, 128, (mm, kk), dtype=torch.int8, device="cuda", generator=g)
+            o = torch.empty((mm, nn), device="cuda")
+            for _ in range(20):
+                M.matmul_int8(a, 0.01, w, mm, o)
+            torch.cuda.synchronize()
+            log(f"profile-gemm {spec}: 20 calls")
         return
 
     # ---- headline: Q8_0 decode GEMV [1,4096] x [4096,11008] ------------------
