@@ -174,7 +174,7 @@ static std::string dims_str(const size_t *dims, size_t ndim) {
 }
 
 // matmul_int8 dispatch on prepared activations [m][kp].
-static mri_status run_int8(const int8_t *act, size_t m, const float *sa_ptr,
+mri_status run_int8(const int8_t *act, size_t m, const float *sa_ptr,
                            int sa_stride, float sa_value, const QMatrixDev &w,
                            float *out, int32_t *acc_out, hipStream_t s) {
     if (gemv_int8_supported(false, m, w.n_tiles, w.k_in, w.kp))
@@ -184,7 +184,7 @@ static mri_status run_int8(const int8_t *act, size_t m, const float *sa_ptr,
 }
 
 // matmul_q8_0_direct dispatch on quantized rows [m][kp] (chunk-permuted).
-static mri_status run_q8(const int8_t *act, size_t m, const float *sa_rows,
+mri_status run_q8(const int8_t *act, size_t m, const float *sa_rows,
                          const Q8MatrixDev &w, float *out, int32_t *block_dots,
                          hipStream_t s) {
     if (gemv_q8_supported(false, m, w.n_tiles, w.k_in, w.kp))

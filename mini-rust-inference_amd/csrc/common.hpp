@@ -305,6 +305,29 @@ mri_status launch_embed_rmsnorm(const float *table, const uint32_t *tokens, size
                                 size_t d, const float *w, float eps, float *x_out, float *out,
                                 hipStream_t s);
 // x += delta, out = rmsnorm(x): one pass.
+// RMSNorm statistics of rows (rms_inv, max |normalized|) per row into
+// stats[2*row], stats[2*row+1] without storing the normalized rows: mode 0
+// norm x, mode 1 gather from the table x by tokens into x_out first, mode 2
+// add delta into x_out (= x) first.  rmsnorm_stats_supported(d): d % 4 == 0
+// and d <= 8192 (16-byte aligned rows).
+bool rmsnorm_stats_supported(size_t d);
+mri_status launch_rmsnorm_stats(int mode, const float *x, const float *delta,
+                                const uint32_t *tokens, float *x_out, size_t rows, size_t d,
+                                const float *w, float eps, float *stats, hipStream_t s);
+// Quantize the normalized rows w * (x * rms_inv) from those statistics:
+// form 0 per-tensor scale into the GEMM-packed layout (ld = kp), form 1
+// per-tensor into [rows][ld] plain, form 2 per-row scales into [rows][ld]
+// chunk-permuted (Q8_0), form 3 the f32 normalized rows into `normed`.
+mri_status launch_norm_quant(int form, const float *x, const float *w, const float *stats,
+                             size_t rows, size_t d, size_t ld, int8_t *q, float *scales,
+                             float *normed, hipStream_t s);
+// capi.cpp: the matmul dispatch on quantized rows [m][kp] (INT8 plain,
+// Q8_0 / W4A8 chunk-permuted), as the entry points use it.
+mri_status run_int8(const int8_t *act, size_t m, const float *sa_ptr, int sa_stride,
+                    float sa_value, const QMatrixDev &w, float *out, int32_t *acc_out,
+                    hipStream_t s);
+mri_status run_q8(const int8_t *act, size_t m, const float *sa_rows, const Q8MatrixDev &w,
+                  float *out, int32_t *block_dots, hipStream_t s);
 mri_status launch_add_rmsnorm(float *x, const float *delta, size_t rows, size_t d,
                               const float *w, float eps, float *out, hipStream_t s);
 // RoPE of q in place; rotated k and v rows into the cache at start_pos + s.

@@ -11,6 +11,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cfloat>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -58,14 +59,21 @@ __global__ __launch_bounds__(256) void k_embed(const float *__restrict__ table,
 // table[tokens[row]], and also stored to x_out (embed + the first norm).
 // MODE 2 (NV > 0): the row is first x + delta (the residual add,
 // forward_int8.rs:100-121), stored back to x_out (= x) before the norm.
-template <int NV, int MODE = 0>
+// STATS (NV > 0): instead of the normalized row, out[2*row] = rms_inv and
+// out[2*row + 1] = max |w * (x * rms_inv)| over the row (the values the
+// quantizer that consumes the row needs; k_norm_quant recomputes the row
+// from x with the same operations, so the normalized rows never go to
+// memory).
+template <int NV, int MODE = 0, bool STATS = false>
 // (x and x_out are the same buffer in MODE 2: neither is restrict.)
 __global__ __launch_bounds__(256) void k_rmsnorm(const float *x, const float *__restrict__ w,
                                                  int d, float eps, float *__restrict__ out,
                                                  const uint32_t *__restrict__ tokens = nullptr,
                                                  const float *__restrict__ delta = nullptr,
                                                  float *x_out = nullptr) {
+    static_assert(!STATS || NV > 0, "row statistics need the register-resident row");
     __shared__ float s_part[4];
+    __shared__ float s_max[4];
     const float *xr = MODE == 1 ? x + (size_t)tokens[blockIdx.x] * d : x + (size_t)blockIdx.x * d;
     float *orow = out + (size_t)blockIdx.x * d;
     float acc = 0.0f;
@@ -117,7 +125,27 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *x, const float *__
     const float sum = ((s_part[0] + s_part[1]) + s_part[2]) + s_part[3];
     const float mean_sq = sum / (float)d;
     const float rms_inv = 1.0f / sqrtf(mean_sq + eps);
-    if constexpr (NV > 0) {
+    if constexpr (STATS) {
+        float mx = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NV; ++c) {
+            const int i = (c * 256 + threadIdx.x) * 4;
+            if (i < d) {
+                const float4 wv = *reinterpret_cast<const float4 *>(w + i);
+                mx = fmaxf(mx, fabsf(wv.x * (xv[c].x * rms_inv)));
+                mx = fmaxf(mx, fabsf(wv.y * (xv[c].y * rms_inv)));
+                mx = fmaxf(mx, fabsf(wv.z * (xv[c].z * rms_inv)));
+                mx = fmaxf(mx, fabsf(wv.w * (xv[c].w * rms_inv)));
+            }
+        }
+        mx = wave_max(mx);
+        if ((threadIdx.x & 63) == 0) s_max[threadIdx.x >> 6] = mx;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            out[2 * (size_t)blockIdx.x] = rms_inv;
+            out[2 * (size_t)blockIdx.x + 1] = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+        }
+    } else if constexpr (NV > 0) {
 #pragma unroll
         for (int c = 0; c < NV; ++c) {
             const int i = (c * 256 + threadIdx.x) * 4;
@@ -808,6 +836,38 @@ mri_status launch_add_rmsnorm(float *x, const float *delta, size_t rows, size_t 
         hipLaunchKernelGGL((k_rmsnorm<8, 2>), g, b, 0, s, x, w, (int)d, eps, out, nullptr,
                            delta, x);
     MRI_LAUNCHED("k_rmsnorm");
+    return MRI_OK;
+}
+
+bool rmsnorm_stats_supported(size_t d) { return d % 4 == 0 && d <= 8192; }
+
+// The statistics of RMSNorm rows (STATS above): mode 0 norm x as is, mode 1
+// gather the rows from `table` by `tokens` into x_out first, mode 2 add
+// delta into x first.  d % 4 == 0, d <= 8192, 16-byte aligned rows.
+mri_status launch_rmsnorm_stats(int mode, const float *x, const float *delta,
+                                const uint32_t *tokens, float *x_out, size_t rows, size_t d,
+                                const float *w, float eps, float *stats, hipStream_t s) {
+    if (!rows) return MRI_OK;
+    if (!rmsnorm_stats_supported(d) || !al16(x) || !al16(w) || (delta && !al16(delta)) ||
+        (x_out && !al16(x_out)))
+        return set_error(MRI_ERR_INVALID_ARGUMENT, "rmsnorm stats: unsupported row shape");
+    const dim3 g((unsigned)rows), b(256);
+    auto go = [&](auto nv) {
+        constexpr int NV = decltype(nv)::value;
+        if (mode == 1)
+            hipLaunchKernelGGL((k_rmsnorm<NV, 1, true>), g, b, 0, s, x, w, (int)d, eps, stats,
+                               tokens, nullptr, x_out);
+        else if (mode == 2)
+            hipLaunchKernelGGL((k_rmsnorm<NV, 2, true>), g, b, 0, s, x, w, (int)d, eps, stats,
+                               nullptr, delta, x_out);
+        else
+            hipLaunchKernelGGL((k_rmsnorm<NV, 0, true>), g, b, 0, s, x, w, (int)d, eps, stats);
+    };
+    if (d <= 1024) go(std::integral_constant<int, 1>{});
+    else if (d <= 2048) go(std::integral_constant<int, 2>{});
+    else if (d <= 4096) go(std::integral_constant<int, 4>{});
+    else go(std::integral_constant<int, 8>{});
+    MRI_LAUNCHED("k_rmsnorm(stats)");
     return MRI_OK;
 }
 

@@ -52,6 +52,17 @@ struct mri_llama {
     float *attn_part = nullptr;   // split-key decode attention partials
     float *logits_buf = nullptr;  // prefill logits for generation, grown on demand
     size_t logits_rows = 0;
+    // Rows path with fused RMSNorm (fuse_norm): the RMSNorm that feeds the
+    // next projections is kept as statistics (nstats: rms_inv and max |y|
+    // per row) over x with weights norm_w; each projection quantizes the
+    // normalized rows straight from x into qact / qscale (qform: the form
+    // held there, -1 none), so the normalized f32 rows are not stored.
+    bool fuse_norm = false;
+    float *nstats = nullptr, *qscale = nullptr;
+    int8_t *qact = nullptr;
+    const float *norm_w = nullptr;
+    int qform = -1;
+    size_t qld = 0;
     int row_path = -1;            // decode rows take the folded path (-1: not yet known)
     std::vector<void *> allocs;
 };
@@ -201,6 +212,48 @@ mri_status proj(const mri_weight_ref &w, const float *in, size_t rows, float *ou
     }
 }
 
+// The projection of the rows RMS-normalized by the statistics in m->nstats
+// (fused path): the activations are quantized from m->x in the form the
+// weight's entry point uses (INT8: one scale over all rows, packed for the
+// GEMM from kGemmMinRows rows; Q8_0 / W4A8: a scale per row; Q4_0: the f32
+// rows themselves), once per form while the statistics stay the same.
+mri_status proj_normed(mri_llama *m, const mri_weight_ref &w, size_t rows, float *out,
+                       hipStream_t s) {
+    const size_t d = m->cfg.dim;
+    auto prepare = [&](int form, size_t ld) -> mri_status {
+        if (m->qform == form && m->qld == ld) return MRI_OK;
+        TRY(launch_norm_quant(form, m->x, m->norm_w, m->nstats, rows, d, ld, m->qact, m->qscale,
+                              m->normed, s));
+        m->qform = form;
+        m->qld = ld;
+        return MRI_OK;
+    };
+    switch (w.format) {
+    case MRI_WEIGHT_INT8: {
+        const QMatrixDev &dv = handle_dev(static_cast<const mri_qmatrix *>(w.ptr));
+        if (dv.n_out == 0) return MRI_OK;
+        const bool gemm = rows >= kGemmMinRows;
+        TRY(prepare(gemm ? 0 : 1, dv.kp));
+        if (!gemm) return run_int8(m->qact, rows, m->qscale, 0, 0.0f, dv, out, nullptr, s);
+        void *ws = nullptr;
+        if (const size_t wsb = gemm_ws_bytes(rows, dv)) TRY(gemm_ws_get(s, wsb, &ws));
+        return launch_gemm_int8(m->qact, rows, m->qscale, 0, 0.0f, dv, out, nullptr, ws, s);
+    }
+    case MRI_WEIGHT_Q8_0:
+    case MRI_WEIGHT_Q4_0_W4A8: {
+        const Q8MatrixDev &dv =
+            w.format == MRI_WEIGHT_Q8_0 ? handle_dev(static_cast<const mri_q8_0_matrix *>(w.ptr))
+                                        : handle_dev(static_cast<const mri_q4_0_matrix *>(w.ptr));
+        if (dv.n_out == 0) return MRI_OK;
+        TRY(prepare(2, dv.kp));
+        return run_q8(m->qact, rows, m->qscale, dv, out, nullptr, s);
+    }
+    default:
+        TRY(prepare(3, d));
+        return proj(w, m->normed, rows, out, s);
+    }
+}
+
 // One decode row through the single-row GEMV, with the steps around the
 // projection that it takes over (RowOps): the RMSNorm or SwiGLU that
 // produces its input, a copy of the input row, and the residual add of its
@@ -289,7 +342,8 @@ mri_status block(mri_llama *m, size_t li, size_t rows, size_t start, mri_kv_cach
         return o;
     };
     auto in_proj = [&](const mri_weight_ref &w, const float *norm, float *out) {
-        if (!fold) return proj(w, m->normed, rows, out, s);
+        if (!fold) return m->fuse_norm ? proj_normed(m, w, rows, out, s)
+                                       : proj(w, m->normed, rows, out, s);
         return row_proj(w, xrow, norm_ops(norm), out, s);
     };
     // projections whose output is added to the residual stream
@@ -300,6 +354,12 @@ mri_status block(mri_llama *m, size_t li, size_t rows, size_t start, mri_kv_cach
             return row_proj(w, in, o, m->x, s);
         }
         TRY(proj(w, in, rows, m->tmp, s));
+        if (m->fuse_norm) {
+            m->norm_w = norm;
+            m->qform = -1;
+            return launch_rmsnorm_stats(2, m->x, m->tmp, nullptr, m->x, rows, g.dim, norm, g.eps,
+                                        m->nstats, s);
+        }
         return launch_add_rmsnorm(m->x, m->tmp, rows, g.dim, norm, g.eps, m->normed, s);
     };
     float *kc = c->k + li * c->max_seq * c->kvd, *vc = c->v + li * c->max_seq * c->kvd;
@@ -390,12 +450,21 @@ mri_status run_rows(mri_llama *m, const uint32_t *tok_dev, size_t rows, size_t s
     if (fold && emb == Emb::kHost) x_in = m->embd + (size_t)host_tok * g.dim;
     else if (fold && emb == Emb::kInX) {}
     else if (fold) TRY(launch_embed(m->embd, tok_dev, 1, g.dim, m->x, s));
-    else TRY(launch_embed_rmsnorm(m->embd, tok_dev, rows, g.dim, first, g.eps, m->x, m->normed, s));
+    else if (m->fuse_norm) {
+        m->norm_w = first;
+        m->qform = -1;
+        TRY(launch_rmsnorm_stats(1, m->embd, nullptr, tok_dev, m->x, rows, g.dim, first, g.eps,
+                                 m->nstats, s));
+    } else {
+        TRY(launch_embed_rmsnorm(m->embd, tok_dev, rows, g.dim, first, g.eps, m->x, m->normed, s));
+    }
     for (size_t li = 0; li < g.n_layers; ++li)
         TRY(block(m, li, rows, start, c,
                   li + 1 < g.n_layers ? m->layers[li + 1].attn_norm : m->out_norm, fold,
                   li == 0 ? x_in : m->x, s));
-    if (!fold) return proj(m->output, m->normed, rows, logits, s);
+    if (!fold)
+        return m->fuse_norm ? proj_normed(m, m->output, rows, logits, s)
+                            : proj(m->output, m->normed, rows, logits, s);
     RowOps o;
     o.norm_w = m->out_norm;
     o.eps = g.eps;
@@ -468,9 +537,12 @@ mri_status mri_llama_create(const mri_llama_config *cfg, const float *token_embd
         (st = dalloc_t(m, R * (m->qd + 2 * m->kvd), &m->qkv)) ||
         (st = dalloc_t(m, R * m->qd, &m->attn)) || (st = dalloc_t(m, R * 2 * g.ffn_dim, &m->gu)) ||
         (st = dalloc_t(m, R * g.ffn_dim, &m->act)) || (st = dalloc_t(m, R, &m->tok)) ||
+        (st = dalloc_t(m, 2 * R, &m->nstats)) || (st = dalloc_t(m, R, &m->qscale)) ||
+        (st = dalloc_t(m, round_up(R, 32) * round_up(g.dim, 256), &m->qact)) ||
         (st = dalloc_t(m, R + 1, &m->gen)) ||
         (st = dalloc_t(m, attention_part_floats(g.n_heads, hd, R), &m->attn_part)))
         return fail(st);
+    m->fuse_norm = rmsnorm_stats_supported(g.dim);
     // RopeTable::new (ops/rope.rs): theta_i = 1 / base^(2i / head_dim) and
     // angle = pos * theta_i in f32, with the C library's powf / cosf / sinf.
     const size_t half = hd / 2;

@@ -365,6 +365,113 @@ mri_status launch_quantize_pack(const float *x, size_t m, size_t k, size_t kp,
     return MRI_OK;
 }
 
+namespace {
+
+// ---------------------------------------------------------------------------
+// Quantization of RMS-normalized rows that are not in memory: row r is
+// y = w * (x[r] * rms_inv[r]) (rmsnorm.rs:100-114, the operations of
+// k_rmsnorm), with rms_inv[r] = stats[2r] and max |y| = stats[2r+1] from
+// the statistics pass.  FORM 0: per-tensor scale (quantize_symmetric over
+// all rows, as matmul_int8_from_f32 quantizes its input), GEMM-packed
+// layout, grid over the rows padded to 32 (padding rows are zero); FORM 1:
+// per-tensor, [rows][ld] plain; FORM 2: per-row scales (matmul_q8_0_direct),
+// [rows][ld] chunk-permuted; FORM 3: the normalized f32 rows themselves.
+// The quantized values equal those of quantizing the stored normalized
+// rows: the same y, the same max, the same scale.
+template <int NV, int FORM>
+__global__ __launch_bounds__(kThreads) void k_norm_quant(
+    const float *__restrict__ x, const float *__restrict__ w, const float *__restrict__ stats,
+    int rows, int d, size_t ld, size_t mg, int8_t *__restrict__ q, float *__restrict__ scales,
+    float *__restrict__ normed) {
+    __shared__ float red[kThreads / 64];
+    const int r = blockIdx.x;
+    const int t = threadIdx.x;
+    if (FORM == 0 && r >= rows) {  // padding rows of the packed layout
+        for (size_t kk = 4 * (size_t)t; kk < ld; kk += 4 * kThreads)
+            *reinterpret_cast<int *>(q + gemm_pack_offset(r, kk, mg)) = 0;
+        return;
+    }
+    const float rms_inv = stats[2 * (size_t)r];
+    const float4 *x4 = reinterpret_cast<const float4 *>(x + (size_t)r * d);
+    const float4 *w4 = reinterpret_cast<const float4 *>(w);
+    float4 y[NV];
+#pragma unroll
+    for (int c = 0; c < NV; ++c) {
+        const int i = c * kThreads + t;
+        if (4 * i < d) {
+            const float4 xv = x4[i], wv = w4[i];
+            y[c] = float4{wv.x * (xv.x * rms_inv), wv.y * (xv.y * rms_inv),
+                          wv.z * (xv.z * rms_inv), wv.w * (xv.w * rms_inv)};
+        } else {
+            y[c] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    }
+    if constexpr (FORM == 3) {
+#pragma unroll
+        for (int c = 0; c < NV; ++c) {
+            const int i = c * kThreads + t;
+            if (4 * i < d) reinterpret_cast<float4 *>(normed + (size_t)r * d)[i] = y[c];
+        }
+        return;
+    }
+    float mx;
+    if constexpr (FORM == 2) {
+        mx = stats[2 * (size_t)r + 1];
+    } else {
+        mx = 0.0f;
+        for (int i = t; i < rows; i += kThreads) mx = fmaxf(mx, stats[2 * (size_t)i + 1]);
+        mx = block_max(mx, red);
+    }
+    const float scale = scale_of(mx);
+    const float inv = __fdiv_rn(1.0f, scale);
+    if (t == 0 && (FORM == 2 || r == 0)) scales[FORM == 2 ? r : 0] = scale;
+#pragma unroll
+    for (int c = 0; c < NV; ++c) {
+        const size_t kk = 4 * (size_t)(c * kThreads + t);
+        if (kk < (size_t)d) {
+            const int packed = ((int)round_clamp_i8(y[c].x * inv) & 255) |
+                               (((int)round_clamp_i8(y[c].y * inv) & 255) << 8) |
+                               (((int)round_clamp_i8(y[c].z * inv) & 255) << 16) |
+                               ((int)round_clamp_i8(y[c].w * inv) << 24);
+            const size_t pos = FORM == 0 ? gemm_pack_offset(r, kk, mg)
+                                         : (size_t)r * ld + row_pos(kk, FORM == 2);
+            *reinterpret_cast<int *>(q + pos) = packed;
+        }
+    }
+    for (size_t kk = (size_t)d + 4 * t; kk < ld; kk += 4 * kThreads) {  // zero padding
+        const size_t pos = FORM == 0 ? gemm_pack_offset(r, kk, mg)
+                                     : (size_t)r * ld + row_pos(kk, FORM == 2);
+        *reinterpret_cast<int *>(q + pos) = 0;
+    }
+}
+
+}  // namespace
+
+mri_status launch_norm_quant(int form, const float *x, const float *w, const float *stats,
+                             size_t rows, size_t d, size_t ld, int8_t *q, float *scales,
+                             float *normed, hipStream_t s) {
+    if (!rows) return MRI_OK;
+    if (d % 4 || d > 8192 || (form != 3 && (ld < d || ld % 4)))
+        return set_error(MRI_ERR_INVALID_ARGUMENT, "norm quant: unsupported row shape");
+    const size_t mg = gemm_row_groups(rows);
+    const dim3 g((unsigned)(form == 0 ? mg * 32 : rows)), b(kThreads);
+    auto go = [&](auto nv) {
+        constexpr int NV = decltype(nv)::value;
+        switch (form) {
+        case 0: hipLaunchKernelGGL((k_norm_quant<NV, 0>), g, b, 0, s, x, w, stats, (int)rows, (int)d, ld, mg, q, scales, normed); break;
+        case 1: hipLaunchKernelGGL((k_norm_quant<NV, 1>), g, b, 0, s, x, w, stats, (int)rows, (int)d, ld, mg, q, scales, normed); break;
+        case 2: hipLaunchKernelGGL((k_norm_quant<NV, 2>), g, b, 0, s, x, w, stats, (int)rows, (int)d, ld, mg, q, scales, normed); break;
+        default: hipLaunchKernelGGL((k_norm_quant<NV, 3>), g, b, 0, s, x, w, stats, (int)rows, (int)d, ld, mg, q, scales, normed); break;
+        }
+    };
+    if (d <= 1024) go(std::integral_constant<int, 1>{});
+    else if (d <= 2048) go(std::integral_constant<int, 2>{});
+    else if (d <= 4096) go(std::integral_constant<int, 4>{});
+    else go(std::integral_constant<int, 8>{});
+    MRI_LAUNCHED("k_norm_quant");
+    return MRI_OK;
+}
+
 mri_status launch_pack_gemm(const int8_t *src, size_t m, size_t k, size_t ld, size_t kp,
                             int8_t *packed, hipStream_t s) {
     const size_t mg = gemm_row_groups(m);
