@@ -231,6 +231,17 @@ def bench_w4a8(torch, M, T, n, k, steps, warmup, seed=4):
                      out)[0]
 
 
+def bench_w4a32_handle(torch, M, T, n, k, steps, warmup, seed=6):
+    """matmul_q4_0_dequant (W4A32) on device-resident Q4_0 handles, M = 1."""
+    raws = [q4_raw_device(torch, n, k, seed + i) for i in range(copies_for(n * k // 32 * 18))]
+    ws = [M.Q4Matrix.from_raw_device(r, n, k) for r in raws]
+    del raws
+    x = torch.randn((1, k), device="cuda")
+    out = torch.empty((1, n), device="cuda")
+    return T.best_ms(lambda i: M.matmul_q4_0_dequant_matrix(x, ws[i], out), steps, warmup,
+                     len(ws), out)[0]
+
+
 def bench_int8_decode(torch, M, T, n, k, steps, warmup, seed=5):
     data, scales = int8_weights_device(torch, M, n, k, seed)
     nrot = copies_for(n * k)
@@ -573,6 +584,12 @@ def main():
             "us": round(ms_q4 * 1e3, 2), "GB_s": round(gbs, 1),
             "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
         log(f"q4_0 decode: {ms_q4*1e3:.2f} us {gbs:.0f} GB/s")
+        ms_h = bench_w4a32_handle(torch, M, T, 11008, 4096, steps2, args.warmup)
+        gbs = q4_bytes(1, 11008, 4096) / (ms_h * 1e-3) / 1e9
+        secondary["q4_0_w4a32_handle_decode_1x4096x11008"] = {
+            "us": round(ms_h * 1e3, 2), "GB_s": round(gbs, 1),
+            "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+        log(f"q4_0 W4A32 (device handle) decode: {ms_h*1e3:.2f} us {gbs:.0f} GB/s")
         ms_w4 = bench_w4a8(torch, M, T, 11008, 4096, steps2, args.warmup)
         gbs = q4_bytes(1, 11008, 4096) / (ms_w4 * 1e-3) / 1e9
         secondary["q4_0_w4a8_decode_1x4096x11008"] = {

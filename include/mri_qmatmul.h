@@ -227,6 +227,19 @@ void mri_q4_0_matrix_destroy(mri_q4_0_matrix *w);
  * InvalidShape unless ndim == 2; ShapeMismatch when dims[1] != k_in.
  * Optional outputs (nullable, device):
  * block_dots_out [m, n_out, k_in/32] int32, act_scales_out [m]. */
+/* matmul_q4_0_dequant (src/ops/matmul/q4_0.rs:94-181, W4A32: f32 inputs,
+ * no activation quantization) on a device-resident Q4_0 handle instead of
+ * raw blocks: the weights stay in the handle's 4-bit lap-block layout and
+ * are dequantized in registers by the decode GEMV, up to four rows per
+ * launch.  Same checks as mri_matmul_q4_0_dequant for the input (ndim != 2
+ * -> InvalidShape, dims[1] != k_in -> ShapeMismatch); input rows 16-byte
+ * aligned.  Outputs within 1e-5 * max(|out|, sum_k |x_k w_k|) of the
+ * reference's sequential sum.  MRI_ERR_UNSUPPORTED when four f32 rows of
+ * K do not fit the 64 KiB LDS staging (K > 4096 at four rows, > 16384 at
+ * one). */
+mri_status mri_matmul_q4_0_dequant_matrix(const float *input, const size_t *dims, size_t ndim,
+                                          const mri_q4_0_matrix *w, float *out, void *stream);
+
 mri_status mri_matmul_q4_0_w4a8(const float *input, const size_t *dims, size_t ndim,
                                 const mri_q4_0_matrix *w, float *out,
                                 int32_t *block_dots_out, float *act_scales_out,

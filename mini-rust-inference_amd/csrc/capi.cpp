@@ -872,6 +872,37 @@ mri_status mri_matmul_q4_0_w4a8(const float *input, const size_t *dims, size_t n
                          act_scales_out, stream);
 }
 
+mri_status mri_matmul_q4_0_dequant_matrix(const float *input, const size_t *dims, size_t ndim,
+                                          const mri_q4_0_matrix *w, float *out, void *stream) {
+    if (!w) return set_error(MRI_ERR_INVALID_ARGUMENT, "null weight handle");
+    if (ndim && !dims) return set_error(MRI_ERR_INVALID_ARGUMENT, "dims is null");
+    if (ndim != 2)
+        return set_error(MRI_ERR_INVALID_SHAPE,
+                         fmt("matmul_q4_0_dequant: `input` must be 2-D, got %zuD (shape %s)",
+                             ndim, dims_str(dims, ndim).c_str()));
+    const Q8MatrixDev &d = w->d;
+    const size_t m = dims[0], k_in = dims[1];
+    if (k_in != d.k_in)
+        return set_error(MRI_ERR_SHAPE_MISMATCH,
+                         fmt("ShapeMismatch { expected: [%zu, %zu], got: [%zu, %zu] }", m, d.k_in,
+                             m, k_in));
+    if (m * k_in && !input) return set_error(MRI_ERR_INVALID_ARGUMENT, "input is null");
+    if (m * d.n_out && !out) return set_error(MRI_ERR_INVALID_ARGUMENT, "out is null");
+    if (m == 0 || d.n_out == 0) return MRI_OK;
+    int dev;
+    mri_status st = current_device(&dev);
+    if (st) return st;
+    auto s = static_cast<hipStream_t>(stream);
+    if (k_in == 0) {  // empty sums
+        MRI_HIP(hipMemsetAsync(out, 0, m * d.n_out * sizeof(float), s));
+        return MRI_OK;
+    }
+    if (!aligned(input, 16) || k_in % 4)
+        return set_error(MRI_ERR_INVALID_ARGUMENT,
+                         "matmul_q4_0_dequant (handle): input rows must be 16-byte aligned");
+    return launch_gemv_w4a32(input, m, k_in, d, out, s);
+}
+
 mri_status mri_matmul_q4_0_dequant(const float *input, const size_t *dims, size_t ndim,
                                    const uint8_t *weight_q4, size_t weight_len,
                                    size_t n_out, size_t k, float *out, void *stream) {

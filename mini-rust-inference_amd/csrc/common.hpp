@@ -249,6 +249,11 @@ const QMatrixDev &handle_dev(const mri_qmatrix *h);
 const Q8MatrixDev &handle_dev(const mri_q8_0_matrix *h);
 const Q8MatrixDev &handle_dev(const mri_q4_0_matrix *h);
 bool gemv_q8_supported(bool fused, size_t m, size_t n_tiles, size_t k, size_t kp);
+// W4A32 (matmul_q4_0_dequant semantics) on a Q4_0 lap-block handle (w.w4):
+// x f32 [m][k], 16-byte aligned, k % 4 == 0; MRI_ERR_UNSUPPORTED when the
+// f32 rows of four do not fit the GEMV's LDS staging.
+mri_status launch_gemv_w4a32(const float *x, size_t m, size_t k, const Q8MatrixDev &w,
+                             float *out, hipStream_t st);
 bool gemv_fusable(size_t m, size_t k, const float *x);
 bool row_ops_ok(const float *x, const RowOps &ops);
 mri_status launch_gemv_int8(const float *x, const int8_t *act, size_t m,

@@ -236,6 +236,144 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
 }
 
 
+// ---------------------------------------------------------------------------
+// Q4_0 with f32 activations (W4A32, matmul_q4_0_dequant, q4_0.rs:94-181) on
+// the same 4-bit lap blocks and GEMV skeleton: x is staged in LDS as f32
+// (no quantization), each lane dequantizes its 8 elements of each block in
+// registers (nibble -> signed int -> f32, the reference's (nibble - 8) as
+// the stored nibble is its 4-bit two's complement) and accumulates
+// d_b * sum_i x_i * q_i with FMAs.  Lane groups g = l / 16 hold the four
+// 8-element slices of a block for row 16T + l % 16; after the sweep they
+// are added across lanes (fixed shuffle order) and the S wave sums through
+// LDS in wave order.  The reference adds x_k * w_k sequentially over all k;
+// the result differs only in f32 rounding (within
+// 1e-5 * max(|out|, sum_k |x_k w_k|)).  Word j of lap piece u is block
+// 8q + 4u + j; byte i of a word holds elements 8g + i (low nibble) and
+// 8g + 4 + i (high nibble).
+// ---------------------------------------------------------------------------
+template <int MR, int S, int RL, int XR>
+__global__ __launch_bounds__(S * kWave) void k_gemv_w4a32(
+    const float *__restrict__ x, int M, int K, int kp, const v4i *__restrict__ laps, int N,
+    int n_tiles, int G, int nb, float *__restrict__ out) {
+    extern __shared__ v4i s_lds[];
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int T = blockIdx.x;
+    const int l = threadIdx.x & 63;
+    const int r = l & 15, g = l >> 4;
+    const int nq = w < G ? (G - w + S - 1) / S : 0;  // laps of this wave
+    constexpr size_t LB = kQ4LapBytes / 16;
+    const v4i *wp = laps + (size_t)T * G * LB + l;
+    const v4i *sp = laps + (size_t)T * G * LB + 128 + r;
+    // LDS: x rows [MR][kp] f32 (zero past K), then the wave sums
+    float *s_x = reinterpret_cast<float *>(s_lds);
+    float *sums = s_x + (size_t)MR * kp;
+
+    v4i wr[RL][2];
+    v4i sr[RL];
+    v4i xr[XR];
+    const int k4 = K / 4, kp4 = kp / 4;
+    const int n4 = M * kp4;  // float4s of the staged rows
+#pragma unroll
+    for (int e = 0; e < XR; ++e) {
+        const int i = min((int)threadIdx.x + S * kWave * e, n4 - 1);
+        const int row = i / kp4, c = i - row * kp4;
+        xr[e] = c < k4 ? reinterpret_cast<const v4i *>(x + (size_t)row * K)[c] : v4i{0, 0, 0, 0};
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < RL; ++u) {
+        const int q = min(min(u, max(nq - 1, 0)) * S + w, G - 1);
+        wr[u][0] = __builtin_nontemporal_load(wp + (size_t)q * LB);
+        wr[u][1] = __builtin_nontemporal_load(wp + (size_t)q * LB + 64);
+        sr[u] = sp[(size_t)q * LB];
+    }
+#pragma unroll
+    for (int e = 0; e < XR; ++e) {
+        const int i = (int)threadIdx.x + S * kWave * e;
+        if (i < n4) reinterpret_cast<v4i *>(s_x)[i] = xr[e];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    float acc[MR];
+#pragma unroll
+    for (int j = 0; j < MR; ++j) acc[j] = 0.0f;
+
+    auto lap = [&](int L, auto slot, bool refill) __attribute__((always_inline)) {
+        constexpr int U = decltype(slot)::value;
+        const int q = L * S + w, qn = q + RL * S;
+        const v4i p0 = wr[U][0], p1 = wr[U][1], sc = sr[U];
+        if (refill) {
+            wr[U][0] = __builtin_nontemporal_load(wp + (size_t)qn * LB);
+            wr[U][1] = __builtin_nontemporal_load(wp + (size_t)qn * LB + 64);
+            sr[U] = sp[(size_t)qn * LB];
+        }
+#pragma unroll
+        for (int jb = 0; jb < 8; ++jb) {  // block 8q + jb: word jb % 4 of piece jb / 4
+            const int b = 8 * q + jb;
+            const v4i pc = jb < 4 ? p0 : p1;
+            const int wd = pc[jb & 3];
+            const unsigned sw = (unsigned)sc[jb >> 1];
+            const float d = f16_bits_to_f32((jb & 1) ? (sw >> 16) : (sw & 0xFFFFu));
+            float qv[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                qv[i] = (float)((wd << (28 - 8 * i)) >> 28);      // low nibble of byte i
+                qv[4 + i] = (float)((wd << (24 - 8 * i)) >> 28);  // high nibble
+            }
+#pragma unroll
+            for (int j = 0; j < MR; ++j) {
+                const float4 *xa = reinterpret_cast<const float4 *>(
+                    s_x + (size_t)j * kp + 32 * b + 8 * g);
+                const float4 lo = xa[0], hi = xa[1];
+                float p = lo.x * qv[0];
+                p = fmaf(lo.y, qv[1], p);
+                p = fmaf(lo.z, qv[2], p);
+                p = fmaf(lo.w, qv[3], p);
+                p = fmaf(hi.x, qv[4], p);
+                p = fmaf(hi.y, qv[5], p);
+                p = fmaf(hi.z, qv[6], p);
+                p = fmaf(hi.w, qv[7], p);
+                const float a = fmaf(d, p, acc[j]);
+                acc[j] = b < nb ? a : acc[j];
+            }
+        }
+    };
+    {
+        const int k = nq / RL, rem = nq - k * RL;
+        for (int it = 0; it + 1 < k; ++it)
+            static_for<RL>([&](auto u) { lap(it * RL + u, u, true); });
+        if (k > 0) static_for<RL>([&](auto u) { lap((k - 1) * RL + u, u, u < rem); });
+        static_for<RL>([&](auto u) {
+            if (u < rem) lap(k * RL + u, u, false);
+        });
+    }
+    // lane groups (fixed order), then waves (in order)
+#pragma unroll
+    for (int j = 0; j < MR; ++j) {
+        float v = acc[j] + __shfl_xor(acc[j], 16);
+        acc[j] = v + __shfl_xor(v, 32);
+    }
+    if constexpr (S > 1) {
+        if (w != 0 && l < 16) {
+#pragma unroll
+            for (int j = 0; j < MR; ++j) sums[((w - 1) * MR + j) * 16 + l] = acc[j];
+        }
+        __syncthreads();
+        if (w != 0) return;
+        const int sw_ = min(S, G);
+        for (int ww = 1; ww < sw_; ++ww) {
+#pragma unroll
+            for (int j = 0; j < MR; ++j) acc[j] = acc[j] + sums[((ww - 1) * MR + j) * 16 + r];
+        }
+    }
+    const int n = T * 16 + l;
+    if (l < 16 && n < N) {
+#pragma unroll
+        for (int j = 0; j < MR; ++j)
+            if (j < M) out[(size_t)j * N + n] = acc[j];
+    }
+}
+
 struct CfgQ8 {
     int s = 0, tpw = 1, rl = 1, xr = 0;  // s == 0: unsupported
 };
@@ -310,7 +448,58 @@ void dispatch_q8_dbg(bool dbg, CfgQ8 c, ActIn in, size_t m, const float *sa_rows
     else dispatch_q8<MR, FUSED, false, false>(c, in, m, sa_rows, w, out, nullptr, st);
 }
 
+// W4A32 on 4-bit lap blocks: rows in groups of up to four per launch,
+// four waves per tile from 512 tiles up, else 8 (K <= 4096) or 16.
+template <int MR, int S, int RL, int XR>
+void launch_w4a32_inst(const float *x, size_t m, size_t k, const Q8MatrixDev &w, float *out,
+                       hipStream_t st) {
+    const size_t lds = ((size_t)MR * w.kp + (size_t)(S - 1) * MR * 16) * 4;
+    hipLaunchKernelGGL((k_gemv_w4a32<MR, S, RL, XR>), dim3((unsigned)w.n_tiles), dim3(S * kWave),
+                       lds, st, x, (int)m, (int)k, (int)w.kp, reinterpret_cast<const v4i *>(w.laps),
+                       (int)w.n_out, (int)w.n_tiles, (int)groups_of(w), (int)w.n_blocks, out);
+}
+
+template <int MR>
+bool launch_w4a32_rows(const float *x, size_t m, size_t k, const Q8MatrixDev &w, float *out,
+                       hipStream_t st) {
+    const size_t G = groups_of(w);
+    const int s = w.n_tiles >= 512 ? 4 : G > 16 ? 16 : 8;
+    const size_t n4 = (size_t)MR * w.kp / 4;
+    const size_t per = ceil_div(n4, (size_t)s * kWave);  // float4s per thread
+    if ((size_t)MR * w.kp * 4 > kMaxLds) return false;
+#define MRI_W4A32(S_, RL_, XR_)                                                  \
+    if (s == S_ && per <= XR_) {                                                  \
+        launch_w4a32_inst<MR, S_, RL_, XR_>(x, m, k, w, out, st);                 \
+        return true;                                                             \
+    }
+    MRI_W4A32(4, 1, 4) MRI_W4A32(4, 1, 16)
+    MRI_W4A32(8, 2, 2) MRI_W4A32(8, 2, 8)
+    MRI_W4A32(16, 2, 1) MRI_W4A32(16, 2, 4)
+#undef MRI_W4A32
+    return false;
+}
+
 }  // namespace
+
+// W4A32 matmul on a device-resident Q4_0 handle (x f32 [m][k], 16-byte
+// aligned rows, k % 4 == 0): four rows per launch.
+mri_status launch_gemv_w4a32(const float *x, size_t m, size_t k, const Q8MatrixDev &w,
+                             float *out, hipStream_t st) {
+    if (w.n_tiles == 0 || m == 0) return MRI_OK;
+    if (!w.w4 || k != w.k_in || k % 4 || (reinterpret_cast<uintptr_t>(x) & 15))
+        return set_error(MRI_ERR_INVALID_ARGUMENT, "w4a32: unsupported input");
+    for (size_t m0 = 0; m0 < m; m0 += 4) {
+        const size_t mc = std::min<size_t>(4, m - m0);
+        const float *xs = x + m0 * k;
+        float *os = out + m0 * w.n_out;
+        const bool ok = mc == 1   ? launch_w4a32_rows<1>(xs, mc, k, w, os, st)
+                        : mc == 2 ? launch_w4a32_rows<2>(xs, mc, k, w, os, st)
+                                  : launch_w4a32_rows<4>(xs, mc, k, w, os, st);
+        if (!ok) return set_error(MRI_ERR_UNSUPPORTED, "w4a32: K too large for the LDS staging");
+        MRI_LAUNCHED("k_gemv_w4a32");
+    }
+    return MRI_OK;
+}
 
 bool gemv_q8_supported(bool fused, size_t m, size_t n_tiles, size_t k, size_t kp) {
     const size_t G = kp / kQ8LapK;

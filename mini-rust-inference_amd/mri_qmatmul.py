@@ -55,6 +55,7 @@ _SIGS = {
     "mri_matmul_int8_from_f32": ([P, P, SZ, P, P, P, P, P, P], ST),
     "mri_matmul_q8_0_direct": ([P, P, SZ, P, P, P, P, P], ST),
     "mri_matmul_q8_0_direct_noalloc": ([P, P, SZ, P, P, P, P, P], ST),
+    "mri_matmul_q4_0_dequant_matrix": ([P, P, SZ, P, P, P], ST),
     "mri_matmul_q4_0_dequant": ([P, P, SZ, P, SZ, SZ, SZ, P, P], ST),
     "mri_q4_0_matrix_from_raw_bytes": ([P, SZ, SZ, SZ, C.c_int, C.POINTER(P)], ST),
     "mri_q4_0_matrix_from_raw_device": ([P, SZ, SZ, SZ, C.c_int, P, C.POINTER(P)], ST),
@@ -329,6 +330,13 @@ def matmul_q8_0_direct_noalloc(x, w: Q8Matrix, out, block_dots_out=None, act_sca
 
 
 NOALLOC_SCRATCH_BYTES = 4 << 20  # MRI_NOALLOC_SCRATCH_BYTES
+
+
+def matmul_q4_0_dequant_matrix(x, w: "Q4Matrix", out, stream=None, shape=None):
+    """matmul_q4_0_dequant (W4A32) on a device-resident Q4_0 handle."""
+    dims, nd = _dims(tuple(x.shape) if shape is None else shape)
+    check(lib().mri_matmul_q4_0_dequant_matrix(_ptr(x), dims, nd, w.h, _ptr(out),
+                                               _stream(stream)))
 
 
 def matmul_q4_0_w4a8(x, w: Q4Matrix, out, block_dots_out=None, act_scales_out=None,

@@ -337,6 +337,49 @@ def test_matmul_q4_0_dequant_ggml_order(m, n, k):
     assert e.value.kind == "InvalidArgument"
 
 
+@pytest.mark.parametrize("m,n,k", [(1, 11008, 4096), (1, 4096, 11008), (1, 32000, 4096),
+                                   (2, 300, 256), (3, 64, 4096), (4, 48, 4096), (5, 40, 512),
+                                   (9, 33, 1024), (1, 16, 32), (1, 50, 96), (1, 1000, 16384)])
+@pytest.mark.parametrize("order", [0, 1])
+def test_matmul_q4_0_dequant_matrix(m, n, k, order):
+    """W4A32 (matmul_q4_0_dequant semantics) on the device-resident 4-bit
+    lap blocks of a Q4_0 handle, uploaded from either nibble order: within
+    1e-5 * max(|ref|, sum_k |x_k w_k|) of the oracle's sequential sum."""
+    say(f"matmul_q4_0_dequant_matrix m={m} n={n} k={k} order={order}")
+    t = torch()
+    rng = np.random.default_rng(m * 7 + n + k + 11 * order)
+    raw = synth_q4_0(rng, n, k)
+    x = rng.standard_normal((m, k)).astype(F32)
+    out0 = O.matmul_q4_0_dequant(x, raw, n, k)
+    up = CF.q4_0_interleaved_to_ggml(raw) if order else raw
+    w = mri().Q4Matrix.from_raw_bytes(up, n, k, order)
+    out = empty((m, n), t.float32)
+    mri().matmul_q4_0_dequant_matrix(dev(x), w, out)
+    got = host(out)
+    scale = np.maximum(np.abs(out0), CF.q4_0_terms_abs_sum(x, raw, n, k))
+    err = np.abs(got.astype(np.float64) - out0)
+    assert np.all(err <= 1e-5 * scale), float(np.max(err / scale))
+
+
+def test_matmul_q4_0_dequant_matrix_errors():
+    t = torch()
+    M = mri()
+    rng = np.random.default_rng(2)
+    w = M.Q4Matrix.from_raw_bytes(synth_q4_0(rng, 16, 64), 16, 64)
+    out = empty((2, 16), t.float32)
+    with pytest.raises(M.MriError) as e:
+        M.matmul_q4_0_dequant_matrix(dev(np.zeros((2, 32), F32)), w, out)
+    assert e.value.kind == "ShapeMismatch"
+    with pytest.raises(M.MriError) as e:
+        M.matmul_q4_0_dequant_matrix(dev(np.zeros((2, 64), F32)), w, out, shape=(2, 8, 8))
+    assert e.value.kind == "InvalidShape"
+    big = M.Q4Matrix.from_raw_bytes(synth_q4_0(rng, 16, 11008), 16, 11008)
+    x = dev(np.zeros((4, 11008), F32))
+    with pytest.raises(M.MriError) as e:  # four f32 rows of K = 11008 exceed the staging
+        M.matmul_q4_0_dequant_matrix(x, big, empty((4, 16), t.float32))
+    assert e.value.kind == "Unsupported"
+
+
 # ---- error behaviour (TensorError kinds and order) ------------------------------------
 
 def test_errors():
