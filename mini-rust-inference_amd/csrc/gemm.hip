@@ -93,12 +93,25 @@ __device__ inline void wait_barrier() {
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(N) : "memory");
 }
 
+constexpr int kBufWord3 = 0x00020000;  // raw buffer resource, dword 3 (gfx950)
+constexpr int kScDevice = 16;          // cache policy sc1: device scope
+constexpr int kWaitVm0 = 0x0F70;       // s_waitcnt vmcnt(0), others untouched
+
+// Whole output tiles, optionally split along K (ks > 1): the ks
+// contributors of a tile each run a contiguous, balanced range of its K
+// steps, store their int32 partial tile to a workspace slot (device-scope
+// sc1 stores) and count themselves on the tile's counter; the one that
+// counts last adds the other partials to its own (exact: int32 addition
+// wraps and is associative, as the reference's i32 sums), applies the f32
+// epilogue and resets the counter to zero for the next call.  No workgroup
+// waits for another.  Splitting K puts more workgroups, and more loads in
+// flight, on products whose tiles alone would leave most CUs idle.
 template <int BM, int BN, int WM, int WN, int NSA, int NSB>
 __global__ __launch_bounds__(WM * WN * kWave) void k_gemm_int8(
     const int8_t *__restrict__ act, int mg, const float *__restrict__ sa_ptr, int sa_stride,
     float sa_value, const int8_t *__restrict__ tiles, const float *__restrict__ wscales,
     int M, int N, int n_tiles, int P, int n_mt, int n_tiles_total, float *__restrict__ out,
-    int32_t *__restrict__ acc_out) {
+    int32_t *__restrict__ acc_out, int ks, int32_t *__restrict__ ws, int *__restrict__ cnt) {
     constexpr int NW = WM * WN;                // waves
     constexpr int FA = BM / 32 * 2, FB = BN / 32 * 2;  // fragments per K step (2 k halves)
     constexpr int TM = BM / WM / 32, TN = BN / WN / 32;  // MFMA tiles per wave
@@ -116,11 +129,18 @@ __global__ __launch_bounds__(WM * WN * kWave) void k_gemm_int8(
     constexpr int WAIT0 = WAIT + LA + LB;
     constexpr int NMX = NSA > NSB ? NSA : NSB;
     extern __shared__ v4i s_buf[];
+    __shared__ int s_last;
 
-    // XCD-aware tile index: this workgroup runs on XCD blockIdx % 8.
+    // XCD-aware work index: this workgroup runs on XCD blockIdx % 8, and the
+    // contributors of one tile (adjacent items) on the same XCD.
     const int per_xcd = (int)(gridDim.x / kXcds);
-    const int tile = (int)(blockIdx.x % kXcds) * per_xcd + (int)(blockIdx.x / kXcds);
+    const int item = (int)(blockIdx.x % kXcds) * per_xcd + (int)(blockIdx.x / kXcds);
+    const int tile = item / ks, sp = item - tile * ks;
     if (tile >= n_tiles_total) return;
+    // K steps p0 .. p0 + PS - 1 of the tile (ks <= P, so PS >= 1)
+    const int kq = P / ks, kr = P - kq * ks;
+    const int p0 = sp * kq + min(sp, kr);
+    const int PS = kq + (sp < kr ? 1 : 0);
     const int mt = tile % n_mt, nt = tile / n_mt;
     const int m0 = mt * BM, T0 = nt * (BN / 16);  // first row, first 16-row weight tile
 
@@ -154,18 +174,20 @@ __global__ __launch_bounds__(WM * WN * kWave) void k_gemm_int8(
     const size_t a_pitch = (size_t)mg * 2 * 1024;   // bytes per K step
     const size_t b_pitch = (size_t)n_tiles * 1024;  // bytes per K slab
 
-    // Step indices are clamped to P - 1: the loads past the end re-read the
-    // last step (cached) into buffers no later step reads, which keeps the
-    // number of loads per step, and so every wait count, constant.
+    // Steps p count from the range's first; their indices are clamped to
+    // PS - 1: the loads past the end re-read the last step (cached) into
+    // buffers no later step reads, which keeps the number of loads per step,
+    // and so every wait count, constant.
+    auto kstep = [&](int p) __attribute__((always_inline)) { return p0 + min(p, PS - 1); };
     auto issue_a = [&](int p) __attribute__((always_inline)) {
         const unsigned st = ldsA + (unsigned)((p % NSA) * SA);
-        const size_t off = (size_t)min(p, P - 1) * a_pitch;
+        const size_t off = (size_t)kstep(p) * a_pitch;
 #pragma unroll
         for (int j = 0; j < LA; ++j) dma16(a_src[j] + off, st + (wv + NW * j) * 1024);
     };
     auto issue_b = [&](int p) __attribute__((always_inline)) {
         const unsigned st = ldsB + (unsigned)((p % NSB) * SB);
-        const size_t off = (size_t)min(p, P - 1) * b_pitch;
+        const size_t off = (size_t)kstep(p) * b_pitch;
 #pragma unroll
         for (int j = 0; j < LB; ++j) dma16_nt(b_src[j] + off, st + (wv + NW * j) * 1024);
     };
@@ -226,13 +248,62 @@ __global__ __launch_bounds__(WM * WN * kWave) void k_gemm_int8(
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
     int p = 0;
-    for (; p + 1 < P; p += 2) {
+    for (; p + 1 < PS; p += 2) {
         step(p, S0{}, S1{});
         step(p + 1, S1{}, S0{});
     }
-    if (p < P) step(p, S0{}, S1{});
+    if (p < PS) step(p, S0{}, S1{});
     // no load may still be writing LDS when the workgroup ends
     asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+
+    if (ks > 1) {
+        // Partial slot `item`: [wave][accumulator a][register group q][lane]
+        // x 16 bytes, so each store and load is 1 KiB contiguous per wave.
+        const __amdgpu_buffer_rsrc_t ws_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            ws, 0, (int)min((long long)n_tiles_total * ks * BM * BN * 4, 0x7fffffffLL), kBufWord3);
+        auto slot_off = [&](int c) {
+            return (int)((((size_t)c * NW + wv) * (TM * TN * 4) * kWave + l) * 16);
+        };
+        const int mine = slot_off(item);
+#pragma unroll
+        for (int a = 0; a < TM * TN; ++a)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    v4i{acc[a / TN][a % TN][4 * q], acc[a / TN][a % TN][4 * q + 1],
+                        acc[a / TN][a % TN][4 * q + 2], acc[a / TN][a % TN][4 * q + 3]},
+                    ws_rsrc, mine + (a * 4 + q) * kWave * 16, 0, kScDevice);
+        // The partial is at the device's point of coherence (sc1 stores,
+        // complete at vmcnt(0)) before any wave passes the barrier and the
+        // count; the last contributor reads the partials with sc1 loads,
+        // which do not hit lines its XCD's L2 cached before.
+        __builtin_amdgcn_s_waitcnt(kWaitVm0);
+        __syncthreads();
+        if (t == 0)
+            s_last = __hip_atomic_fetch_add(&cnt[tile], 1, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT) == ks - 1;
+        __syncthreads();
+        if (!s_last) return;
+        for (int c = tile * ks; c < tile * ks + ks; ++c) {
+            if (c == item) continue;
+            const int off = slot_off(c);
+            v4i u[TM * TN][4];
+#pragma unroll
+            for (int a = 0; a < TM * TN; ++a)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    u[a][q] = __builtin_amdgcn_raw_buffer_load_b128(
+                        ws_rsrc, off + (a * 4 + q) * kWave * 16, 0, kScDevice);
+#pragma unroll
+            for (int a = 0; a < TM * TN; ++a)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[a / TN][a % TN][4 * q + e] += u[a][q][e];
+        }
+        if (t == 0)  // ready for the next call on this stream
+            __hip_atomic_store(&cnt[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 
     // epilogue: lane l, register r of tile (i, j) holds row
     // m0 + 32*(wm*TM + i) + 8*(r/4) + 4*(l/32) + r%4 and column
@@ -336,9 +407,6 @@ constexpr size_t gemm_lds_bytes() {
 constexpr int kSkNs = 4;                        // ring stages
 constexpr int kSkTileInts = 256 * 256;          // int32 of one partial tile
 constexpr int kSkMaxTiles = 65536;              // tile counters at the workspace start
-constexpr int kBufWord3 = 0x00020000;           // raw buffer resource, dword 3 (gfx950)
-constexpr int kScDevice = 16;                   // cache policy sc1: device scope
-constexpr int kWaitVm0 = 0x0F70;                // s_waitcnt vmcnt(0), others untouched
 
 // Split of `iters` iterations into nwg ranges: q = iters / nwg each, the
 // first rem = iters % nwg ranges one more.  Neither query divides by more
@@ -706,10 +774,12 @@ __global__ __launch_bounds__(512) void k_gemm_sk(
     asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
 }
 
+// ks > 1: K split in ks ranges per tile, with ws the stream-K workspace
+// (tile counters first, then the partial slots).
 template <int BM, int BN, int WM, int WN, int NSA, int NSB>
 mri_status launch(const int8_t *act_packed, size_t m, const float *sa_ptr, int sa_stride,
                   float sa_value, const QMatrixDev &w, float *out, int32_t *acc_out,
-                  hipStream_t s) {
+                  hipStream_t s, int ks = 1, void *ws = nullptr) {
     constexpr size_t lds = gemm_lds_bytes<BM, BN, NSA, NSB>();
     static DeviceOnce attr;  // the attribute belongs to the function
     MRI_HIP(attr.run([&](int) {
@@ -720,12 +790,16 @@ mri_status launch(const int8_t *act_packed, size_t m, const float *sa_ptr, int s
     const size_t n_mt = (m + BM - 1) / BM;
     const size_t n_nt = (w.n_tiles + BN / 16 - 1) / (BN / 16);
     const size_t total = n_mt * n_nt;
-    const size_t grid = (total + kXcds - 1) / kXcds * kXcds;
+    if (ks < 1 || (size_t)ks > w.kp / kChunkK || (ks > 1 && !ws))
+        return set_error(MRI_ERR_INVALID_ARGUMENT, "gemm: bad K split");
+    const size_t grid = (total * ks + kXcds - 1) / kXcds * kXcds;
+    int *cnt = static_cast<int *>(ws);
+    int32_t *part = ws ? reinterpret_cast<int32_t *>(cnt + kSkMaxTiles) : nullptr;
     hipLaunchKernelGGL((k_gemm_int8<BM, BN, WM, WN, NSA, NSB>), dim3((unsigned)grid),
                        dim3(WM * WN * kWave), lds, s, act_packed, (int)gemm_row_groups(m),
                        sa_ptr, sa_stride, sa_value, w.tiles, w.scales, (int)m, (int)w.n_out,
                        (int)w.n_tiles, (int)(w.kp / kChunkK), (int)n_mt, (int)total, out,
-                       acc_out);
+                       acc_out, ks, part, cnt);
     return MRI_OK;
 }
 
@@ -775,52 +849,133 @@ mri_status launch_sk(const int8_t *act_packed, size_t m, const float *sa_ptr, in
     return MRI_OK;
 }
 
-}  // namespace
+// Kernel plan of an m-row product.  Measured on MI355X (random int8
+// operands, K = 4096 and 11008, M = 64 .. 1024, N = 4096 and 11008): the K
+// loop of every tile shape is bound by the CU's LDS port (DMA writes plus
+// each wave's fragment reads) more than by HBM or MFMA, so the shape that
+// keeps the most CUs busy in one pass wins, and a K split pays for its
+// partial tiles only while it adds CUs.
+//  - 128 x 64 tiles when at most one per CU and either one M tile (M <= 128)
+//    or at least half the CUs: 128 x 4096 x 4096 in 11.8 us with a 4-way K
+//    split (24.8 us as 128 x 128 tiles), 512 x 4096 x 4096 in 18.1 us;
+//  - 128 x 128 tiles when they fit one pass: 1024 x 4096 x 4096 in 26.2 us
+//    (36.3 us as stream-K), 256 x 11008 x 4096 in 24.4 us;
+//  - else 256 x 128 whole tiles or stream-K, by how well whole tiles fill
+//    the CUs.
+// A K split is at most 4-way, keeps at least 16 K steps per contributor
+// and at most one workgroup per CU.
+enum class GemmKind { T128x64, T128x128, T256x128, SK128, SK256 };
+struct GemmPlan {
+    GemmKind kind = GemmKind::T256x128;
+    int ks = 1;
+    SkShape sk;
+    size_t tiles = 0;  // whole tiles of the T kinds
+};
 
-size_t gemm_ws_bytes(size_t m, const QMatrixDev &w) {
-    // the narrower tiles have the more tiles; both widths have the same grid
-    const SkShape sh = sk_shape(m, w, 128);
-    if (sh.nwg == 0) return 0;
-    // [tile counters, fixed place and size][partial tiles: 2 slots per workgroup]
-    return (size_t)kSkMaxTiles * sizeof(int) + (size_t)sh.nwg * 2 * kSkTileInts * sizeof(int32_t);
+GemmPlan plan_gemm(size_t m, const QMatrixDev &w) {
+    GemmPlan pl;
+    const size_t cus = (size_t)std::max(device_cus(), 0);
+    const size_t P = w.kp / kChunkK;
+    const size_t mt128 = (m + 127) / 128;
+    const size_t t64 = mt128 * ((w.n_tiles + 3) / 4), t128 = mt128 * ((w.n_tiles + 7) / 8);
+    auto split = [&](size_t tiles) {
+        const size_t ks = std::min<size_t>({cus / tiles, 4, P / 16});
+        return (int)std::max<size_t>(ks, 1);
+    };
+    if (cus > 0 && t64 <= cus && (mt128 == 1 || 2 * t64 >= cus)) {
+        pl.kind = GemmKind::T128x64;
+        pl.tiles = t64;
+        pl.ks = split(t64);
+        return pl;
+    }
+    if (cus > 0 && t128 <= cus) {
+        pl.kind = GemmKind::T128x128;
+        pl.tiles = t128;
+        pl.ks = split(t128);
+        return pl;
+    }
+    // Stream-K pays for split tiles (partials through memory) and for rows
+    // padded to 256; whole tiles pay for idle CUs.  Whole tiles win when
+    // they fill 60-100% of one pass; stream-K wins otherwise, with 256 x 256
+    // tiles only when they come in whole passes (no split tile).
+    const size_t big = ((m + 255) / 256) * ((w.n_tiles + 7) / 8);
+    pl.kind = GemmKind::T256x128;
+    pl.tiles = big;
+    const SkShape sh4 = sk_shape(m, w, 256), sh2 = sk_shape(m, w, 128);
+    if (sh2.nwg > 0) {
+        const double fill = (double)big / sh2.nwg;
+        if (!(fill <= 1.0 && fill >= 0.6)) {
+            if (sh4.nwg > 0 && sh4.n_tt >= sh4.nwg && sh4.n_tt % sh4.nwg == 0) {
+                pl.kind = GemmKind::SK256;
+                pl.sk = sh4;
+            } else {
+                pl.kind = GemmKind::SK128;
+                pl.sk = sh2;
+            }
+        }
+    }
+    return pl;
 }
 
+size_t plan_ws_bytes(const GemmPlan &pl) {
+    switch (pl.kind) {
+        case GemmKind::SK128:
+        case GemmKind::SK256:
+            // [tile counters, fixed place and size][partial tiles: 2 slots per workgroup]
+            return (size_t)kSkMaxTiles * sizeof(int) +
+                   (size_t)pl.sk.nwg * 2 * kSkTileInts * sizeof(int32_t);
+        case GemmKind::T128x64:
+        case GemmKind::T128x128:
+            if (pl.ks > 1) {
+                const size_t tile = pl.kind == GemmKind::T128x64 ? 128 * 64 : 128 * 128;
+                return (size_t)kSkMaxTiles * sizeof(int) +
+                       pl.tiles * (size_t)pl.ks * tile * sizeof(int32_t);
+            }
+            return 0;
+        default:
+            return 0;
+    }
+}
+
+}  // namespace
+
+size_t gemm_ws_bytes(size_t m, const QMatrixDev &w) { return plan_ws_bytes(plan_gemm(m, w)); }
+
 // act_packed: activations in the GEMM fragment layout (gemm_pack_bytes).
-// ws: gemm_ws_bytes(m, w) bytes; its first kSkMaxTiles ints (the tile
-// counters, at the same place for every shape) were zeroed when it was
-// allocated, and every call leaves them zero again.
+// ws: gemm_ws_bytes(m, w) bytes (may be null when that is 0); its first
+// kSkMaxTiles ints (the tile counters, at the same place for every shape)
+// were zeroed when it was allocated, and every call leaves them zero again.
+// Without a workspace the plan falls back to whole tiles and no K split.
 mri_status launch_gemm_int8(const int8_t *act_packed, size_t m, const float *sa_ptr,
                             int sa_stride, float sa_value, const QMatrixDev &w,
                             float *out, int32_t *acc_out, void *ws, hipStream_t s) {
     if (w.n_tiles == 0 || m == 0) return MRI_OK;
-    // Whole-tile kernel: 256 x 128 tiles when they still give at least half
-    // as many workgroups as CUs, else 128 x 128.
-    const size_t big = ((m + 255) / 256) * ((w.n_tiles + 7) / 8);
-    const size_t tiles_dp = big >= 128 ? big : ((m + 127) / 128) * ((w.n_tiles + 7) / 8);
-    // Stream-K pays for split tiles (partials through memory) and for rows
-    // padded to 256; whole tiles pay for idle CUs.  Measured on MI355X
-    // (K = 4096 and 11008, random int8 operands): whole tiles win when they
-    // fill 60-100% of one wave, or a third of it at M = 128, where half of
-    // stream-K's rows are padding; stream-K wins otherwise, with 256 x 256
-    // tiles only when they come in whole waves (no split tile).
-    const SkShape sh4 = sk_shape(m, w, 256), sh2 = sk_shape(m, w, 128);
-    if (ws && sh2.nwg > 0) {
-        const double fill = (double)tiles_dp / sh2.nwg;
-        const double row_eff = (double)m / ((double)sh2.n_mt * 256);
-        const bool dp = fill <= 1.0 && (fill >= 0.6 || fill >= 0.65 * row_eff);
-        if (!dp) {
-            if (sh4.nwg > 0 && sh4.n_tt >= sh4.nwg && sh4.n_tt % sh4.nwg == 0)
-                return launch_sk<4>(act_packed, m, sa_ptr, sa_stride, sa_value, w, out, acc_out,
-                                    ws, sh4, s);
-            return launch_sk<2>(act_packed, m, sa_ptr, sa_stride, sa_value, w, out, acc_out, ws,
-                                sh2, s);
-        }
+    GemmPlan pl = plan_gemm(m, w);
+    if (!ws) {
+        pl.ks = 1;
+        if (pl.kind == GemmKind::SK128 || pl.kind == GemmKind::SK256) pl.kind = GemmKind::T256x128;
     }
-    mri_status st =
-        big >= 128 ? launch<256, 128, 4, 2, 4, 8>(act_packed, m, sa_ptr, sa_stride, sa_value, w,
-                                                  out, acc_out, s)
-                   : launch<128, 128, 2, 2, 4, 8>(act_packed, m, sa_ptr, sa_stride, sa_value, w,
-                                                  out, acc_out, s);
+    mri_status st = MRI_OK;
+    switch (pl.kind) {
+        case GemmKind::SK256:
+            return launch_sk<4>(act_packed, m, sa_ptr, sa_stride, sa_value, w, out, acc_out, ws,
+                                pl.sk, s);
+        case GemmKind::SK128:
+            return launch_sk<2>(act_packed, m, sa_ptr, sa_stride, sa_value, w, out, acc_out, ws,
+                                pl.sk, s);
+        case GemmKind::T128x64:
+            st = launch<128, 64, 4, 1, 8, 8>(act_packed, m, sa_ptr, sa_stride, sa_value, w, out,
+                                             acc_out, s, pl.ks, ws);
+            break;
+        case GemmKind::T128x128:
+            st = launch<128, 128, 2, 2, 8, 8>(act_packed, m, sa_ptr, sa_stride, sa_value, w, out,
+                                              acc_out, s, pl.ks, ws);
+            break;
+        default:
+            st = launch<256, 128, 4, 2, 4, 8>(act_packed, m, sa_ptr, sa_stride, sa_value, w, out,
+                                              acc_out, s);
+            break;
+    }
     if (st) return st;
     MRI_LAUNCHED("k_gemm_int8");
     return MRI_OK;
