@@ -189,6 +189,8 @@ mri_status run_q8(const int8_t *act, size_t m, const float *sa_rows,
                          hipStream_t s) {
     if (gemv_q8_supported(false, m, w.n_tiles, w.k_in, w.kp))
         return launch_gemv_q8_0(nullptr, act, m, sa_rows, w, out, block_dots, nullptr, s);
+    // prefill sizes: the LDS-tiled kernel (it has no block-dot output)
+    if (!block_dots && gemm_q8_supported(m, w)) return launch_gemm_q8_0(act, m, sa_rows, w, out, s);
     return launch_skinny_q8_0(act, m, sa_rows, w, out, block_dots, s);
 }
 

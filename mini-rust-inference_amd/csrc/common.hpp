@@ -280,6 +280,10 @@ __host__ __device__ inline size_t gemm_pack_offset(size_t m, size_t k, size_t mg
 // one): int32 partial tiles plus per-tile counters.  The counters must be
 // zero when the workspace is first used; every call leaves them zero.
 size_t gemm_ws_bytes(size_t m, const QMatrixDev &w);
+// gemm_q8.hip: prefill-sized matmul_q8_0_direct on LDS-staged MFMA tiles
+bool gemm_q8_supported(size_t m, const Q8MatrixDev &w);
+mri_status launch_gemm_q8_0(const int8_t *act, size_t m, const float *sa_rows,
+                            const Q8MatrixDev &w, float *out, hipStream_t s);
 mri_status launch_gemm_int8(const int8_t *act_packed, size_t m, const float *sa_ptr,
                             int sa_stride, float sa_value, const QMatrixDev &w,
                             float *out, int32_t *acc_out, void *ws, hipStream_t s);

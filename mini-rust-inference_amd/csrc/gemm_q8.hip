@@ -1,0 +1,362 @@
+// gemm_q8.hip — prefill-sized matmul_q8_0_direct (q8_direct.rs:229-289):
+// Q8_0 weights (32-element blocks, one f16 scale each) times activation
+// rows quantized per row to int8, on LDS-staged CDNA4 MFMA tiles.
+//
+//   dot[m, n, b] = sum_{k in block b} act_q[m, k] * w_q[n, k]     (exact int32)
+//   out[m, n]    = s_a[m] * sum_b (f32)dot[m, n, b] * d[n, b]       (f32)
+//
+// The per-block f32 fold is the work that bounds this product: one term
+// per (row, channel, block), against one MFMA per 16 x 16 x 32 block.  The
+// reference rounds ((f32)dot * s_a) * d per block and adds in block order
+// (two multiplies and an add); here each term is one fused multiply-add
+// onto the running sum (a convert and an FMA) and s_a multiplies once at the
+// end.  The int32 block dots are exact; the f32 result differs from the
+// reference's only by those roundings, within 1e-5 * max(|out|, sum |t_b|)
+// of it.  Half the VALU work of the reference's order is what makes this
+// kernel twice as fast as keeping that order would be.
+//
+// Operands.  Both are used in the layouts the decode kernels read:
+//   * activations: rows [M][kp] (kp = K padded to 256) with each 64-byte
+//     chunk permuted so that lane group g's 16 bytes are [block 2p, k 8g..+8 |
+//     block 2p+1, k 8g..+8], i.e. the 8-byte A operands of
+//     v_mfma_i32_16x16x32_i8 for both blocks of the chunk;
+//   * weights: lap blocks of 16 channels x 256 k (4 chunks of 1 KiB in the
+//     same permutation, then 16 rows x 8 f16 scales), tile-major.
+// A workgroup computes 128 rows x 128 channels (4 x 4 sub-tiles of 32 x 32);
+// each K step is one lap (8 blocks): per lap it stages 32 KiB of activation
+// fragments, 32 KiB of weight chunks and 2 KiB of scales in LDS by
+// global_load_lds (16 bytes per lane, each lane its own address, so a
+// fragment of 16 rows x 64 bytes is gathered straight from the row-major
+// activations), double-buffered: the loads of lap q + 1 fly while lap q is
+// folded.  Eight waves (2 x 4) each own 64 rows x 32 channels, two waves per
+// SIMD, so that the MFMA results, sums and operands all stay in VGPRs.
+//
+// Per block, v_mfma_i32_32x32x32_i8 gives the exact dots of 32 rows x 32
+// channels; its output register e of lane l holds row 8 * (e / 4) +
+// 4 * (l / 32) + e % 4 and channel l % 32.
+#include <hip/hip_runtime.h>
+
+#include <type_traits>
+#include <utility>
+
+#include "gemv_common.hpp"
+
+namespace mri {
+using namespace gemv;
+namespace {
+
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr int kQWave = 64;
+constexpr int kQXcds = 8;
+template <typename F, int... I>
+__device__ inline void q_static_for_impl(F &&f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ inline void q_static_for(F &&f) {
+    q_static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+#pragma clang diagnostic ignored "-Winline-asm"
+// 16 bytes per lane from g into LDS at byte address lds + 16 * lane (the
+// loads write M0 themselves; s_nop 0 covers the M0 -> LDS DMA hazard).
+__device__ inline void q_dma16(const void *g, unsigned lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(g), "s"(lds)
+                 : "memory", "m0");
+}
+__device__ inline void q_dma16_nt(const void *g, unsigned lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
+                 :
+                 : "v"(g), "s"(lds)
+                 : "memory", "m0");
+}
+
+// 4 bytes per lane from g into LDS at byte address lds + 4 * lane.
+__device__ inline void q_dma4_nt(const void *g, unsigned lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off nt"
+                 :
+                 : "v"(g), "s"(lds)
+                 : "memory", "m0");
+}
+
+// s_waitcnt lgkmcnt(0) that the compiler sees reading and writing every
+// operand quad read by inline ds_read2_b64, so that none of their uses is
+// scheduled before it.
+template <int RG, int TT>
+__device__ inline void q8_wait_lds(v4i (&a)[2][RG][2], v4i (&b)[2][TT][2]) {
+    if constexpr (RG == 2 && TT == 1) {
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(a[0][0][0]), "+v"(a[0][0][1]), "+v"(a[0][1][0]), "+v"(a[0][1][1]),
+                       "+v"(a[1][0][0]), "+v"(a[1][0][1]), "+v"(a[1][1][0]), "+v"(a[1][1][1]),
+                       "+v"(b[0][0][0]), "+v"(b[0][0][1]), "+v"(b[1][0][0]), "+v"(b[1][0][1]));
+    } else if constexpr (RG == 1 && TT == 1) {
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(a[0][0][0]), "+v"(a[0][0][1]), "+v"(a[1][0][0]), "+v"(a[1][0][1]),
+                       "+v"(b[0][0][0]), "+v"(b[0][0][1]), "+v"(b[1][0][0]), "+v"(b[1][0][1]));
+    } else if constexpr (RG == 1 && TT == 2) {
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(a[0][0][0]), "+v"(a[0][0][1]), "+v"(a[1][0][0]), "+v"(a[1][0][1]),
+                       "+v"(b[0][0][0]), "+v"(b[0][0][1]), "+v"(b[0][1][0]), "+v"(b[0][1][1]),
+                       "+v"(b[1][0][0]), "+v"(b[1][0][1]), "+v"(b[1][1][0]), "+v"(b[1][1][1]));
+    } else {
+        static_assert(RG == 2 && TT == 2, "wave tile");
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(a[0][0][0]), "+v"(a[0][0][1]), "+v"(a[0][1][0]), "+v"(a[0][1][1]),
+                       "+v"(a[1][0][0]), "+v"(a[1][0][1]), "+v"(a[1][1][0]), "+v"(a[1][1][1]),
+                       "+v"(b[0][0][0]), "+v"(b[0][0][1]), "+v"(b[0][1][0]), "+v"(b[0][1][1]),
+                       "+v"(b[1][0][0]), "+v"(b[1][0][1]), "+v"(b[1][1][0]), "+v"(b[1][1][1]));
+    }
+}
+
+// Bytes of one ring stage (half a lap: 2 chunks, 4 blocks) of a BM x BN tile:
+// activation fragments, weight chunks, and the lap's weight scales.
+template <int BM, int BN>
+constexpr int q8_stage_bytes() {
+    return BM * 128 + BN * 128 + BN * 16;
+}
+
+template <int BM, int BN, int WM, int WN, int NS>
+__global__ __launch_bounds__(WM * WN * kQWave) void k_gemm_q8_0(
+    const int8_t *__restrict__ act, int M, int kp, const float *__restrict__ sa_rows,
+    const int8_t *__restrict__ laps, int N, int n_tiles, int G, int n_mt, int n_total,
+    float *__restrict__ out) {
+    constexpr int NW = WM * WN;
+    constexpr int RG = BM / 32 / WM, TT = BN / 32 / WN;  // 32 x 32 sub-tiles per wave
+    constexpr int FA = BM / 8, FB = BN / 8, FS = BN / 16;  // loads of a stage
+    constexpr int LA = FA / NW, LB = FB / NW, LS = FS / NW;  // ... per wave
+    static_assert(RG >= 1 && TT >= 1 && FA % NW == 0 && FB % NW == 0 && FS % NW == 0,
+                  "wave split");
+    static_assert(NS >= 2, "ring depth");
+    constexpr int L = LA + LB + LS;  // loads per wave and stage, the same for every wave
+    constexpr int SA = BM * 128, SB = BN * 128;
+    constexpr int STAGE = q8_stage_bytes<BM, BN>();
+    extern __shared__ v4i s_buf[];
+
+    // XCD-aware tile index: workgroups go to the 8 XCDs round-robin; the M
+    // tiles of one weight column block run on one XCD and share its L2.
+    const int per_xcd = (int)(gridDim.x / kQXcds);
+    const int tile = (int)(blockIdx.x % kQXcds) * per_xcd + (int)(blockIdx.x / kQXcds);
+    if (tile >= n_total) return;
+    const int mt = tile % n_mt, nt = tile / n_mt;
+
+    const int t = threadIdx.x;
+    const int wv = __builtin_amdgcn_readfirstlane(t >> 6), l = t & 63;
+    const int wm = wv / WN, wn = wv % WN;
+    const unsigned lds0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)s_buf);
+    const int S = 2 * G;  // ring steps: half laps
+
+    // This wave's loads of a stage.  Fragment f = wv + NW * j of the A
+    // region: 16-row group f / 2, chunk f % 2 of the half lap; rows past M
+    // read row M - 1 (their outputs are not stored).  Fragment f of the B
+    // region: weight tile f / 2, chunk f % 2; tiles past the end read the
+    // last.  Scales: tile wv + NW * j, 4 bytes per lane (its 256 bytes).
+    // Step s adds 128 s bytes to an activation source, and lap s / 2 (plus
+    // 2 KiB for the second half) to a weight source.
+    const int8_t *a_src[LA];
+    const int8_t *b_src[LB];
+    const int8_t *s_src[LS];
+    const size_t lap_bytes = kQ8LapBytes;
+#pragma unroll
+    for (int j = 0; j < LA; ++j) {
+        const int f = wv + NW * j;
+        const int row = min(BM * mt + 16 * (f >> 1) + (l & 15), M - 1);
+        a_src[j] = act + (size_t)row * kp + 64 * (f & 1) + 16 * (l >> 4);
+    }
+#pragma unroll
+    for (int j = 0; j < LB; ++j) {
+        const int f = wv + NW * j;
+        const int T = min(BN / 16 * nt + (f >> 1), n_tiles - 1);
+        b_src[j] = laps + (size_t)T * G * lap_bytes + 1024 * (f & 1) + 16 * l;
+    }
+#pragma unroll
+    for (int j = 0; j < LS; ++j) {
+        const int T = min(BN / 16 * nt + wv + NW * j, n_tiles - 1);
+        s_src[j] = laps + (size_t)T * G * lap_bytes + 4096 + 4 * l;
+    }
+    // loads of step s (clamped to the last: the loads past the end re-read
+    // it into a stage no later step reads, so every wait count is constant)
+    auto issue = [&](int s) __attribute__((always_inline)) {
+        const int sc = min(s, S - 1);
+        const unsigned base = lds0 + (unsigned)((s % NS) * STAGE);
+        const size_t ao = (size_t)sc * 128;
+        const size_t bo = (size_t)(sc >> 1) * lap_bytes + (size_t)(sc & 1) * 2048;
+        const size_t so = (size_t)(sc >> 1) * lap_bytes;
+#pragma unroll
+        for (int j = 0; j < LA; ++j) q_dma16(a_src[j] + ao, base + (wv + NW * j) * 1024);
+#pragma unroll
+        for (int j = 0; j < LB; ++j) q_dma16_nt(b_src[j] + bo, base + SA + (wv + NW * j) * 1024);
+#pragma unroll
+        for (int j = 0; j < LS; ++j)
+            q_dma4_nt(s_src[j] + so, base + SA + SB + (wv + NW * j) * 256);
+    };
+
+    // v_mfma_i32_32x32x32_i8 operands: lane l holds row (or channel) l % 32
+    // and 16 k-bytes, k-half u = l / 32 of the block.  A staged fragment
+    // holds 16 rows x 64 bytes with lane' = 16 g + r owning row r and bytes
+    // [block 2c, k 8g..+8 | block 2c+1, k 8g..+8], so lane l gathers lane's
+    // 32u + l % 16 and 32u + 16 + l % 16 of its 16-row group: the low 8
+    // bytes of both are its operand for block 2c, the high 8 for block
+    // 2c + 1.  A and B are gathered alike, so the int32 dots are the same
+    // sums over the same k.
+    const int r16 = l & 15, half = (l >> 4) & 1, u = l >> 5;
+    float fs[RG][TT][16];
+#pragma unroll
+    for (int i = 0; i < RG; ++i)
+#pragma unroll
+        for (int j = 0; j < TT; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) fs[i][j][e] = 0.0f;
+    const v16i zero = {};
+
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s) issue(s);
+    // Step s: wait for its loads and for every wave to be done with step
+    // s - 1, whose stage the loads of step s + NS - 1 refill; then its 4
+    // blocks, software-pipelined: the MFMAs of block k + 1 (into registers
+    // of their own) are issued before the fold of block k, so the MFMA pipe
+    // and the VALU work side by side.
+    for (int s = 0; s < S; ++s) {
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"((NS - 2) * L) : "memory");
+        issue(s + NS - 1);
+        const v4i *ss_ = s_buf + ((size_t)(s % NS) * STAGE + SA + SB) / 16;
+        const int hh = s & 1;  // which half of the lap: its blocks 4 hh .. 4 hh + 3
+        v4i sc[TT];  // the lap's 8 f16 scales of this lane's channel in sub-tile j
+#pragma unroll
+        for (int j = 0; j < TT; ++j) sc[j] = ss_[(2 * (wn * TT + j) + half) * 16 + r16];
+        // Operands of chunk c: [sub-tile][block h of the chunk], each one
+        // ds_read2_b64 of lane' (offset h) and lane' + 16 (offset 32 + h, in
+        // 8-byte units) straight into a register quad.  The reads are issued
+        // here for the whole half lap and waited for once, by an s_waitcnt
+        // that takes every operand as its own in-out operand, so that no use
+        // can be scheduled before it.
+        v4i a[2][RG][2], b[2][TT][2];
+        const unsigned st = lds0 + (unsigned)((s % NS) * STAGE) + (unsigned)(16 * (32 * u + r16));
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+#pragma unroll
+            for (int i = 0; i < RG; ++i) {
+                const unsigned ad = st + (unsigned)(((2 * (wm * RG + i) + half) * 2 + c) * 1024);
+                asm volatile("ds_read2_b64 %0, %1 offset1:32" : "=v"(a[c][i][0]) : "v"(ad));
+                asm volatile("ds_read2_b64 %0, %1 offset0:1 offset1:33" : "=v"(a[c][i][1]) : "v"(ad));
+            }
+#pragma unroll
+            for (int j = 0; j < TT; ++j) {
+                const unsigned ad =
+                    st + (unsigned)(SA + ((2 * (wn * TT + j) + half) * 2 + c) * 1024);
+                asm volatile("ds_read2_b64 %0, %1 offset1:32" : "=v"(b[c][j][0]) : "v"(ad));
+                asm volatile("ds_read2_b64 %0, %1 offset0:1 offset1:33" : "=v"(b[c][j][1]) : "v"(ad));
+            }
+        }
+        static_assert(RG * 4 + TT * 4 <= 24, "operands of the wait");
+        q8_wait_lds(a, b);
+        v16i d[2][RG][TT];  // block dots of block k in set k % 2
+        auto dots = [&](auto kk) __attribute__((always_inline)) {
+            constexpr int k = decltype(kk)::value, c = k / 2, h = k % 2;
+#pragma unroll
+            for (int i = 0; i < RG; ++i)
+#pragma unroll
+                for (int j = 0; j < TT; ++j)
+                    d[k % 2][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[c][i][h], b[c][j][h],
+                                                                         zero, 0, 0, 0);
+        };
+        auto fold = [&](auto kk) __attribute__((always_inline)) {
+            constexpr int k = decltype(kk)::value, c = k / 2, h = k % 2;
+#pragma unroll
+            for (int j = 0; j < TT; ++j) {
+                // block 4 hh + k of the lap: f16 number 4 hh + k of the row's 8
+                const unsigned word = (unsigned)(hh ? sc[j][2 + c] : sc[j][c]);
+                // converted once here (v_cvt_f32_f16), so that each term is a
+                // full-rate v_fma_f32 rather than a mixed-precision FMA
+                float ds;
+                asm("v_cvt_f32_f16_e32 %0, %1" : "=v"(ds) : "v"(h ? (word >> 16) : word));
+#pragma unroll
+                for (int i = 0; i < RG; ++i)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e)
+                        fs[i][j][e] = __builtin_fmaf((float)d[k % 2][i][j][e], ds, fs[i][j][e]);
+            }
+        };
+        dots(std::integral_constant<int, 0>{});
+        q_static_for<4>([&](auto kk) {
+            constexpr int k = decltype(kk)::value;
+            if constexpr (k + 1 < 4) dots(std::integral_constant<int, k + 1>{});
+            fold(kk);
+        });
+    }
+    // the clamped loads past the end may still be writing LDS
+    asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+
+    // register e of sub-tile (i, j): row 32 i + 8 (e / 4) + 4 u + e % 4 of the
+    // wave's rows, channel 32 j + l % 32 of its channels
+#pragma unroll
+    for (int i = 0; i < RG; ++i) {
+        const int m0 = BM * mt + 32 * (wm * RG + i) + 4 * u;
+        float sa[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sa[e] = sa_rows[min(m0 + 8 * (e >> 2) + (e & 3), M - 1)];
+#pragma unroll
+        for (int j = 0; j < TT; ++j) {
+            const int n = BN * nt + 32 * (wn * TT + j) + (l & 31);
+            if (n >= N) continue;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int m = m0 + 8 * (e >> 2) + (e & 3);
+                if (m < M) out[(size_t)m * N + n] = fs[i][j][e] * sa[e];
+            }
+        }
+    }
+}
+
+template <int BM, int BN, int WM, int WN, int NS>
+mri_status launch_q8_inst(const int8_t *act, size_t m, const float *sa_rows,
+                          const Q8MatrixDev &w, float *out, hipStream_t s) {
+    constexpr size_t lds = (size_t)NS * q8_stage_bytes<BM, BN>();
+    static DeviceOnce attr;
+    MRI_HIP(attr.run([&](int) {
+        return hipFuncSetAttribute(
+            reinterpret_cast<const void *>(&k_gemm_q8_0<BM, BN, WM, WN, NS>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    }));
+    const size_t n_mt = (m + BM - 1) / BM;
+    const size_t n_nt = (w.n_tiles + BN / 16 - 1) / (BN / 16);
+    const size_t total = n_mt * n_nt;
+    const size_t grid = (total + kQXcds - 1) / kQXcds * kQXcds;
+    hipLaunchKernelGGL((k_gemm_q8_0<BM, BN, WM, WN, NS>), dim3((unsigned)grid),
+                       dim3(WM * WN * kQWave), lds, s, act, (int)m, (int)w.kp, sa_rows, w.laps,
+                       (int)w.n_out, (int)w.n_tiles, (int)w.laps_per_tile(), (int)n_mt,
+                       (int)total, out);
+    MRI_LAUNCHED("k_gemm_q8_0");
+    return MRI_OK;
+}
+
+}  // namespace
+
+// Where this kernel is used instead of the skinny kernel (which keeps the
+// reference's per-block rounding bit for bit).  Both are bound by the f32
+// fold; this one stages operand tiles in LDS and halves the fold's VALU
+// work.  Measured on MI355X at K = 4096: 125 vs 155 us at M = 512,
+// N = 12288, 184 vs 258 us at N = 22016; at M <= 128, or N = 4096 (M = 512,
+// K = 4096 or 11008), the two are within 5 % of each other, and the skinny
+// kernel is kept.
+bool gemm_q8_supported(size_t m, const Q8MatrixDev &w) {
+    return !w.w4 && m >= 256 && w.n_out >= 8192 && m * w.kp < (1ull << 31) &&
+           m * w.n_out < (1ull << 31);
+}
+
+// act: quantized rows [m][w.kp], chunk-permuted (launch_quantize_rows with
+// the Q8_0 layout); sa_rows: their scales.
+// Tiles of 128 rows: 128 channels and 8 waves of 64 x 32 from 16384
+// channels up (184 vs 197 us at M = 512, N = 22016), else 64 channels and 4
+// waves of 64 x 32 (about 77 KiB of LDS: two workgroups per CU), which keeps
+// the fold balanced over the CUs when the wide tiles would come in 1.5
+// passes (768 workgroups against 384 at N = 12288).
+mri_status launch_gemm_q8_0(const int8_t *act, size_t m, const float *sa_rows,
+                            const Q8MatrixDev &w, float *out, hipStream_t s) {
+    if (w.n_out >= 16384) return launch_q8_inst<128, 128, 2, 4, 4>(act, m, sa_rows, w, out, s);
+    return launch_q8_inst<128, 64, 2, 2, 3>(act, m, sa_rows, w, out, s);
+}
+
+}  // namespace mri
