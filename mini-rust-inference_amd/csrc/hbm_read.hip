@@ -10,22 +10,27 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-// Grid-stride over n16 16-byte vectors, four loads in flight per thread;
-// the values are folded into one word that is stored only if it equals a
-// value the data never produce in practice, so the loads cannot be dropped.
+// Each wave reads one contiguous 4 KiB chunk (four 16-byte non-temporal
+// loads per lane, all issued before any use); the values are folded into
+// one word that is stored only if it equals a value the data never produce
+// in practice, so the loads cannot be dropped.  Measured on MI355X over 48 MB
+// (9 rotated copies): 8.16 us, against 8.2-8.7 us for 8-16 KiB per wave,
+// 10.1 us for 32 KiB, 8.2-8.9 us for persistent waves looping over 4 KiB
+// chunks, and 8.8 us for a grid-stride loop of single loads.
 __global__ __launch_bounds__(256) void k_hbm_read(const v4i *__restrict__ p, size_t n16,
                                                   int *__restrict__ sink) {
+    const int l = threadIdx.x & 63;
+    const size_t base = ((size_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 256;
     int acc = 0;
-    const size_t stride = (size_t)gridDim.x * 256;
-    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    for (; i + 3 * stride < n16; i += 4 * stride) {
-        const v4i a = __builtin_nontemporal_load(p + i);
-        const v4i b = __builtin_nontemporal_load(p + i + stride);
-        const v4i c = __builtin_nontemporal_load(p + i + 2 * stride);
-        const v4i d = __builtin_nontemporal_load(p + i + 3 * stride);
-        acc ^= a.x ^ b.y ^ c.z ^ d.w;
+    if (base + 256 <= n16) {
+        v4i r[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) r[u] = __builtin_nontemporal_load(p + base + u * 64 + l);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc ^= r[u].x ^ r[u].w;
+    } else {
+        for (size_t i = base + l; i < n16; i += 64) acc ^= p[i].x;
     }
-    for (; i < n16; i += stride) acc ^= p[i].x;
     if (acc == 0x5a5a5a5a && sink) *sink = acc;
 }
 
@@ -34,8 +39,9 @@ __global__ __launch_bounds__(256) void k_hbm_read(const v4i *__restrict__ p, siz
 mri_status launch_hbm_read(const void *p, size_t bytes, int32_t *sink, hipStream_t s) {
     const size_t n16 = bytes / 16;
     if (n16 == 0) return MRI_OK;
-    const int cus = device_cus();
-    const unsigned grid = (unsigned)std::max(1, 16 * (cus > 0 ? cus : 256));
+    const size_t waves = (n16 + 255) / 256;  // one 4 KiB chunk per wave
+    if ((waves + 3) / 4 > 0x7fffffff) return set_error(MRI_ERR_UNSUPPORTED, "hbm_read: too large");
+    const unsigned grid = (unsigned)((waves + 3) / 4);
     hipLaunchKernelGGL(k_hbm_read, dim3(grid), dim3(256), 0, s, static_cast<const v4i *>(p), n16,
                        reinterpret_cast<int *>(sink));
     MRI_LAUNCHED("k_hbm_read");
