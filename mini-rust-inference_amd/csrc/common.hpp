@@ -348,7 +348,9 @@ mri_status launch_rope_qkv(float *q, const float *k, const float *v, size_t seq,
 bool attention_supported(size_t head_dim);
 // Causal GQA of seq_q query rows (positions start_pos ..) against cache rows
 // 0 .. start_pos + seq_q - 1.  part: attention_part_floats(...) floats of
-// workspace for the split-key one-row form (nullable: one workgroup per head).
+// workspace for the split-key one-row form (nullable: one workgroup per head);
+// its first words are per-head arrival counters, zeroed before the first
+// call and left zero by every call.
 size_t attention_part_floats(size_t n_heads, size_t head_dim, size_t max_seq);
 mri_status launch_attention(const float *q, size_t q_stride, size_t seq_q, const float *kc,
                             const float *vc, size_t n_heads, size_t n_kv_heads, size_t head_dim,

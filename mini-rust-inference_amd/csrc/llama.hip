@@ -359,20 +359,75 @@ __global__ __launch_bounds__(256) void k_attention(
 // thread t forms the partial dot of key t % 64 over dims (t / 64) * HD/4 ..,
 // the four partials are added in order; then the chunk's max m_c, weights
 // e_j = exp(s_j - m_c) and their sum l_c, and the chunk's weighted value
-// sum o_c (four key quarters added in order).  part: [heads][chunks][HD+2].
+// sum o_c (four key quarters added in order).  The value rows a thread
+// needs are loaded with its key row, so their latency overlaps the score
+// pass.  The chunk's (m_c, l_c, o_c) go to part ([heads][chunks][HD+2])
+// through device-scope (sc1) stores, complete before the workgroup counts
+// itself on its head's counter (relaxed, device scope); the workgroup that
+// counts last for a head combines the chunks (attn_combine) and resets the
+// counter, so no workgroup waits for another and no second launch is needed.
+// The partials reach the point of coherence of all XCDs before the count
+// (vmcnt(0) and a barrier), and the combining workgroup reads them with sc1
+// loads, which do not hit lines its XCD's L2 cached before.
+// cnt: one word per head, zero between calls.
+template <int HD>
+__device__ inline void attn_combine(const float *ph, int nch, int d, float *s_m, float *s_l,
+                                    float *out) {
+    for (int c = d; c < nch; c += HD) {
+        s_m[c] = __hip_atomic_load(ph + c * (HD + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_l[c] = __hip_atomic_load(ph + c * (HD + 2) + 1, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (d >= HD) return;
+    float m = -INFINITY;
+    for (int c = 0; c < nch; ++c) m = fmaxf(m, s_m[c]);
+    float l = 0.0f, o = 0.0f;
+    for (int c0 = 0; c0 < nch; c0 += 16) {
+        float ov[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u)
+            ov[u] = c0 + u < nch ? __hip_atomic_load(ph + (c0 + u) * (HD + 2) + 2 + d,
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                 : 0.0f;
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            if (c0 + u < nch) {
+                const float f = expf(s_m[c0 + u] - m);
+                l = l + s_l[c0 + u] * f;
+                o = o + ov[u] * f;
+            }
+        }
+    }
+    out[d] = o / l;
+}
+
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_decode_part(
     const float *__restrict__ q, const float *__restrict__ kc, const float *__restrict__ vc,
-    int kvd, int L, int groups, float scale, float *__restrict__ part) {
+    int kvd, int L, int groups, float scale, float *__restrict__ part, int *__restrict__ cnt,
+    float *__restrict__ out) {
     constexpr int Q4 = HD / 16;  // float4 per thread in the score pass
     constexpr int E = HD / kWave;
+    static_assert(HD <= 256, "one thread per output element in the combine");
     __shared__ float s_s[4][64];
     __shared__ float s_w[64];
     __shared__ float s_o[4][HD];
+    __shared__ float s_m[1024], s_l[1024];
+    __shared__ int s_last;
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     const int c = blockIdx.x, h = blockIdx.y, kh = h / groups, nch = gridDim.x;
     const int j = 64 * c + lane;
     const float *qr = q + (size_t)h * HD + wv * (HD / 4);
+    // the value rows of keys 16 wv .. 16 wv + 15 of the chunk
+    float vv[16][E];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+        const int jj = 64 * c + 16 * wv + u;
+#pragma unroll
+        for (int e = 0; e < E; ++e)
+            vv[u][e] = jj < L ? vc[(size_t)jj * kvd + kh * HD + lane * E + e] : 0.0f;
+    }
     float acc = 0.0f;
     if (j < L) {
         const float4 *kr = reinterpret_cast<const float4 *>(kc + (size_t)j * kvd + kh * HD +
@@ -395,6 +450,7 @@ __global__ __launch_bounds__(256) void k_attn_decode_part(
     }
     s_s[wv][lane] = acc;
     __syncthreads();
+    float *pc = part + ((size_t)h * nch + c) * (HD + 2);
     if (wv == 0) {
         const float sc = (((s_s[0][lane] + s_s[1][lane]) + s_s[2][lane]) + s_s[3][lane]) * scale;
         const float sv = j < L ? sc : -INFINITY;
@@ -403,8 +459,8 @@ __global__ __launch_bounds__(256) void k_attn_decode_part(
         const float l = wave_sum(e);
         s_w[lane] = e;
         if (lane == 0) {
-            part[((size_t)h * nch + c) * (HD + 2)] = m;
-            part[((size_t)h * nch + c) * (HD + 2) + 1] = l;
+            __hip_atomic_store(pc, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(pc + 1, l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
     __syncthreads();
@@ -412,14 +468,6 @@ __global__ __launch_bounds__(256) void k_attn_decode_part(
     float o[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) o[e] = 0.0f;
-    float vv[16][E];
-#pragma unroll
-    for (int u = 0; u < 16; ++u) {
-        const int jj = 64 * c + 16 * wv + u;
-#pragma unroll
-        for (int e = 0; e < E; ++e)
-            vv[u][e] = jj < L ? vc[(size_t)jj * kvd + kh * HD + lane * E + e] : 0.0f;
-    }
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
         const float w = s_w[16 * wv + u];
@@ -433,44 +481,17 @@ __global__ __launch_bounds__(256) void k_attn_decode_part(
     for (int e = 0; e < E; ++e) s_o[wv][lane * E + e] = o[e];
     __syncthreads();
     for (int d = t; d < HD; d += 256)
-        part[((size_t)h * nch + c) * (HD + 2) + 2 + d] =
-            ((s_o[0][d] + s_o[1][d]) + s_o[2][d]) + s_o[3][d];
-}
-
-// Combines the chunks of head blockIdx.x: m = max m_c,
-// out = sum_c o_c e^(m_c - m) / sum_c l_c e^(m_c - m).
-// Chunk maxima and sums are read once, in parallel, into LDS (up to 1024
-// chunks); each thread then reads its dimension of every chunk with the
-// loads issued ahead of the sums.
-template <int HD>
-__global__ __launch_bounds__(HD) void k_attn_decode_combine(const float *__restrict__ part,
-                                                            int nch, float *__restrict__ out) {
-    __shared__ float s_m[1024], s_l[1024];
-    const int h = blockIdx.x, d = threadIdx.x;
-    const float *ph = part + (size_t)h * nch * (HD + 2);
-    for (int c = d; c < nch; c += HD) {
-        s_m[c] = ph[c * (HD + 2)];
-        s_l[c] = ph[c * (HD + 2) + 1];
-    }
+        __hip_atomic_store(pc + 2 + d, ((s_o[0][d] + s_o[1][d]) + s_o[2][d]) + s_o[3][d],
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's partials are at the device
     __syncthreads();
-    float m = -INFINITY;
-    for (int c = 0; c < nch; ++c) m = fmaxf(m, s_m[c]);
-    float l = 0.0f, o = 0.0f;
-    for (int c0 = 0; c0 < nch; c0 += 16) {
-        float ov[16];
-#pragma unroll
-        for (int u = 0; u < 16; ++u)
-            ov[u] = c0 + u < nch ? ph[(c0 + u) * (HD + 2) + 2 + d] : 0.0f;
-#pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            if (c0 + u < nch) {
-                const float f = expf(s_m[c0 + u] - m);
-                l = l + s_l[c0 + u] * f;
-                o = o + ov[u] * f;
-            }
-        }
-    }
-    out[(size_t)h * HD + d] = o / l;
+    if (t == 0)
+        s_last = __hip_atomic_fetch_add(&cnt[h], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 nch - 1;
+    __syncthreads();
+    if (!s_last) return;
+    attn_combine<HD>(part + (size_t)h * nch * (HD + 2), nch, t, s_m, s_l, out + (size_t)h * HD);
+    if (t == 0) __hip_atomic_store(&cnt[h], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---- SwiGLU (ops/activation/swiglu.rs): out = gate / (1 + exp(-gate)) * up ----
@@ -718,6 +739,9 @@ mri_status attn_launch(const float *q, int qs, int qd, const float *kc, const fl
     return MRI_OK;
 }
 
+// Words of the per-head counters at the start of the partials buffer.
+inline size_t attn_cnt_words(size_t n_heads) { return (n_heads + 63) / 64 * 64; }
+
 template <int HD>
 mri_status attn_dispatch(const float *q, int qs, int qd, const float *kc, const float *vc, int kvd,
                          int seq_q, int start_pos, int groups, int n_heads, float *out,
@@ -726,12 +750,11 @@ mri_status attn_dispatch(const float *q, int qs, int qd, const float *kc, const 
     if (seq_q == 1 && part && L <= 1024 * 64) {  // the combine holds <= 1024 chunks
         const int nch = (L + 63) / 64;
         const float scale = 1.0f / sqrtf((float)HD);
+        // [head counters, padded to 64 words][partials]
+        int *cnt = reinterpret_cast<int *>(part);
         hipLaunchKernelGGL(k_attn_decode_part<HD>, dim3(nch, n_heads), dim3(256), 0, s, q, kc,
-                           vc, kvd, L, groups, scale, part);
+                           vc, kvd, L, groups, scale, part + attn_cnt_words(n_heads), cnt, out);
         MRI_LAUNCHED("k_attn_decode_part");
-        hipLaunchKernelGGL(k_attn_decode_combine<HD>, dim3(n_heads), dim3(HD), 0, s, part, nch,
-                           out);
-        MRI_LAUNCHED("k_attn_decode_combine");
         return MRI_OK;
     }
     const int lcap = (L + 3) / 4 * 4;
@@ -889,7 +912,7 @@ mri_status launch_rope_qkv(float *q, const float *k, const float *v, size_t seq,
 bool attention_supported(size_t head_dim) { return head_dim == 64 || head_dim == 128; }
 
 size_t attention_part_floats(size_t n_heads, size_t head_dim, size_t max_seq) {
-    return n_heads * ((max_seq + 63) / 64) * (head_dim + 2);
+    return attn_cnt_words(n_heads) + n_heads * ((max_seq + 63) / 64) * (head_dim + 2);
 }
 
 mri_status launch_attention(const float *q, size_t q_stride, size_t seq_q, const float *kc,

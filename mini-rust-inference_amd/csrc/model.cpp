@@ -542,6 +542,10 @@ mri_status mri_llama_create(const mri_llama_config *cfg, const float *token_embd
         (st = dalloc_t(m, R + 1, &m->gen)) ||
         (st = dalloc_t(m, attention_part_floats(g.n_heads, hd, R), &m->attn_part)))
         return fail(st);
+    // the decode attention's per-head counters start at zero
+    if (const hipError_t e =
+            hipMemset(m->attn_part, 0, attention_part_floats(g.n_heads, hd, R) * sizeof(float)))
+        return fail(hip_error(e, "hipMemset(attention workspace)"));
     m->fuse_norm = rmsnorm_stats_supported(g.dim);
     // RopeTable::new (ops/rope.rs): theta_i = 1 / base^(2i / head_dim) and
     // angle = pos * theta_i in f32, with the C library's powf / cosf / sinf.
