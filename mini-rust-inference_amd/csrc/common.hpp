@@ -72,6 +72,8 @@ constexpr int kQK = 32;           // Q8_0 / Q4_0 block elements
 constexpr int kQ8Bytes = 34;      // raw Q8_0 block bytes
 constexpr int kQ4Bytes = 18;      // raw Q4_0 block bytes
 constexpr int kQ8ScaleGroup = 8;  // blocks per scale group (16 bytes of f16)
+constexpr int kBufWord3 = 0x00020000;  // raw buffer resource, dword 3 (gfx950): loads past
+                                       // num_records return zeros
 
 inline size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
 

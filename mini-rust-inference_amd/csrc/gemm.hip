@@ -93,7 +93,6 @@ __device__ inline void wait_barrier() {
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(N) : "memory");
 }
 
-constexpr int kBufWord3 = 0x00020000;  // raw buffer resource, dword 3 (gfx950)
 constexpr int kScDevice = 16;          // cache policy sc1: device scope
 constexpr int kWaitVm0 = 0x0F70;       // s_waitcnt vmcnt(0), others untouched
 

@@ -714,6 +714,316 @@ __global__ __launch_bounds__(256) void k_argmax_split(const float *__restrict__ 
     for (int i = threadIdx.x; i < d; i += 256) x_out[i] = src[i];
 }
 
+// Prefill form on the fp32 matrix cores (head dim 128): the same causal
+// attention as k_attention, in the flash-attention order.  Workgroup =
+// (block of 32 query rows, head h), heaviest blocks first; its 4 waves take
+// the visible key tiles of 32 round-robin (wave w: tiles w, w + 4, ...), each
+// with its own running max, sum and output, and the four partials are
+// combined through LDS at the end.  Per tile, with v_mfma_f32_32x32x2_f32:
+//   S^T (32 keys x 32 queries) = K_tile . Q^T   (64 MFMAs over the 128 dims)
+//   online softmax per query in base 2: P = 2^(S log2(e) / sqrt(128) - m),
+//     with m (and l, O^T) moved to the running max only when that grows by
+//     more than 12
+//   O^T (128 dims x 32 queries) += V_tile^T . P^T   (4 x 16 MFMAs)
+// A wave's vector work (softmax) does not overlap its own matrix-core work,
+// only another wave's: two workgroups share each CU (80 KiB of LDS and at
+// most 256 registers per wave each), so every SIMD runs two waves whose
+// softmax, load waits and products interleave.  Each wave stages its tiles
+// in its own 16 KiB of LDS with direct global->LDS loads (16 bytes per lane)
+// in two 8 KiB halves: dims 0-63 and 64-127 of the K tile, then keys 0-15
+// and 16-31 of the V tile, each half loaded while the other half's products
+// run.  The layout is the order the lanes read it, so every operand read is
+// one conflict-free ds_read_b128 per lane.  The matrix cores sum over k in
+// any order, so the dims are permuted to suit that: k-step 4j + c of S pairs
+// dims 8j + c (lanes 0-31) and 8j + 4 + c (lanes 32-63) of K row "key" and
+// Q row "query"; dim tile dt of O^T holds dims 4i + dt, so V row key's dims
+// 4i .. 4i + 3 are one read of lane i.  Each lane holds one query (column
+// l % 32), so the softmax's reductions are over its own registers and the
+// other half-wave (one shuffle), and P^T feeds the second product from
+// registers: in k-step r, lane half u contributes the key of its output
+// register r, 8(r/4) + 4u + r%4.  The result differs from the reference's
+// sequential sums only in f32 rounding (and v_exp_f32's 1 ulp).
+typedef float v16f __attribute__((ext_vector_type(16)));
+constexpr int kAmQ = 32;         // query rows per workgroup
+constexpr int kAmK = 32;         // keys per tile
+constexpr int kAmP = 132;        // combine pitch in floats: [wave][query][dim]
+constexpr int kAmHalf = 8192;    // bytes of half a staged tile
+constexpr int kAmTile = 2 * kAmHalf;
+constexpr int kAmQOff = 4 * kAmTile;                  // Q block after the 4 waves' tiles
+constexpr size_t kAmLds = (size_t)kAmQOff + kAmTile;  // 80 KiB: two workgroups per CU
+constexpr int kAmMlOff = 4 * kAmQ * kAmP * 4;         // m [4][32], l [4][32] after the partials
+constexpr float kAmMove = 12.0f;                      // P <= 2^12 between moves of m
+static_assert((size_t)kAmMlOff + 2 * 4 * kAmQ * sizeof(float) <= kAmLds,
+              "combine partials, m and l alias the staged tiles and the queries");
+
+// 16 bytes per lane from a per-lane address into LDS at lds + 16 * lane
+__device__ inline void am_dma16(const void *g, unsigned lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(g), "s"(lds)
+                 : "memory", "m0");
+}
+// the same from a uniform base plus a per-lane 32-bit offset
+__device__ inline void am_dma16_s(const void *base, unsigned voff, unsigned lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :
+                 : "v"(voff), "s"(base), "s"(lds)
+                 : "memory", "m0");
+}
+template <int N>
+__device__ inline void am_wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+__device__ inline void am_wait_lds_reads() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+__global__ __launch_bounds__(256, 2) void k_attention_mfma(
+    const float *__restrict__ q, int qs, const float *__restrict__ kc,
+    const float *__restrict__ vc, int kvd, int seq_q, int start_pos, int groups, int n_heads,
+    float scale_log2, float *__restrict__ out, int qd) {
+    constexpr int HD = 128;
+    extern __shared__ __align__(16) char s_amb[];
+    const int t = threadIdx.x, l = t & 63, lq = l & 31, hf = l >> 5;
+    const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int nqb = (seq_q + kAmQ - 1) / kAmQ;
+    const int h = blockIdx.x % n_heads, qb = nqb - 1 - blockIdx.x / n_heads;
+    const int kh = h / groups;
+    const int i0 = qb * kAmQ;
+    const int qi = i0 + lq;           // this lane's query row
+    const bool qvalid = qi < seq_q;
+    const int pq = start_pos + qi;    // its absolute position: keys 0 .. pq
+    const int last_row = min(i0 + kAmQ, seq_q) - 1;
+    const int Lw = start_pos + last_row + 1;  // keys the block sees
+    const int nt = (Lw + kAmK - 1) / kAmK;
+
+    const unsigned lds0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)s_amb);
+    const unsigned kv_lds = lds0 + w * kAmTile;  // this wave's K, then V tile
+    const unsigned q_lds = lds0 + kAmQOff;
+    // reader offsets: step j (r) of lane l reads bytes 1024 j + 16 l
+    const char *kv_rd = s_amb + w * kAmTile + 16 * l;
+    const char *q_rd = s_amb + kAmQOff + 16 * l;
+
+    // Staging: a tile whose 32 rows all lie before the block's last visible
+    // key uses uniform row addresses and a fixed per-lane offset; the
+    // block's last tile clamps every row to that key (finite values; their
+    // scores are masked).
+    const size_t row_bytes = (size_t)kvd * 4;
+    const char *k_head = reinterpret_cast<const char *>(kc + (size_t)kh * HD);
+    const char *v_head = reinterpret_cast<const char *>(vc + (size_t)kh * HD);
+    const unsigned k_voff = (unsigned)(lq * row_bytes) + 16 * hf;       // K row lq, dims 4hf ..
+    const unsigned v_voff = (unsigned)(4 * hf * row_bytes) + 16 * lq;   // V row 4hf, dims 4lq ..
+    auto dma_k = [&](int kt, int half) __attribute__((always_inline)) {
+        const unsigned lds = kv_lds + half * kAmHalf;
+        if ((kt + 1) * kAmK <= Lw) {
+            const char *b = k_head + (size_t)kt * kAmK * row_bytes + 256 * half;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) am_dma16_s(b + 32 * j, k_voff, lds + 1024 * j);
+        } else {
+            const float *src = kc + (size_t)min(kt * kAmK + lq, Lw - 1) * kvd + (size_t)kh * HD +
+                               4 * hf + 64 * half;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) am_dma16(src + 8 * j, lds + 1024 * j);
+        }
+    };
+    auto dma_v = [&](int kt, int half) __attribute__((always_inline)) {
+        const unsigned lds = kv_lds + half * kAmHalf;
+        if ((kt + 1) * kAmK <= Lw) {
+#pragma unroll
+            for (int rr = 0; rr < 8; ++rr) {
+                const int r = 8 * half + rr;
+                am_dma16_s(v_head + (size_t)(kt * kAmK + 8 * (r >> 2) + (r & 3)) * row_bytes,
+                           v_voff, lds + 1024 * rr);
+            }
+        } else {
+#pragma unroll
+            for (int rr = 0; rr < 8; ++rr) {
+                const int r = 8 * half + rr;
+                const int key = min(kt * kAmK + 8 * (r >> 2) + 4 * hf + (r & 3), Lw - 1);
+                am_dma16(vc + (size_t)key * kvd + (size_t)kh * HD + 4 * lq, lds + 1024 * rr);
+            }
+        }
+    };
+    // the query block, in the K tile's order (rows past seq_q repeat the last
+    // row; their scores are masked): wave w stages steps 4w .. 4w + 3
+    {
+        const float *src = q + (size_t)min(qi, seq_q - 1) * qs + (size_t)h * HD + 4 * hf;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) am_dma16(src + 8 * (4 * w + u), q_lds + 1024 * (4 * w + u));
+    }
+
+    auto s_half = [&](int half, v16f &x0, v16f &x1) __attribute__((always_inline)) {
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+            const int j = 8 * half + jj;
+            const float4 kv = *reinterpret_cast<const float4 *>(kv_rd + 1024 * j);
+            const float4 qv = *reinterpret_cast<const float4 *>(q_rd + 1024 * j);
+            x0 = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qv.x, x0, 0, 0, 0);
+            x1 = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qv.y, x1, 0, 0, 0);
+            x0 = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qv.z, x0, 0, 0, 0);
+            x1 = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qv.w, x1, 0, 0, 0);
+        }
+    };
+    // Online softmax with a lazily moved reference m: P = 2^(y - m), and m
+    // (with l and O) moves to the tile max only when that exceeds it by more
+    // than kAmMove.  A query with no visible key yet keeps m = -inf, l = 0,
+    // O = 0.  Only tiles that reach past the block's first query, or a block
+    // with rows past seq_q, need the mask.
+    float m_ref = -INFINITY, l_run = 0.0f;
+    v16f o[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) o[dt] = v16f{};
+    float p[16];
+    const bool rows_short = i0 + kAmQ > seq_q;
+    auto softmax = [&](const v16f &x, int kt) __attribute__((always_inline)) {
+        float y[16];
+        if (rows_short || kt * kAmK + kAmK - 1 > start_pos + i0) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = kt * kAmK + 8 * (r >> 2) + 4 * hf + (r & 3);
+                y[r] = (qvalid && key <= pq) ? x[r] * scale_log2 : -INFINITY;
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) y[r] = x[r] * scale_log2;
+        }
+        float mt = y[0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mt = fmaxf(mt, y[r]);
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        const bool move = mt > m_ref + kAmMove;
+        const float alpha = move ? __builtin_amdgcn_exp2f(m_ref - mt) : 1.0f;  // 0 from -inf
+        m_ref = move ? mt : m_ref;
+        const float m_use = m_ref == -INFINITY ? 0.0f : m_ref;  // then every y is -inf
+        float ps = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            p[r] = __builtin_amdgcn_exp2f(y[r] - m_use);
+            ps = ps + p[r];
+        }
+        ps = ps + __shfl_xor(ps, 32);
+        l_run = l_run * alpha + ps;
+        if (__any(move)) {
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) o[dt] = o[dt] * alpha;
+        }
+    };
+    auto pv_half = [&](int half) __attribute__((always_inline)) {
+#pragma unroll
+        for (int rr = 0; rr < 8; ++rr) {
+            const int r = 8 * half + rr;
+            const float4 vv = *reinterpret_cast<const float4 *>(kv_rd + 1024 * r);
+            o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.x, p[r], o[0], 0, 0, 0);
+            o[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.y, p[r], o[1], 0, 0, 0);
+            o[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.z, p[r], o[2], 0, 0, 0);
+            o[3] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.w, p[r], o[3], 0, 0, 0);
+        }
+    };
+    // This wave's tiles kt = w, w + 4, ...  Each half is staged once the
+    // reads of what its LDS held before have returned; every wait leaves
+    // exactly the other half's 8 loads in flight, in this order:
+    //   K lo, K hi | S lo | V lo | S hi | V hi | softmax | PV lo | next K lo
+    //   | PV hi | next K hi
+    if (w < nt) {
+        dma_k(w, 0);
+        dma_k(w, 1);
+        am_wait_vm<8>();  // this wave's share of the queries, K lo
+        __syncthreads();  // every wave's share of the queries
+        for (int kt = w; kt < nt; kt += 4) {
+            const bool more = kt + 4 < nt;
+            am_wait_vm<8>();  // K lo
+            v16f x0 = v16f{}, x1 = v16f{};
+            s_half(0, x0, x1);
+            am_wait_lds_reads();
+            dma_v(kt, 0);
+            am_wait_vm<8>();  // K hi
+            s_half(1, x0, x1);
+            am_wait_lds_reads();
+            dma_v(kt, 1);
+            softmax(x0 + x1, kt);
+            am_wait_vm<8>();  // V lo
+            pv_half(0);
+            am_wait_lds_reads();
+            if (more) {
+                dma_k(kt + 4, 0);
+                am_wait_vm<8>();  // V hi
+            } else {
+                am_wait_vm<0>();  // V hi
+            }
+            pv_half(1);
+            am_wait_lds_reads();
+            if (more) dma_k(kt + 4, 1);
+        }
+    } else {
+        am_wait_vm<0>();
+        __syncthreads();
+    }
+    const float m_run = m_ref;
+    // combine: O = sum_w c_w O_w / sum_w c_w l_w, c_w = 2^(m_w - max_w m_w)
+    // (a wave that saw no key of a query has m_w = -inf, l_w = 0, O_w = 0);
+    // the partials overwrite the staged tiles once every wave is done
+    __syncthreads();
+    {
+        float *s_am = reinterpret_cast<float *>(s_amb);
+        float *pw = s_am + (size_t)(w * kAmQ + lq) * kAmP;
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            *reinterpret_cast<float4 *>(pw + 4 * (8 * (r >> 2) + 4 * hf + (r & 3))) =
+                make_float4(o[0][r], o[1][r], o[2][r], o[3][r]);
+        float *sm = reinterpret_cast<float *>(s_amb + kAmMlOff), *sl = sm + 4 * kAmQ;
+        if (hf == 0) {
+            sm[w * kAmQ + lq] = m_run;
+            sl[w * kAmQ + lq] = l_run;
+        }
+        __syncthreads();
+        const int qq = t >> 3, seg = t & 7;  // query, 16-dim segment
+        if (i0 + qq >= seq_q) return;
+        float mw[4], M = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            mw[u] = sm[u * kAmQ + qq];
+            M = fmaxf(M, mw[u]);
+        }
+        float c[4], L = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            c[u] = __builtin_amdgcn_exp2f(mw[u] - M);  // 0 for m_w = -inf (M is finite)
+            L = L + c[u] * sl[u * kAmQ + qq];
+        }
+        const float inv = 1.0f / L;
+        float *op = out + (size_t)(i0 + qq) * qd + (size_t)h * HD + 16 * seg;
+#pragma unroll
+        for (int d4 = 0; d4 < 4; ++d4) {
+            float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float4 v = *reinterpret_cast<const float4 *>(
+                    s_am + (size_t)(u * kAmQ + qq) * kAmP + 16 * seg + 4 * d4);
+                acc.x = acc.x + c[u] * v.x;
+                acc.y = acc.y + c[u] * v.y;
+                acc.z = acc.z + c[u] * v.z;
+                acc.w = acc.w + c[u] * v.w;
+            }
+            *reinterpret_cast<float4 *>(op + 4 * d4) =
+                make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+        }
+    }
+}
+
+mri_status attn_mfma_launch(const float *q, int qs, int qd, const float *kc, const float *vc,
+                            int kvd, int seq_q, int start_pos, int groups, int n_heads,
+                            float *out, hipStream_t s) {
+    static DeviceOnce attr;
+    MRI_HIP(attr.run([](int) {
+        return hipFuncSetAttribute(reinterpret_cast<const void *>(&k_attention_mfma),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)kAmLds);
+    }));
+    const float scale_log2 = (float)(1.4426950408889634 / sqrt(128.0));  // log2(e) / sqrt(128)
+    const int nqb = (seq_q + kAmQ - 1) / kAmQ;
+    hipLaunchKernelGGL(k_attention_mfma, dim3(nqb * n_heads), dim3(256), kAmLds, s, q, qs, kc, vc,
+                       kvd, seq_q, start_pos, groups, n_heads, scale_log2, out, qd);
+    MRI_LAUNCHED("k_attention_mfma");
+    return MRI_OK;
+}
+
 // query rows per prefill workgroup: 16, else 4 when the weight rows do not fit
 template <int HD, int QB>
 size_t attn_lds(int lcap) {
@@ -757,6 +1067,8 @@ mri_status attn_dispatch(const float *q, int qs, int qd, const float *kc, const 
         MRI_LAUNCHED("k_attn_decode_part");
         return MRI_OK;
     }
+    if (HD == 128 && seq_q >= 32)
+        return attn_mfma_launch(q, qs, qd, kc, vc, kvd, seq_q, start_pos, groups, n_heads, out, s);
     const int lcap = (L + 3) / 4 * 4;
     constexpr size_t kMax = 160 * 1024;
     if (attn_lds<HD, 16>(lcap) <= kMax)
