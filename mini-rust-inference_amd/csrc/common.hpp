@@ -234,6 +234,10 @@ struct RowOps {
     float eps = 0.0f;
     float *x_out = nullptr;         // receives a copy of x as read
     bool accum = false;             // out += the projection (a residual add)
+    // The row x is the gate half of a SwiGLU: the projection's input is
+    // x / (1 + exp(-x)) * up elementwise (ops/activation/swiglu.rs), computed
+    // as the separate SwiGLU kernel does (not with norm_w or x_out).
+    const float *up = nullptr;
     // RoPE (ops/rope.rs) on output channels [0, rope_n): the pairs
     // (2i, 2i+1) of each head of hd channels rotate by the table entries
     // i % (hd/2) of rope_cos / rope_sin (one position's rows).
@@ -243,7 +247,7 @@ struct RowOps {
     // out2[n - seg2] (q | k | v of a fused projection into the KV cache).
     int seg1 = INT_MAX, seg2 = INT_MAX;
     float *out1 = nullptr, *out2 = nullptr;
-    bool any() const { return norm_w || x_out || accum || rope_n > 0 || out1 || out2; }
+    bool any() const { return norm_w || x_out || accum || up || rope_n > 0 || out1 || out2; }
 };
 bool gemv_int8_supported(bool fused, size_t m, size_t n_tiles, size_t k, size_t kp);
 // The device matrices behind the public handles (capi.cpp).

@@ -98,6 +98,7 @@ struct ActIn {
     const float *norm_w = nullptr;  // optional [K], 16-byte aligned (fused path)
     float eps = 0.0f;
     float *x_out = nullptr;         // optional [K], 16-byte aligned (fused path)
+    const float *up = nullptr;      // optional [K]: x is a SwiGLU gate row (fused path)
     int accum = 0;
     const float *rope_cos = nullptr, *rope_sin = nullptr;
     int rope_n = 0, hd = 2, seg1 = INT_MAX, seg2 = INT_MAX;
@@ -105,7 +106,7 @@ struct ActIn {
 
     ActIn(const float *x_, const int8_t *act_, int k, int8_t *aq, float *so, const RowOps &o)
         : x(x_), act(act_), K(k), act_q_out(aq), scale_out(so), norm_w(o.norm_w), eps(o.eps),
-          x_out(o.x_out), accum(o.accum ? 1 : 0), rope_cos(o.rope_cos), rope_sin(o.rope_sin),
+          x_out(o.x_out), up(o.up), accum(o.accum ? 1 : 0), rope_cos(o.rope_cos), rope_sin(o.rope_sin),
           rope_n(o.rope_n), hd(o.hd), seg1(o.seg1), seg2(o.seg2), out1(o.out1), out2(o.out2) {}
 };
 
@@ -132,6 +133,27 @@ template <int S, int XR>
 __device__ inline void stage_load(const v4i *src, int n16, v4i (&xr)[XR]) {
 #pragma unroll
     for (int e = 0; e < XR; ++e) xr[e] = src[min((int)threadIdx.x + S * kWave * e, n16 - 1)];
+}
+
+// SwiGLU of the staged gate pieces with the up pieces staged in wn
+// (ops/activation/swiglu.rs): x = g / (1 + exp(-g)) * u, the expression of
+// the separate SwiGLU kernels, so the values are theirs.
+template <int S, int XR>
+__device__ inline void act_swiglu(const ActIn &in, v4i (&xr)[XR], const v4i (&wn)[XR]) {
+    const int K4 = in.K / 4;
+#pragma unroll
+    for (int e = 0; e < XR; ++e) {
+        if ((int)threadIdx.x + S * kWave * e < K4) {
+            const float4 g = __builtin_bit_cast(float4, xr[e]);
+            const float4 u = __builtin_bit_cast(float4, wn[e]);
+            float4 y;
+            y.x = g.x / (1.0f + expf(-g.x)) * u.x;
+            y.y = g.y / (1.0f + expf(-g.y)) * u.y;
+            y.z = g.z / (1.0f + expf(-g.z)) * u.z;
+            y.w = g.w / (1.0f + expf(-g.w)) * u.w;
+            xr[e] = __builtin_bit_cast(v4i, y);
+        }
+    }
 }
 
 // The activation prologue runs after the priming of the weight ring: the

@@ -56,12 +56,16 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_int8(
     v4i wn[XR];  // RMS norm weights (row operations)
     if constexpr (FUSED && OPS) {
         if (in.norm_w) stage_load<NW, XR>(reinterpret_cast<const v4i *>(in.norm_w), n16, wn);
+        else if (in.up) stage_load<NW, XR>(reinterpret_cast<const v4i *>(in.up), n16, wn);
     }
     // activation loads before the ring's (they return first; see gemv_q8.hip)
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int s = 0; s < D; ++s)
         wr[s] = __builtin_nontemporal_load(wp + (size_t)min(c0 + s, last) * pitch);
+    if constexpr (FUSED && OPS) {
+        if (in.up) act_swiglu<NW, XR>(in, xr, wn);
+    }
     act_begin<NW, XR, FUSED, OPS>(in, n16, xr, s_act, red);
     act_end<NW, XR, FUSED, OPS>(in, false, xr, wn, s_act, red, sa_value, blockIdx.x == 0);
     if constexpr (FUSED) sa_ptr = nullptr;
@@ -196,7 +200,8 @@ bool row_ops_ok(const float *x, const RowOps &o) {
                                         o.rope_n % 2 == 0);
     const bool segs = (o.seg1 == INT_MAX || o.out1) && (o.seg2 == INT_MAX || o.out2) &&
                       o.seg1 <= o.seg2 && o.seg1 >= 0;
-    return x && al(o.norm_w) && al(o.x_out) && rope && segs;
+    const bool glu = !o.up || (al(o.up) && !o.norm_w && !o.x_out);
+    return x && al(o.norm_w) && al(o.x_out) && glu && rope && segs;
 }
 
 bool gemv_fusable(size_t m, size_t k, const float *x) {

@@ -93,6 +93,7 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     v4i wn[XR];  // RMS norm weights (row operations)
     if constexpr (FUSED && OPS) {
         if (in.norm_w) stage_load<NW, XR>(reinterpret_cast<const v4i *>(in.norm_w), n16, wn);
+        else if (in.up) stage_load<NW, XR>(reinterpret_cast<const v4i *>(in.up), n16, wn);
     }
     float sa[LR];
     if constexpr (!FUSED) {
@@ -114,6 +115,9 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
         for (int s = 0; s < NP; ++s)
             wr[u][s] = __builtin_nontemporal_load(wp + (size_t)q * LB + s * 64);
         sr[u] = sp[(size_t)q * LB];
+    }
+    if constexpr (FUSED && OPS) {
+        if (in.up) act_swiglu<NW, XR>(in, xr, wn);
     }
     act_begin<NW, XR, FUSED, OPS>(in, n16, xr, s_act, red);
     act_end<NW, XR, FUSED, OPS>(in, true, xr, wn, s_act, red, sa[0], blockIdx.x == 0);

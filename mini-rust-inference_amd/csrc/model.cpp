@@ -347,10 +347,13 @@ mri_status block(mri_llama *m, size_t li, size_t rows, size_t start, mri_kv_cach
         return row_proj(w, xrow, norm_ops(norm), out, s);
     };
     // projections whose output is added to the residual stream
-    auto out_proj = [&](const mri_weight_ref &w, const float *in, const float *norm) {
+    // (up: in is a SwiGLU gate row, applied in the projection; one row only)
+    auto out_proj = [&](const mri_weight_ref &w, const float *in, const float *norm,
+                        const float *up = nullptr) {
         if (fold) {
             RowOps o;
             o.accum = true;
+            o.up = up;
             return row_proj(w, in, o, m->x, s);
         }
         TRY(proj(w, in, rows, m->tmp, s));
@@ -418,17 +421,20 @@ mri_status block(mri_llama *m, size_t li, size_t rows, size_t start, mri_kv_cach
                          m->attn_part, s));
     TRY(out_proj(L.w[3], m->attn, L.ffn_norm));
     xrow = m->x;
-    float *act;
+    // gate rows, then up rows (one row: the SwiGLU runs in the down
+    // projection's prologue)
+    if (L.gu.ptr) TRY(in_proj(L.gu, L.ffn_norm, m->gu));
+    else {
+        TRY(in_proj(L.w[4], L.ffn_norm, m->gu));
+        TRY(in_proj(L.w[5], L.ffn_norm, m->gu + rows * g.ffn_dim));
+    }
+    if (fold) return out_proj(L.w[6], m->gu, next_norm, m->gu + g.ffn_dim);
+    float *act = m->gu;
     if (L.gu.ptr) {
-        TRY(in_proj(L.gu, L.ffn_norm, m->gu));
         act = m->act;
         TRY(launch_swiglu_rows(m->gu, rows, g.ffn_dim, act, s));
     } else {
-        act = m->gu;
-        float *up = m->gu + rows * g.ffn_dim;
-        TRY(in_proj(L.w[4], L.ffn_norm, act));
-        TRY(in_proj(L.w[5], L.ffn_norm, up));
-        TRY(launch_swiglu(act, up, rows * g.ffn_dim, act, s));
+        TRY(launch_swiglu(act, m->gu + rows * g.ffn_dim, rows * g.ffn_dim, act, s));
     }
     return out_proj(L.w[6], act, next_norm);
 }
