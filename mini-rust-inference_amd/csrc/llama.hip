@@ -494,6 +494,130 @@ __global__ __launch_bounds__(256) void k_attn_decode_part(
     if (t == 0) __hip_atomic_store(&cnt[h], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Decode form with one workgroup per head, for contexts up to
+// kDecHeadMaxL keys: no partials leave the workgroup, so the partial
+// stores, counter and combine of the split form are gone (5.7 against
+// 7.1 us at contexts of 9-72 keys, 32 heads of 128).  A head's keys then
+// stream through one CU, which at 512-575 keys is slower than the split
+// form (11.6 against 10.3 us), so longer contexts split.  The 8 waves
+// hold 32 groups of 16 lanes; in step s group G takes keys 128 s + 4 G ..
+// + 3, each lane 8 dims of each (float4 loads, 512 contiguous bytes per key
+// row).  A group keeps its own online softmax over its keys (max m, sum l,
+// output o; four keys per update), and the 32 group states are combined
+// through LDS at the end.  The next step's rows, if any, are loaded while
+// the current step is computed.  Differs from the reference's sequential
+// sums only in f32 rounding.
+constexpr int kDecHeadMaxL = 128;
+template <int HD>
+__global__ __launch_bounds__(512) void k_attn_decode_head(
+    const float *__restrict__ q, const float *__restrict__ kc, const float *__restrict__ vc,
+    int kvd, int L, int groups, float scale, float *__restrict__ out) {
+    constexpr int DPL = HD / 16;  // dims per lane
+    constexpr int V4 = DPL / 4;   // float4 per lane and key row
+    constexpr int KPG = 4;        // keys per group and step
+    constexpr int NG = 32;        // groups
+    constexpr int KPS = NG * KPG; // keys per step
+    static_assert(HD % 64 == 0 && HD <= 256, "16 lanes of float4 per key row");
+    __shared__ float s_m[NG], s_l[NG];
+    __shared__ float s_o[NG][HD + 4];
+    const int t = threadIdx.x, l = t & 63, li = l & 15;
+    const int grp = (t >> 6) * 4 + (l >> 4);
+    const int h = blockIdx.x, kh = h / groups;
+    float4 qv[V4];
+#pragma unroll
+    for (int v = 0; v < V4; ++v)
+        qv[v] = reinterpret_cast<const float4 *>(q + (size_t)h * HD + li * DPL)[v];
+    const float *kb = kc + (size_t)kh * HD + li * DPL, *vb = vc + (size_t)kh * HD + li * DPL;
+    const int nsteps = (L + KPS - 1) / KPS;
+    float4 kr[2][KPG][V4], vr[2][KPG][V4];
+    auto load = [&](auto buf, int st) __attribute__((always_inline)) {
+        constexpr int B = decltype(buf)::value;
+#pragma unroll
+        for (int k = 0; k < KPG; ++k) {
+            const size_t j = (size_t)min(st * KPS + grp * KPG + k, L - 1);
+#pragma unroll
+            for (int v = 0; v < V4; ++v) {
+                kr[B][k][v] = reinterpret_cast<const float4 *>(kb + j * kvd)[v];
+                vr[B][k][v] = reinterpret_cast<const float4 *>(vb + j * kvd)[v];
+            }
+        }
+    };
+    float m = -INFINITY, lsum = 0.0f, o[DPL];
+#pragma unroll
+    for (int d = 0; d < DPL; ++d) o[d] = 0.0f;
+    auto step = [&](auto cur, int st) __attribute__((always_inline)) {
+        constexpr int C = decltype(cur)::value;
+        if (st + 1 < nsteps) load(std::integral_constant<int, 1 - C>{}, st + 1);
+        float sc[KPG];
+#pragma unroll
+        for (int k = 0; k < KPG; ++k) {
+            float d = 0.0f;
+#pragma unroll
+            for (int v = 0; v < V4; ++v) {
+                d = d + qv[v].x * kr[C][k][v].x;
+                d = d + qv[v].y * kr[C][k][v].y;
+                d = d + qv[v].z * kr[C][k][v].z;
+                d = d + qv[v].w * kr[C][k][v].w;
+            }
+#pragma unroll
+            for (int x = 8; x > 0; x >>= 1) d = d + __shfl_xor(d, x);
+            sc[k] = st * KPS + grp * KPG + k < L ? d * scale : -INFINITY;
+        }
+        const float m_new = fmaxf(fmaxf(m, fmaxf(sc[0], sc[1])), fmaxf(sc[2], sc[3]));
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;  // then every score is -inf
+        const float alpha = expf(m - m_use);
+        float p[KPG];
+#pragma unroll
+        for (int k = 0; k < KPG; ++k) p[k] = expf(sc[k] - m_use);
+        lsum = lsum * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+#pragma unroll
+        for (int v = 0; v < V4; ++v) {
+            float4 a = {o[4 * v] * alpha, o[4 * v + 1] * alpha, o[4 * v + 2] * alpha,
+                        o[4 * v + 3] * alpha};
+#pragma unroll
+            for (int k = 0; k < KPG; ++k) {
+                a.x = a.x + p[k] * vr[C][k][v].x;
+                a.y = a.y + p[k] * vr[C][k][v].y;
+                a.z = a.z + p[k] * vr[C][k][v].z;
+                a.w = a.w + p[k] * vr[C][k][v].w;
+            }
+            o[4 * v] = a.x;
+            o[4 * v + 1] = a.y;
+            o[4 * v + 2] = a.z;
+            o[4 * v + 3] = a.w;
+        }
+        m = m_new;
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    load(I0{}, 0);
+    int st = 0;
+    for (; st + 1 < nsteps; st += 2) {
+        step(I0{}, st);
+        step(I1{}, st + 1);
+    }
+    if (st < nsteps) step(I0{}, st);
+    // combine the groups: out = sum_G c_G o_G / sum_G c_G l_G, c_G = e^(m_G - max m)
+    // (a group that saw no key has m = -inf, l = 0, o = 0; key 0 is always seen)
+    if (li == 0) {
+        s_m[grp] = m;
+        s_l[grp] = lsum;
+    }
+#pragma unroll
+    for (int d = 0; d < DPL; ++d) s_o[grp][li * DPL + d] = o[d];
+    __syncthreads();
+    if (t >= HD) return;
+    float M = -INFINITY;
+    for (int G = 0; G < NG; ++G) M = fmaxf(M, s_m[G]);
+    float den = 0.0f, num = 0.0f;
+    for (int G = 0; G < NG; ++G) {
+        const float c = expf(s_m[G] - M);
+        den = den + c * s_l[G];
+        num = num + c * s_o[G][t];
+    }
+    out[(size_t)h * HD + t] = num / den;
+}
+
 // ---- SwiGLU (ops/activation/swiglu.rs): out = gate / (1 + exp(-gate)) * up ----
 __global__ __launch_bounds__(256) void k_swiglu(const float *__restrict__ gate,
                                                 const float *__restrict__ up, size_t n,
@@ -1057,6 +1181,14 @@ mri_status attn_dispatch(const float *q, int qs, int qd, const float *kc, const 
                          int seq_q, int start_pos, int groups, int n_heads, float *out,
                          float *part, hipStream_t s) {
     const int L = start_pos + seq_q;
+    const bool rows16 =
+        (((uintptr_t)q | (uintptr_t)kc | (uintptr_t)vc) & 15) == 0 && kvd % 4 == 0;
+    if (seq_q == 1 && HD % 64 == 0 && L <= kDecHeadMaxL && rows16) {
+        hipLaunchKernelGGL(k_attn_decode_head<HD>, dim3(n_heads), dim3(512), 0, s, q, kc, vc, kvd,
+                           L, groups, 1.0f / sqrtf((float)HD), out);
+        MRI_LAUNCHED("k_attn_decode_head");
+        return MRI_OK;
+    }
     if (seq_q == 1 && part && L <= 1024 * 64) {  // the combine holds <= 1024 chunks
         const int nch = (L + 63) / 64;
         const float scale = 1.0f / sqrtf((float)HD);

@@ -4,9 +4,12 @@ hidden 4096, 32 heads of 128 (n_kv_heads = 32), SwiGLU FFN 11008, vocab
 
 This is the code the 7B layer runs and the small-model tests do not reach:
 - prefill chunks of 64 and more rows (the GEMM / skinny-above-32-rows
-  projections, k_rmsnorm over 4096 columns, k_attention over up to 130 keys);
+  projections, k_rmsnorm over 4096 columns, the matrix-core attention
+  k_attention_mfma over up to 130 keys, the second chunk at start_pos 66);
 - decode steps at contexts of 131-133 keys (three 64-key chunks of the split
-  decode attention and their combine);
+  decode attention, k_attn_decode_part, and their combine in the last
+  workgroup of each head) and, in the property test below, past 1024 keys
+  (17 chunks);
 - the decode row-operation GEMVs at their 7B sizes (the fused 12288-row
   q/k/v projection with RoPE and the cache write in its epilogue, the fused
   22016-row gate/up, down with K = 11008 adding into the residual row, the
@@ -227,3 +230,30 @@ def test_llama_7b_layer_512_prompt_128_steps_q8_0():
     f = host(full)[511:]
     for i in range(steps + 1):
         close(g[i], f[i], f"step {i} vs prefill row {511 + i}", TOL["q8_0"])
+
+
+def test_llama_7b_layer_decode_past_1024_keys_q4_0():
+    """Decode at contexts of 1029-1032 keys, where the attention splits each
+    head's keys over workgroups and the last one combines them: greedy steps
+    after a 1028-token prompt give the logits of one prefill over the same
+    1032 tokens.  Q4_0 weights (W4A32) quantize no activation, so the two
+    launch shapes differ only in f32 summation order: 1e-4 of the largest
+    logit (a lost or doubled 64-key chunk moves them by far more)."""
+    t = torch()
+    say("7B layer q4_0 1028 + 4: building")
+    _, gpu, rng = build_7b("q4_0", seed=76, max_seq=1088)
+    prompt = rng.integers(0, VOCAB, 1028).tolist()
+    steps = 4
+    glg = empty((steps + 1, VOCAB), t.float32)
+    say("7B layer q4_0 1028 + 4: generate_greedy")
+    got = gpu.generate_greedy(prompt, steps, gpu.kv_cache(), glg)
+    g = host(glg)
+    for i in range(steps + 1):
+        assert got[i] == O.argmax(g[i]), f"step {i}: not the argmax of its own logits"
+    seq = prompt + [int(v) for v in got[:steps]]
+    say("7B layer q4_0 1028 + 4: prefill of all 1032 positions")
+    full = empty((len(seq), VOCAB), t.float32)
+    gpu.forward_cached(seq, 0, gpu.kv_cache(), full)
+    f = host(full)[1027:]
+    for i in range(steps + 1):
+        close(g[i], f[i], f"step {i} vs prefill row {1027 + i}", TOL["q4_0"])
