@@ -859,11 +859,19 @@ mri_status launch_sk(const int8_t *act_packed, size_t m, const float *sa_ptr, in
 //    split (24.8 us as 128 x 128 tiles), 512 x 4096 x 4096 in 18.1 us;
 //  - 128 x 128 tiles when they fit one pass: 1024 x 4096 x 4096 in 26.2 us
 //    (36.3 us as stream-K), 256 x 11008 x 4096 in 24.4 us;
-//  - else 256 x 128 whole tiles or stream-K, by how well whole tiles fill
-//    the CUs.
+//  - else 256 x 256 stream-K when its tiles come in whole passes (no split
+//    tile: 4096 x 4096 x 4096 in 82.7 us, 92.2 as 256 x 128 whole tiles),
+//  - else the cheapest of 256 x 128 whole tiles, 128 x 192 whole tiles and
+//    256 x 128 stream-K.  A whole-tile launch takes about one tile's time per
+//    pass of the CUs, however full the last pass (~37.5 us at K = 4096 for
+//    256 x 128, ~35 for 128 x 192), and stream-K about 1.6 tile times per
+//    pass of work (its partial tiles and fix-ups): at K = 4096, N = 11008,
+//    M = 512 / 768 / 1024 / 1280 / 1536 / 2048 take 35.8 / 70.7 / 75.3 / 81.0
+//    / 115 / 127 us as 256 x 128 whole tiles, 34.2 / 66.0 / 69-76 / 105 /
+//    112 / 149 as 128 x 192 and - / 62.9 / 86 / 102 / 118 / 153 as stream-K.
 // A K split is at most 4-way, keeps at least 16 K steps per contributor
 // and at most one workgroup per CU.
-enum class GemmKind { T128x64, T128x128, T256x128, SK128, SK256 };
+enum class GemmKind { T128x64, T128x128, T128x192, T256x128, SK128, SK256 };
 struct GemmPlan {
     GemmKind kind = GemmKind::T256x128;
     int ks = 1;
@@ -893,25 +901,26 @@ GemmPlan plan_gemm(size_t m, const QMatrixDev &w) {
         pl.ks = split(t128);
         return pl;
     }
-    // Stream-K pays for split tiles (partials through memory) and for rows
-    // padded to 256; whole tiles pay for idle CUs.  Whole tiles win when
-    // they fill 60-100% of one pass; stream-K wins otherwise, with 256 x 256
-    // tiles only when they come in whole passes (no split tile).
     const size_t big = ((m + 255) / 256) * ((w.n_tiles + 7) / 8);
+    const size_t mid = mt128 * ((w.n_tiles + 11) / 12);  // 128 x 192 tiles
     pl.kind = GemmKind::T256x128;
     pl.tiles = big;
+    if (cus == 0) return pl;
     const SkShape sh4 = sk_shape(m, w, 256), sh2 = sk_shape(m, w, 128);
-    if (sh2.nwg > 0) {
-        const double fill = (double)big / sh2.nwg;
-        if (!(fill <= 1.0 && fill >= 0.6)) {
-            if (sh4.nwg > 0 && sh4.n_tt >= sh4.nwg && sh4.n_tt % sh4.nwg == 0) {
-                pl.kind = GemmKind::SK256;
-                pl.sk = sh4;
-            } else {
-                pl.kind = GemmKind::SK128;
-                pl.sk = sh2;
-            }
-        }
+    if (sh4.nwg > 0 && sh4.n_tt >= sh4.nwg && sh4.n_tt % sh4.nwg == 0) {
+        pl.kind = GemmKind::SK256;
+        pl.sk = sh4;
+        return pl;
+    }
+    auto passes = [&](size_t tiles) { return (double)((tiles + cus - 1) / cus); };
+    const double t_big = passes(big), t_mid = 0.94 * passes(mid);
+    const double t_sk = sh2.nwg > 0 ? 1.6 * (double)big / (double)cus : 1e30;
+    if (t_mid < t_big && t_mid <= t_sk) {
+        pl.kind = GemmKind::T128x192;
+        pl.tiles = mid;
+    } else if (t_sk < t_big) {
+        pl.kind = GemmKind::SK128;
+        pl.sk = sh2;
     }
     return pl;
 }
@@ -969,6 +978,10 @@ mri_status launch_gemm_int8(const int8_t *act_packed, size_t m, const float *sa_
         case GemmKind::T128x128:
             st = launch<128, 128, 2, 2, 8, 8>(act_packed, m, sa_ptr, sa_stride, sa_value, w, out,
                                               acc_out, s, pl.ks, ws);
+            break;
+        case GemmKind::T128x192:
+            st = launch<128, 192, 2, 2, 4, 8>(act_packed, m, sa_ptr, sa_stride, sa_value, w, out,
+                                              acc_out, s);
             break;
         default:
             st = launch<256, 128, 4, 2, 4, 8>(act_packed, m, sa_ptr, sa_stride, sa_value, w, out,

@@ -149,7 +149,13 @@ def test_matmul_int8_bit_exact(m, n, k):
                                    # 4-way (129 x 2000); 128 x 64 2-way at 256 x 4096,
                                    # 128 x 128 whole at 192 x 11008
                                    (100, 1000, 4096), (200, 300, 2048), (129, 2000, 4096),
-                                   (256, 4096, 4096), (192, 11008, 4096)])
+                                   (256, 4096, 4096), (192, 11008, 4096),
+                                   # the larger plans: 128 x 192 whole tiles (512 and
+                                   # 1536 x 11008), 256 x 128 stream-K (768 x 11008),
+                                   # 256 x 128 whole (1280 x 11008), 256 x 256 stream-K
+                                   # in whole passes (4096 x 4096)
+                                   (768, 11008, 4096), (1536, 11008, 4096), (1280, 11008, 4096),
+                                   (4096, 4096, 4096)])
 def test_matmul_int8_prefill_closed_form(m, n, k):
     """Prefill-sized matmul_int8 (int8.rs:61-98) at full shapes: the int32
     accumulators against an exact float64 matmul (|sum| <= 127^2 * K < 2^53)
@@ -178,7 +184,8 @@ def test_matmul_int8_prefill_back_to_back():
     t = torch()
     cases = []
     for m, n, k in [(300, 200, 1024), (2048, 512, 4096), (300, 200, 1024), (1024, 4096, 4096),
-                    (2048, 512, 4096), (100, 1000, 4096), (200, 300, 2048), (100, 1000, 4096)]:
+                    (2048, 512, 4096), (100, 1000, 4096), (200, 300, 2048), (100, 1000, 4096),
+                    (768, 11008, 4096), (512, 11008, 4096), (768, 11008, 4096)]:
         rng = np.random.default_rng(m * 5 + n + k)
         wq = rng.integers(-127, 128, (n, k)).astype(np.int8)
         ws = rng.uniform(1e-4, 1e-3, n).astype(F32)
