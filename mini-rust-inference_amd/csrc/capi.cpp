@@ -146,8 +146,8 @@ mri_status gemm_ws_get(hipStream_t stream, size_t bytes, void **ptr) {
     return zeroed_ws_get(g_ws, stream, bytes, ptr);
 }
 
-mri_status argmax_ws_get(hipStream_t stream, void **ptr) {
-    return zeroed_ws_get(g_aws, stream, kArgmaxWsBytes, ptr);
+mri_status argmax_ws_get(hipStream_t stream, void **ptr, size_t bytes) {
+    return zeroed_ws_get(g_aws, stream, std::max(bytes, kArgmaxWsBytes), ptr);
 }
 
 static inline bool aligned(const void *p, size_t a) {

@@ -112,6 +112,17 @@ struct Q8MatrixDev {
 
 // Exact f16 -> f32 decode (v_cvt_f32_f16), the f16_to_f32 of
 // gguf/quantization.rs:416-459 for every finite input.
+// The greedy argmax's order (sampling/mod.rs:144-151, max_by over
+// partial_cmp) as one 64-bit key: the value's bits mapped to an unsigned
+// order (-0 counted as +0), then the index, so equal values go to the larger
+// index; NaN gets key 0, below every value (it is never chosen).
+__device__ inline unsigned long long argmax_key(float v, int n) {
+    if (v != v) return 0ull;
+    const unsigned b = __float_as_uint(v == 0.0f ? 0.0f : v);
+    const unsigned ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((unsigned long long)ord << 32) | (unsigned)n;
+}
+
 __device__ inline float f16_bits_to_f32(unsigned bits) {
     return (float)__builtin_bit_cast(_Float16, (unsigned short)bits);
 }
@@ -238,6 +249,12 @@ struct RowOps {
     // x / (1 + exp(-x)) * up elementwise (ops/activation/swiglu.rs), computed
     // as the separate SwiGLU kernel does (not with norm_w or x_out).
     const float *up = nullptr;
+    // First half of the greedy argmax of the output row (sampling/mod.rs:
+    // 144-151): each 16-channel tile T writes the largest key of its outputs
+    // to arg_keys[T] (argmax_key: the order of the reference's max_by, the
+    // last of equal maxima, NaN never chosen; 0 for no candidate), and
+    // launch_argmax_keys reduces them.
+    unsigned long long *arg_keys = nullptr;
     // RoPE (ops/rope.rs) on output channels [0, rope_n): the pairs
     // (2i, 2i+1) of each head of hd channels rotate by the table entries
     // i % (hd/2) of rope_cos / rope_sin (one position's rows).
@@ -247,7 +264,9 @@ struct RowOps {
     // out2[n - seg2] (q | k | v of a fused projection into the KV cache).
     int seg1 = INT_MAX, seg2 = INT_MAX;
     float *out1 = nullptr, *out2 = nullptr;
-    bool any() const { return norm_w || x_out || accum || up || rope_n > 0 || out1 || out2; }
+    bool any() const {
+        return norm_w || x_out || accum || up || arg_keys || rope_n > 0 || out1 || out2;
+    }
 };
 bool gemv_int8_supported(bool fused, size_t m, size_t n_tiles, size_t k, size_t kp);
 // The device matrices behind the public handles (capi.cpp).
@@ -371,7 +390,13 @@ mri_status launch_add(const float *a, const float *b, size_t n, float *out, hipS
 // stream's argmax workspace (argmax_ws_get: kArgmaxWsBytes, zeroed).
 mri_status launch_argmax(const float *v, size_t rows, size_t n, uint32_t *idx, hipStream_t s);
 constexpr size_t kArgmaxWsBytes = 4096;
-mri_status argmax_ws_get(hipStream_t stream, void **ptr);
+mri_status argmax_ws_get(hipStream_t stream, void **ptr, size_t bytes = kArgmaxWsBytes);
+// Reduces n keys of argmax_key (arg_keys of a one-row projection, one per
+// 16-channel tile) to the index of the largest (0 when every key is 0) in
+// idx[0]; with table, copies that row of table ([*][d] f32, 16-byte aligned,
+// d % 4 == 0) to x_out.
+mri_status launch_argmax_keys(const unsigned long long *keys, size_t n, uint32_t *idx,
+                              const float *table, size_t d, float *x_out, hipStream_t s);
 // One row: the argmax, then row idx of table ([*][d]) copied to x_out.
 mri_status launch_argmax_embed(const float *v, size_t n, uint32_t *idx, const float *table,
                                size_t d, float *x_out, hipStream_t s);

@@ -99,6 +99,7 @@ struct ActIn {
     float eps = 0.0f;
     float *x_out = nullptr;         // optional [K], 16-byte aligned (fused path)
     const float *up = nullptr;      // optional [K]: x is a SwiGLU gate row (fused path)
+    unsigned long long *arg_keys = nullptr;  // optional: per-tile argmax keys (RowOps)
     int accum = 0;
     const float *rope_cos = nullptr, *rope_sin = nullptr;
     int rope_n = 0, hd = 2, seg1 = INT_MAX, seg2 = INT_MAX;
@@ -106,7 +107,7 @@ struct ActIn {
 
     ActIn(const float *x_, const int8_t *act_, int k, int8_t *aq, float *so, const RowOps &o)
         : x(x_), act(act_), K(k), act_q_out(aq), scale_out(so), norm_w(o.norm_w), eps(o.eps),
-          x_out(o.x_out), up(o.up), accum(o.accum ? 1 : 0), rope_cos(o.rope_cos), rope_sin(o.rope_sin),
+          x_out(o.x_out), up(o.up), arg_keys(o.arg_keys), accum(o.accum ? 1 : 0), rope_cos(o.rope_cos), rope_sin(o.rope_sin),
           rope_n(o.rope_n), hd(o.hd), seg1(o.seg1), seg2(o.seg2), out1(o.out1), out2(o.out2) {}
 };
 
@@ -124,6 +125,21 @@ __device__ inline void row_store(const ActIn &in, float *out, int n, float v, fl
              : n >= in.seg1 ? in.out1 + (n - in.seg1)
                             : out + n;
     *o = in.accum ? *o + v : v;
+}
+
+// Greedy argmax keys in the epilogue of a one-row projection, called by the
+// one wave of tile T that holds its outputs (lanes with mine set hold
+// channel n's value v): the tile's largest argmax_key goes to keys[T].
+__device__ inline void row_argmax_key(unsigned long long *keys, int T, float v, int n,
+                                      bool mine) {
+    unsigned long long key = mine ? argmax_key(v, n) : 0ull;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const unsigned lo = __shfl_xor((unsigned)key, o), hi = __shfl_xor((unsigned)(key >> 32), o);
+        const unsigned long long ok = ((unsigned long long)hi << 32) | lo;
+        key = ok > key ? ok : key;
+    }
+    if ((threadIdx.x & 63) == 0) keys[T] = key;
 }
 
 // Each thread stages XR 16-byte pieces of the activations in registers:

@@ -115,9 +115,12 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_int8(
         float v = (float)acc[0] * sa_value;
         v = v * wscales[min(n, N - 1)];
         const float pv = __shfl_xor(v, 1);
-        if (g != 0 || n >= N) return;
-        if (acc_out) acc_out[n] = acc[0];
-        row_store(in, out, n, v, pv);
+        const bool mine = g == 0 && n < N;
+        if (mine) {
+            if (acc_out) acc_out[n] = acc[0];
+            row_store(in, out, n, v, pv);
+        }
+        if (in.arg_keys) row_argmax_key(in.arg_keys, T, v, n, mine);
         return;
     }
     if (n >= N || g != 0) return;
@@ -201,7 +204,8 @@ bool row_ops_ok(const float *x, const RowOps &o) {
     const bool segs = (o.seg1 == INT_MAX || o.out1) && (o.seg2 == INT_MAX || o.out2) &&
                       o.seg1 <= o.seg2 && o.seg1 >= 0;
     const bool glu = !o.up || (al(o.up) && !o.norm_w && !o.x_out);
-    return x && al(o.norm_w) && al(o.x_out) && glu && rope && segs;
+    const bool arg = !o.arg_keys || (reinterpret_cast<uintptr_t>(o.arg_keys) & 7) == 0;
+    return x && al(o.norm_w) && al(o.x_out) && glu && arg && rope && segs;
 }
 
 bool gemv_fusable(size_t m, size_t k, const float *x) {

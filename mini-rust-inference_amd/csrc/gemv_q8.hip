@@ -229,6 +229,7 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     if constexpr (OPS) {  // one row: lanes 0-15 hold channels 16T .. 16T+15
         const float pv = __shfl_xor(fs[0], 1);
         if (g == 0 && n < N) row_store(in, out, n, fs[0], pv);
+        if (in.arg_keys) row_argmax_key(in.arg_keys, T, fs[0], n, g == 0 && n < N);
         return;
     }
     if (g >= LG || n >= N) return;

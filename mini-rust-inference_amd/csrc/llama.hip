@@ -735,6 +735,35 @@ __device__ inline bool arg_better(float ov, int oi, float bv, int bi) {
     return oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi > bi));
 }
 
+// The second half of the fused greedy argmax: the largest of n keys
+// (argmax_key, one per 16-channel tile of the output projection) in one
+// workgroup; writes its index (0 when every key is 0, i.e. every value
+// NaN) and, with table, copies that row of table to x_out.
+__global__ __launch_bounds__(256) void k_argmax_keys(const unsigned long long *__restrict__ keys,
+                                                     int n, uint32_t *__restrict__ idx,
+                                                     const float *__restrict__ table, int d,
+                                                     float *__restrict__ x_out) {
+    __shared__ unsigned long long s_k[4];
+    unsigned long long k = 0;
+    for (int i = threadIdx.x; i < n; i += 256) k = keys[i] > k ? keys[i] : k;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const unsigned lo = __shfl_xor((unsigned)k, o), hi = __shfl_xor((unsigned)(k >> 32), o);
+        const unsigned long long ok = ((unsigned long long)hi << 32) | lo;
+        k = ok > k ? ok : k;
+    }
+    if ((threadIdx.x & 63) == 0) s_k[threadIdx.x >> 6] = k;
+    __syncthreads();
+    k = s_k[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) k = s_k[w] > k ? s_k[w] : k;
+    const uint32_t id = k ? (uint32_t)k : 0u;
+    if (threadIdx.x == 0) idx[0] = id;
+    if (!table) return;
+    const float4 *src = reinterpret_cast<const float4 *>(table + (size_t)id * d);
+    for (int i = threadIdx.x; i < d / 4; i += 256) reinterpret_cast<float4 *>(x_out)[i] = src[i];
+}
+
 // One row split over the blocks: block b reduces its slice, stores its
 // (value, index) and counts itself; the block that counts last combines
 // the gridDim.x <= 64 candidates, writes idx[0], resets the counter, and
@@ -800,10 +829,12 @@ __global__ __launch_bounds__(256) void k_argmax_split(const float *__restrict__ 
         __hip_atomic_store(&part_v[blockIdx.x], __float_as_int(bv), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(&part_i[blockIdx.x], bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the candidate has reached the device
-        // release: publishes this block's candidate; acquire: the last block
-        // reads every candidate after it
-        s_last = __hip_atomic_fetch_add(count, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_SYSTEM) ==
+        // the candidate (device-scope atomic stores) is at the point of
+        // coherence of all XCDs before the count; the last block reads the
+        // candidates with device-scope atomic loads, which do not hit lines
+        // its XCD's L2 cached before
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        s_last = __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                  gridDim.x - 1;
     }
     __syncthreads();
@@ -829,7 +860,7 @@ __global__ __launch_bounds__(256) void k_argmax_split(const float *__restrict__ 
         if (b == 0) {
             idx[0] = ci < 0 ? 0u : (uint32_t)ci;
             s_tok = ci < 0 ? 0 : ci;
-            __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
     if (!table) return;
@@ -1429,6 +1460,16 @@ static mri_status launch_argmax_split(const float *v, size_t n, uint32_t *idx,
     hipLaunchKernelGGL(k_argmax_split, dim3(blocks), dim3(256), 0, s, v, (int)n, idx, table,
                        (int)d, x_out, static_cast<unsigned *>(ws));
     MRI_LAUNCHED("k_argmax_split");
+    return MRI_OK;
+}
+
+mri_status launch_argmax_keys(const unsigned long long *keys, size_t n, uint32_t *idx,
+                              const float *table, size_t d, float *x_out, hipStream_t s) {
+    if (table && (d % 4 || !al16(table) || !al16(x_out)))
+        return set_error(MRI_ERR_INVALID_ARGUMENT, "argmax: table rows must be float4-aligned");
+    hipLaunchKernelGGL(k_argmax_keys, dim3(1), dim3(256), 0, s, keys, (int)n, idx, table, (int)d,
+                       x_out);
+    MRI_LAUNCHED("k_argmax_keys");
     return MRI_OK;
 }
 

@@ -446,9 +446,11 @@ mri_status block(mri_llama *m, size_t li, size_t rows, size_t start, mri_kv_cach
 // or already in m->x (kInX, written by the previous step's argmax).
 enum class Emb { kDevice, kHost, kInX };
 
+// arg: for a folded row, the greedy argmax (and next embedding row) that the
+// output projection's epilogue computes (the RowOps arg_* fields).
 mri_status run_rows(mri_llama *m, const uint32_t *tok_dev, size_t rows, size_t start,
                     mri_kv_cache *c, float *logits, hipStream_t s, Emb emb = Emb::kDevice,
-                    uint32_t host_tok = 0) {
+                    uint32_t host_tok = 0, const RowOps *arg = nullptr) {
     const mri_llama_config &g = m->cfg;
     const bool fold = rows == 1 && row_path(m);
     const float *first = g.n_layers ? m->layers[0].attn_norm : m->out_norm;
@@ -474,6 +476,7 @@ mri_status run_rows(mri_llama *m, const uint32_t *tok_dev, size_t rows, size_t s
     RowOps o;
     o.norm_w = m->out_norm;
     o.eps = g.eps;
+    if (arg) o.arg_keys = arg->arg_keys;
     return row_proj(m->output, g.n_layers ? m->x : x_in, o, logits, s);
 }
 
@@ -689,17 +692,33 @@ mri_status mri_llama_generate_greedy(mri_llama *m, const uint32_t *prompt, size_
     if (logits_out)
         MRI_HIP(hipMemcpyAsync(logits_out, last, V * sizeof(float), hipMemcpyDeviceToDevice, s));
     // folded decode rows: each argmax also gathers the chosen token's
-    // embedding row into m->x for the next step
+    // embedding row into m->x for the next step; after the prompt by its own
+    // kernel, after each decode row in the output projection's epilogue
     const bool fold = row_path(m);
     auto pick = [&](const float *lg, uint32_t *id, bool next) {
         return fold && next ? launch_argmax_embed(lg, V, id, m->embd, m->cfg.dim, m->x, s)
                             : launch_argmax(lg, 1, V, id, s);
     };
     TRY(pick(last, m->gen, n_steps > 0));
+    // the decode rows' argmax keys (one per 16-channel tile of the output
+    // projection), after the split argmax's words in its workspace
+    void *aws = nullptr;
+    const size_t n_keys = (V + kTileN - 1) / kTileN;
+    if (fold && n_steps) TRY(argmax_ws_get(s, &aws, kArgmaxWsBytes + n_keys * 8));
+    auto *keys = reinterpret_cast<unsigned long long *>(static_cast<char *>(aws) + kArgmaxWsBytes);
     for (size_t i = 0; i < n_steps; ++i) {
         float *lg = logits_out ? logits_out + (i + 1) * V : m->logits_buf;
-        TRY(run_rows(m, m->gen + i, 1, n_prompt + i, c, lg, s, Emb::kInX));
-        TRY(pick(lg, m->gen + i + 1, i + 1 < n_steps));
+        if (fold) {
+            RowOps arg;
+            arg.arg_keys = keys;
+            TRY(run_rows(m, m->gen + i, 1, n_prompt + i, c, lg, s, Emb::kInX, 0, &arg));
+            const bool next = i + 1 < n_steps;
+            TRY(launch_argmax_keys(keys, n_keys, m->gen + i + 1, next ? m->embd : nullptr,
+                                   m->cfg.dim, m->x, s));
+        } else {
+            TRY(run_rows(m, m->gen + i, 1, n_prompt + i, c, lg, s, Emb::kInX));
+            TRY(pick(lg, m->gen + i + 1, i + 1 < n_steps));
+        }
     }
     MRI_HIP(hipMemcpyAsync(tokens_out, m->gen, (n_steps + 1) * sizeof(uint32_t),
                            hipMemcpyDeviceToHost, s));

@@ -38,9 +38,11 @@ MIXED = {"wq": "int8", "wk": "q8_0", "wv": "w4a8", "wo": "q8_0", "wgate": "w4a8"
          "wdown": "int8", "out": "q8_0"}
 
 
-def build(fmt, seed=0, d=256, nh=4, nkv=2, ffn=512, vocab=300, max_seq=48, n_layers=2):
+def build(fmt, seed=0, d=256, nh=4, nkv=2, ffn=512, vocab=300, max_seq=48, n_layers=2,
+          out_w=None):
     """The same random model on both sides (fmt "mixed": a different format
-    per projection role, MIXED)."""
+    per projection role, MIXED); out_w: the output projection's f32 weights
+    instead of random ones."""
     L, Q = mods()
     rng = np.random.default_rng(seed)
     hd = d // nh
@@ -52,8 +54,9 @@ def build(fmt, seed=0, d=256, nh=4, nkv=2, ffn=512, vocab=300, max_seq=48, n_lay
             return proj_fmt(MIXED[role], n, k)
         return proj_fmt(fmt, n, k)
 
-    def proj_fmt(fmt, n, k):
-        w = (rng.standard_normal((n, k)) * 0.05).astype(F32)
+    def proj_fmt(fmt, n, k, w=None):
+        if w is None:
+            w = (rng.standard_normal((n, k)) * 0.05).astype(F32)
         if fmt == "int8":
             data, scales = O.quantize_per_channel(w, n, k)
             return O.Proj("int8", n, k, data, scales), Q.QMatrix.from_host(data, scales)
@@ -78,7 +81,10 @@ def build(fmt, seed=0, d=256, nh=4, nkv=2, ffn=512, vocab=300, max_seq=48, n_lay
         g_layers.append(gl)
     embd = rng.standard_normal((vocab, d)).astype(F32)
     onorm = rng.uniform(0.8, 1.2, d).astype(F32)
-    o_out, g_out = proj(vocab, d)
+    if out_w is None:
+        o_out, g_out = proj(vocab, d)
+    else:
+        o_out, g_out = proj_fmt(MIXED["out"] if fmt == "mixed" else fmt, vocab, d, out_w)
     oracle = O.LlamaOracle(cfg, embd, o_layers, onorm, o_out)
     gpu = L.Llama(cfg, embd, onorm, g_out, g_layers)
     return oracle, gpu, rng
@@ -204,6 +210,29 @@ def test_llama_generate_greedy(fmt):
         assert toks[i] == O.argmax(g[i])  # the GPU picked its own argmax
         margin = ref[i].max() - ref[i][toks[i]]
         assert margin <= TOL[fmt] * np.abs(ref[i]).max(), f"step {i}: margin {margin}"
+
+
+@pytest.mark.parametrize("fmt", ["q8_0", "int8"])
+def test_llama_generate_greedy_ties(fmt):
+    """The greedy loop's argmax (in the output projection's epilogue) on
+    ties: only rows 7 and 123 of the output weights are non-zero, and equal,
+    so those two logits are equal and every other one is exactly zero; each
+    step must choose the last of its equal maxima (123 when their value is
+    positive, else 299), as the reference's max_by does."""
+    t = torch()
+    rng = np.random.default_rng(21)
+    w = np.zeros((300, 256), F32)
+    w[7] = w[123] = (rng.standard_normal(256) * 0.05).astype(F32)
+    _, gpu, rng = build(fmt, seed=12, out_w=w)
+    prompt = rng.integers(0, 300, 9).tolist()
+    steps = 6
+    lg = empty((steps + 1, 300), t.float32)
+    toks = gpu.generate_greedy(prompt, steps, gpu.kv_cache(), lg)
+    g = host(lg)
+    for i in range(steps + 1):
+        assert g[i][7] == g[i][123] and np.count_nonzero(g[i]) <= 2
+        want = 123 if g[i][123] > 0 else 299
+        assert toks[i] == want == O.argmax(g[i]), f"step {i}: {toks[i]} (logit {g[i][123]})"
 
 
 def test_argmax_last_of_ties():
