@@ -32,6 +32,14 @@ namespace {
 // block dots are exact.  (Keeping the reference's order needed an LDS
 // barrier per round and measured ~0.3 us slower at [1,4096]x[4096,11008].)
 //
+// LAZY (the plain fused row, 512-1023 tiles): the prologue stages the f32
+// row in LDS and reduces max|x| (one barrier) without quantizing it; each
+// wave then quantizes only the laps it consumes, one lap (4 values a lane,
+// the same round-half-away and clamp) into a 256-byte area of its own,
+// after the previous lap's MFMAs and refills, while the next lap is in
+// flight.  Every workgroup re-quantizes the row it uses; quantizing it all
+// up front put that VALU work ahead of every wave's first lap.
+//
 // W4: a lap's quants are two 16-byte loads per lane instead of four; the B
 // operand of a chunk is unpacked from two u32 words by moving each nibble
 // to the high half of its byte, which gives 16 * quant as int8 (the stored
@@ -39,7 +47,8 @@ namespace {
 // is 16 times the block dot and an arithmetic shift by 4 recovers it.
 // ---------------------------------------------------------------------------
 
-template <int MR, int S, int TPW, int RL, int XR, bool FUSED, bool OPS, bool DEBUG, bool W4>
+template <int MR, int S, int TPW, int RL, int XR, bool FUSED, bool OPS, bool DEBUG, bool W4,
+          bool LAZY = false>
 __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     ActIn in, int M, int kp, const float *__restrict__ sa_rows,
     const v4i *__restrict__ laps, int N, int n_tiles, int G, int nb, float *__restrict__ out,
@@ -48,6 +57,7 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     constexpr int LR = MR == 1 ? 1 : 2;       // rows per result lane
     constexpr int LG = (MR + 1) / 2;          // lane groups holding results
     static_assert(!FUSED || MR == 1, "the fused prologue quantizes one row");
+    static_assert(!LAZY || (FUSED && !OPS), "lap-wise quantization: the plain fused row");
     extern __shared__ v4i s_lds[];
     const int wl = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int tw_ = wl / S;                   // tile of the wave within the WG
@@ -67,10 +77,14 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     const v4i *sp = laps + (size_t)Tc * G * LB + SO + r;
     const int n = T * 16 + r;
 
-    // LDS: [act M*kp][red NW floats][wave sums TPW x (S-1) x LG x 16 x LR floats]
+    // LDS: [act M*kp int8, or with LAZY the f32 row (kp floats)][red NW
+    // floats][wave sums TPW x (S-1) x LG x 16 x LR floats][LAZY: one
+    // quantized lap (256 bytes) per wave]
     int8_t *s_act = reinterpret_cast<int8_t *>(s_lds);
-    float *red = reinterpret_cast<float *>(s_act + (size_t)M * kp);
+    float *red = reinterpret_cast<float *>(s_act + (size_t)(LAZY ? 4 : M) * kp);
     float *sums = red + 4 * NW;
+    int8_t *s_lap = reinterpret_cast<int8_t *>(sums + (size_t)TPW * (S - 1) * LG * 16 * LR) +
+                    (size_t)wl * 256;
     auto sslot = [&](int ww) {  // sums of wave ww >= 1 of this tile, this lane
         return sums + ((((size_t)tw_ * (S - 1) + (ww - 1)) * LG + (g < LG ? g : 0)) * 16 + r) * LR;
     };
@@ -81,7 +95,7 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     const bool aval = arow < M;
     const int mlo = (aval && !(r & 1)) ? -1 : 0;
     const int mhi = (aval && (r & 1)) ? -1 : 0;
-    const v4i *ap = reinterpret_cast<const v4i *>(s_act + (size_t)(aval ? arow : 0) * kp) + g;
+    const v4i *ap = reinterpret_cast<const v4i *>(LAZY ? s_lap : s_act + (size_t)(aval ? arow : 0) * kp) + g;
 
     v4i wr[RL][4];
     v4i sr[RL];
@@ -119,8 +133,49 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     if constexpr (FUSED && OPS) {
         if (in.up) act_swiglu<NW, XR>(in, xr, wn);
     }
-    act_begin<NW, XR, FUSED, OPS>(in, n16, xr, s_act, red);
-    act_end<NW, XR, FUSED, OPS>(in, true, xr, wn, s_act, red, sa[0], blockIdx.x == 0);
+    float inv = 0.0f;  // LAZY: 1 / scale of the row
+    if constexpr (LAZY) {
+        // the per-wave max|x| as act_begin computes it, the f32 pieces into
+        // LDS, one barrier, then the row scale as act_end computes it; each
+        // wave quantizes the laps it consumes, one at a time (quant_lap)
+        const int t = threadIdx.x, K4 = in.K / 4;
+        v4i *s_x4 = reinterpret_cast<v4i *>(s_act);
+        float mx = 0.0f;
+#pragma unroll
+        for (int e = 0; e < XR; ++e) {
+            if (t + NW * kWave * e < K4) {
+                const float4 v = __builtin_bit_cast(float4, xr[e]);
+                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+                s_x4[t + NW * kWave * e] = xr[e];
+            }
+        }
+        mx = wave_max(mx);
+        if ((t & 63) == 0) red[t >> 6] = mx;
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        mx = 0.0f;
+#pragma unroll
+        for (int s = 0; s < NW; ++s) mx = fmaxf(mx, red[s]);
+        sa[0] = mx == 0.0f ? 1.0f : __fdiv_rn(mx, 127.0f);
+        inv = __fdiv_rn(1.0f, sa[0]);
+        if (blockIdx.x == 0 && t == 0 && in.scale_out) in.scale_out[0] = sa[0];
+    } else {
+        act_begin<NW, XR, FUSED, OPS>(in, n16, xr, s_act, red);
+        act_end<NW, XR, FUSED, OPS>(in, true, xr, wn, s_act, red, sa[0], blockIdx.x == 0);
+    }
+    // LAZY: quantize lap q of the row (lane l: elements 256q + 4l .. + 3,
+    // zero past K) into this wave's 256-byte area, chunk-permuted
+    auto quant_lap = [&](int q) __attribute__((always_inline)) {
+        const int kk = 256 * q + 4 * l;
+        const float4 v = kk < in.K ? reinterpret_cast<const float4 *>(s_act)[kk >> 2]
+                                   : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        const int packed = (round_clamp_i8(v.x * inv) & 255) | ((round_clamp_i8(v.y * inv) & 255) << 8) |
+                           ((round_clamp_i8(v.z * inv) & 255) << 16) | (round_clamp_i8(v.w * inv) << 24);
+        *reinterpret_cast<int *>(s_lap + ((4 * l) & ~63) + q8_perm((4 * l) & 63)) = packed;
+    };
+    if constexpr (LAZY) {
+        if (nq > 0) quant_lap(w);
+    }
     float fs[LR];
 #pragma unroll
     for (int j = 0; j < LR; ++j) fs[j] = 0.0f;
@@ -133,7 +188,7 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
         const int q = L * S + w;
         v4i a[4];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) a[s] = ap[(size_t)(4 * q + s) * 4];
+        for (int s = 0; s < 4; ++s) a[s] = ap[(size_t)((LAZY ? 0 : 4 * q) + s) * 4];
         int dt[4][2 * LR];
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
@@ -193,6 +248,9 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
             }
         }
         if (refill) sr[U] = sp[(size_t)(q + RL * S) * LB];
+        if constexpr (LAZY) {
+            if (L + 1 < nq) quant_lap(q + S);  // while the next laps are in flight
+        }
     };
 
     using T1 = std::true_type;
@@ -379,18 +437,29 @@ __global__ __launch_bounds__(S * kWave) void k_gemv_w4a32(
     }
 }
 
+// Lap-wise quantization of the fused row (k_gemv_q8_0's LAZY instances):
+// waves per tile and laps in flight.  Measured at [1,4096]x[4096,11008]
+// (688 tiles): 9.07-9.11 us against 9.30-9.34 for the row quantized into
+// LDS up front; 8 waves 9.7-9.9, 16 waves 11.1.  At 2000 tiles (4096 ->
+// 32000) it was slower (22.3 against 21.6 us), so it stops at 1024 tiles.
+constexpr int kLazyS = 4;
+constexpr int kLazyRL = 1;
+constexpr size_t kLazyMaxTiles = 1024;
+
 struct CfgQ8 {
     int s = 0, tpw = 1, rl = 1, xr = 0;  // s == 0: unsupported
+    bool lazy = false;                    // lap-wise quantization of the fused row
 };
 
 // Rows of the Q8_0 kernel instance for m rows: 1, 2 or 4.
 inline int mr_of(size_t m) { return m <= 1 ? 1 : m == 2 ? 2 : 4; }
 
-size_t lds_q8(int s, int tpw, size_t m, size_t kp, size_t G) {
+size_t lds_q8(int s, int tpw, size_t m, size_t kp, size_t G, bool lazy = false) {
     (void)G;
     const size_t mr = (size_t)mr_of(m);
     const size_t lr = mr == 1 ? 1 : 2, lg = (mr + 1) / 2;
-    return m * kp + (size_t)s * tpw * 16 + (size_t)tpw * (s - 1) * lg * 16 * lr * 4;
+    return (lazy ? 4 : m) * kp + (size_t)s * tpw * 16 + (size_t)tpw * (s - 1) * lg * 16 * lr * 4 +
+           (lazy ? (size_t)s * tpw * 256 : 0);
 }
 
 // Activation pieces per thread of the instances with S waves per tile.
@@ -401,8 +470,18 @@ inline int xr_large(int s) { return 48 / s; }
 // K = 4096 and 11008): four waves per tile and one lap in flight per wave
 // from 512 tiles up; below, more waves per tile (8 at K <= 4096, 16 above)
 // with two laps in flight, so that the launch still has >= 2048 waves.
-CfgQ8 pick_q8(bool fused, size_t n_tiles, size_t m, size_t k, size_t kp, size_t G) {
+CfgQ8 pick_q8(bool fused, size_t n_tiles, size_t m, size_t k, size_t kp, size_t G,
+              bool ops = false) {
     CfgQ8 c;
+    if (fused && !ops && m == 1 && n_tiles >= 512 && n_tiles < kLazyMaxTiles) {
+        CfgQ8 z;
+        z.s = kLazyS;
+        z.rl = kLazyRL;
+        z.lazy = true;
+        const size_t nx = ceil_div(k / 4, (size_t)z.s * kWave);
+        z.xr = nx <= (size_t)xr_small(z.s) ? xr_small(z.s) : nx <= (size_t)xr_large(z.s) ? xr_large(z.s) : 0;
+        if (z.xr != 0 && lds_q8(z.s, z.tpw, m, kp, G, true) <= kMaxLds) return z;
+    }
     if (n_tiles >= 512) {
         c.s = 4;
         c.rl = 1;
@@ -420,13 +499,14 @@ CfgQ8 pick_q8(bool fused, size_t n_tiles, size_t m, size_t k, size_t kp, size_t 
 
 inline size_t groups_of(const Q8MatrixDev &w) { return w.laps_per_tile(); }
 
-template <int MR, int S, int TPW, int RL, int XR, bool FUSED, bool OPS, bool DEBUG, bool W4>
+template <int MR, int S, int TPW, int RL, int XR, bool FUSED, bool OPS, bool DEBUG, bool W4,
+          bool LAZY = false>
 void launch_q8(ActIn in, size_t m, const float *sa_rows, const Q8MatrixDev &w,
                float *out, int32_t *block_dots, hipStream_t st) {
     const size_t G = groups_of(w);
-    hipLaunchKernelGGL((k_gemv_q8_0<MR, S, TPW, RL, XR, FUSED, OPS, DEBUG, W4>),
+    hipLaunchKernelGGL((k_gemv_q8_0<MR, S, TPW, RL, XR, FUSED, OPS, DEBUG, W4, LAZY>),
                        dim3((unsigned)ceil_div(w.n_tiles, TPW)), dim3(S * TPW * kWave),
-                       lds_q8(S, TPW, m, w.kp, G), st, in, (int)m, (int)w.kp, sa_rows,
+                       lds_q8(S, TPW, m, w.kp, G, LAZY), st, in, (int)m, (int)w.kp, sa_rows,
                        reinterpret_cast<const v4i *>(w.laps), (int)w.n_out,
                        (int)w.n_tiles, (int)G, (int)w.n_blocks, out, block_dots);
 }
@@ -440,6 +520,21 @@ void dispatch_q8(CfgQ8 c, ActIn in, size_t m, const float *sa_rows, const Q8Matr
                           in, m, sa_rows, w, out, block_dots, st)                          \
                     : launch_q8<MR, S_, TPW_, RL_, XR_, FUSED, OPS, DEBUG, false>(         \
                           in, m, sa_rows, w, out, block_dots, st);
+    if constexpr (FUSED && !OPS && MR == 1) {
+        if (c.lazy) {
+            const int xs = xr_small(kLazyS), xl = xr_large(kLazyS);
+            if (c.xr == xs)
+                return w.w4 ? launch_q8<1, kLazyS, 1, kLazyRL, 16 / kLazyS, true, false, DEBUG, true, true>(
+                                  in, m, sa_rows, w, out, block_dots, st)
+                            : launch_q8<1, kLazyS, 1, kLazyRL, 16 / kLazyS, true, false, DEBUG, false, true>(
+                                  in, m, sa_rows, w, out, block_dots, st);
+            if (c.xr == xl)
+                return w.w4 ? launch_q8<1, kLazyS, 1, kLazyRL, 48 / kLazyS, true, false, DEBUG, true, true>(
+                                  in, m, sa_rows, w, out, block_dots, st)
+                            : launch_q8<1, kLazyS, 1, kLazyRL, 48 / kLazyS, true, false, DEBUG, false, true>(
+                                  in, m, sa_rows, w, out, block_dots, st);
+        }
+    }
     MRI_Q8(4, 1, 1, 4) MRI_Q8(4, 1, 1, 12)
     MRI_Q8(8, 1, 2, 2) MRI_Q8(8, 1, 2, 6)
     MRI_Q8(16, 1, 2, 1) MRI_Q8(16, 1, 2, 3)
@@ -516,7 +611,7 @@ mri_status launch_gemv_q8_0(const float *x, const int8_t *act, size_t m,
                             int32_t *block_dots, float *scales_out, hipStream_t st,
                             const RowOps &ops) {
     if (w.n_tiles == 0 || m == 0) return MRI_OK;
-    const CfgQ8 c = pick_q8(x != nullptr, w.n_tiles, m, w.k_in, w.kp, groups_of(w));
+    const CfgQ8 c = pick_q8(x != nullptr, w.n_tiles, m, w.k_in, w.kp, groups_of(w), ops.any());
     if (c.s == 0) return set_error(MRI_ERR_INVALID_ARGUMENT, "gemv: shape not supported");
     if (!row_ops_ok(x, ops))
         return set_error(MRI_ERR_INVALID_ARGUMENT, "gemv: row operations need the fused path");

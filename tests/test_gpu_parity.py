@@ -252,6 +252,9 @@ Q8_SHAPES = [
     # the benchmarked decode shapes: [1,4096]x[4096,4096] and [4096,11008], and the
     # batched decode rows M = 8, 16, 32 at N = 11008
     (1, 11008, 4096), (1, 4096, 4096), (8, 11008, 4096), (16, 11008, 4096), (32, 11008, 4096),
+    # one row at 512-1023 tiles (the row quantized lap by lap in the GEMV): K with
+    # padding blocks in its last lap, and K = 11008
+    (1, 8200, 992), (1, 12000, 11008),
     # prefill sizes: partial row and channel tiles, K with padding blocks in its last lap
     # (992), many laps (11008); from 256 rows and 8192 channels the LDS-tiled kernel,
     # with 64-channel (8192, 8200) and 128-channel (16400) tiles

@@ -32,7 +32,7 @@ W4A8_SHAPES = [
     (1, 16, 32), (1, 16, 256), (1, 50, 96), (1, 1024, 4096), (1, 11008, 4096),
     (1, 64, 11008), (1, 32000 // 8, 4096), (2, 33, 256), (3, 48, 1024), (4, 64, 4096),
     (5, 40, 512), (9, 24, 1024), (16, 272, 4096), (33, 48, 256), (100, 40, 1024),
-    (2, 32, 16384), (1, 48, 20480),
+    (2, 32, 16384), (1, 48, 20480), (1, 8200, 992),
 ]
 
 
