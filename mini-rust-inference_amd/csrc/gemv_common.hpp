@@ -301,5 +301,56 @@ __device__ inline void act_end(const ActIn &in, bool perm, v4i (&xr)[XR], const 
     }
 }
 
+// The end of the prologue for the lap-wise quantization (the kernels'
+// LAZY instances): the same arithmetic as act_end up to the row scale, but
+// the row (RMS-normalized when in.norm_w) goes to LDS as f32 (s_xf, K
+// floats) instead of being quantized; returns 1 / scale.  act_begin has run.
+template <int S, int XR, bool OPS>
+__device__ inline float act_end_lazy(const ActIn &in, v4i (&xr)[XR], const v4i (&wn)[XR],
+                                     float *s_xf, float *red, float &scale, bool writer) {
+    const int t = threadIdx.x;
+    const int K4 = in.K / 4;
+    v4i *s_x4 = reinterpret_cast<v4i *>(s_xf);
+    const bool norm = OPS && in.norm_w;
+    if (!norm) {
+#pragma unroll
+        for (int e = 0; e < XR; ++e)
+            if (t + S * kWave * e < K4) s_x4[t + S * kWave * e] = xr[e];
+    }
+    __syncthreads();
+    float mx = 0.0f;
+    if (norm) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int s = 0; s < S; ++s) ss = ss + red[s];
+        const float mean_sq = __fdiv_rn(ss, (float)in.K);
+        const float rms_inv = __fdiv_rn(1.0f, __fsqrt_rn(mean_sq + in.eps));
+#pragma unroll
+        for (int e = 0; e < XR; ++e) {
+            if (t + S * kWave * e < K4) {
+                const float4 v = __builtin_bit_cast(float4, xr[e]);
+                const float4 w = __builtin_bit_cast(float4, wn[e]);
+                const float4 y = {w.x * (v.x * rms_inv), w.y * (v.y * rms_inv),
+                                  w.z * (v.z * rms_inv), w.w * (v.w * rms_inv)};
+                s_x4[t + S * kWave * e] = __builtin_bit_cast(v4i, y);
+                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)),
+                                     fmaxf(fabsf(y.z), fabsf(y.w))));
+            }
+        }
+        mx = wave_max(mx);
+        if ((t & 63) == 0) red[S + (t >> 6)] = mx;
+        __syncthreads();
+        mx = 0.0f;
+#pragma unroll
+        for (int s = 0; s < S; ++s) mx = fmaxf(mx, red[S + s]);
+    } else {
+#pragma unroll
+        for (int s = 0; s < S; ++s) mx = fmaxf(mx, red[s]);
+    }
+    scale = mx == 0.0f ? 1.0f : __fdiv_rn(mx, 127.0f);
+    if (writer && t == 0 && in.scale_out) in.scale_out[0] = scale;
+    return __fdiv_rn(1.0f, scale);
+}
+
 }  // namespace gemv
 }  // namespace mri

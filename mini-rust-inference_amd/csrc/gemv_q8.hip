@@ -135,30 +135,12 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     }
     float inv = 0.0f;  // LAZY: 1 / scale of the row
     if constexpr (LAZY) {
-        // the per-wave max|x| as act_begin computes it, the f32 pieces into
-        // LDS, one barrier, then the row scale as act_end computes it; each
-        // wave quantizes the laps it consumes, one at a time (quant_lap)
-        const int t = threadIdx.x, K4 = in.K / 4;
-        v4i *s_x4 = reinterpret_cast<v4i *>(s_act);
-        float mx = 0.0f;
-#pragma unroll
-        for (int e = 0; e < XR; ++e) {
-            if (t + NW * kWave * e < K4) {
-                const float4 v = __builtin_bit_cast(float4, xr[e]);
-                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-                s_x4[t + NW * kWave * e] = xr[e];
-            }
-        }
-        mx = wave_max(mx);
-        if ((t & 63) == 0) red[t >> 6] = mx;
-        __builtin_amdgcn_sched_barrier(0);
-        __syncthreads();
-        mx = 0.0f;
-#pragma unroll
-        for (int s = 0; s < NW; ++s) mx = fmaxf(mx, red[s]);
-        sa[0] = mx == 0.0f ? 1.0f : __fdiv_rn(mx, 127.0f);
-        inv = __fdiv_rn(1.0f, sa[0]);
-        if (blockIdx.x == 0 && t == 0 && in.scale_out) in.scale_out[0] = sa[0];
+        // the row and its scale as act_begin / act_end compute them, the
+        // f32 row staged in LDS; each wave quantizes the laps it consumes
+        // (quant_lap)
+        act_begin<NW, XR, FUSED, OPS>(in, n16, xr, s_act, red);
+        inv = act_end_lazy<NW, XR, OPS>(in, xr, wn, reinterpret_cast<float *>(s_act), red, sa[0],
+                                        blockIdx.x == 0);
     } else {
         act_begin<NW, XR, FUSED, OPS>(in, n16, xr, s_act, red);
         act_end<NW, XR, FUSED, OPS>(in, true, xr, wn, s_act, red, sa[0], blockIdx.x == 0);
@@ -442,6 +424,9 @@ __global__ __launch_bounds__(S * kWave) void k_gemv_w4a32(
 // (688 tiles): 9.07-9.11 us against 9.30-9.34 for the row quantized into
 // LDS up front; 8 waves 9.7-9.9, 16 waves 11.1.  At 2000 tiles (4096 ->
 // 32000) it was slower (22.3 against 21.6 us), so it stops at 1024 tiles.
+// The row-operation instances of the decode step (RMSNorm or SwiGLU in the
+// prologue) gave the same step time with it (81.0-81.7 us per token for
+// any tile range, 85 with all of them) and keep the up-front form.
 constexpr int kLazyS = 4;
 constexpr int kLazyRL = 1;
 constexpr size_t kLazyMaxTiles = 1024;
@@ -524,14 +509,14 @@ void dispatch_q8(CfgQ8 c, ActIn in, size_t m, const float *sa_rows, const Q8Matr
         if (c.lazy) {
             const int xs = xr_small(kLazyS), xl = xr_large(kLazyS);
             if (c.xr == xs)
-                return w.w4 ? launch_q8<1, kLazyS, 1, kLazyRL, 16 / kLazyS, true, false, DEBUG, true, true>(
+                return w.w4 ? launch_q8<1, kLazyS, 1, kLazyRL, 16 / kLazyS, true, OPS, DEBUG, true, true>(
                                   in, m, sa_rows, w, out, block_dots, st)
-                            : launch_q8<1, kLazyS, 1, kLazyRL, 16 / kLazyS, true, false, DEBUG, false, true>(
+                            : launch_q8<1, kLazyS, 1, kLazyRL, 16 / kLazyS, true, OPS, DEBUG, false, true>(
                                   in, m, sa_rows, w, out, block_dots, st);
             if (c.xr == xl)
-                return w.w4 ? launch_q8<1, kLazyS, 1, kLazyRL, 48 / kLazyS, true, false, DEBUG, true, true>(
+                return w.w4 ? launch_q8<1, kLazyS, 1, kLazyRL, 48 / kLazyS, true, OPS, DEBUG, true, true>(
                                   in, m, sa_rows, w, out, block_dots, st)
-                            : launch_q8<1, kLazyS, 1, kLazyRL, 48 / kLazyS, true, false, DEBUG, false, true>(
+                            : launch_q8<1, kLazyS, 1, kLazyRL, 48 / kLazyS, true, OPS, DEBUG, false, true>(
                                   in, m, sa_rows, w, out, block_dots, st);
         }
     }
