@@ -140,7 +140,9 @@ __global__ __launch_bounds__(kThreads) void k_q4_0_lds(const float *__restrict__
     const uint8_t *s_w = reinterpret_cast<const uint8_t *>(s_raw);
     {
         // every load in flight before the first store (at most 12 pieces a
-        // thread: the launcher keeps R rows within 48 KiB)
+        // thread: the launcher keeps R rows within 48 KiB; the pieces past
+        // the rows re-read the last one, which measured faster than
+        // skipping them under a branch: 11.8 against 21.3 us at N = 11008)
         const int4 *src = reinterpret_cast<const int4 *>(w + (size_t)n0 * row_bytes);
         const int n16 = rows * row_bytes / 16;
         int4 v[12];
@@ -252,8 +254,11 @@ mri_status launch_q4(const float *x, size_t m, size_t k, const uint8_t *w, size_
     // at most 64 KiB of LDS per workgroup (several workgroups per CU)
     const bool al = ((uintptr_t)w & 15) == 0 && ((uintptr_t)x & 15) == 0 && k % 256 == 0;
     if (al && m <= 4 && k <= (1u << 16) && n_out <= (1u << 30)) {
-        // rows per workgroup: 16, 8 or 4, as ~40 KiB of LDS allows
-        if (q4_lds_bytes(16, k) <= 40 * 1024) return launch_lds<16, GG>(x, m, k, w, n_out, out, s);
+        // rows per workgroup: 8, or 4 where 8 rows exceed ~40 KiB of LDS.
+        // Measured at K = 4096 (us per call): 8 rows 11.8 (N = 11008) and
+        // 6.4 (N = 4096), against 13.1 and 8.4 for 16 rows and 12.7 and 6.4
+        // for 4 (more workgroups per CU overlap one's loads with another's
+        // arithmetic)
         if (q4_lds_bytes(8, k) <= 40 * 1024) return launch_lds<8, GG>(x, m, k, w, n_out, out, s);
         if (q4_lds_bytes(4, k) <= 48 * 1024) return launch_lds<4, GG>(x, m, k, w, n_out, out, s);
     }
