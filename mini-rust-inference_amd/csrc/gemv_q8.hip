@@ -420,15 +420,17 @@ __global__ __launch_bounds__(S * kWave) void k_gemv_w4a32(
 }
 
 // Lap-wise quantization of the fused row (k_gemv_q8_0's LAZY instances):
-// waves per tile and laps in flight.  Measured at [1,4096]x[4096,11008]
-// (688 tiles): 9.07-9.11 us against 9.30-9.34 for the row quantized into
-// LDS up front; 8 waves 9.7-9.9, 16 waves 11.1.  At 2000 tiles (4096 ->
-// 32000) it was slower (22.3 against 21.6 us), so it stops at 1024 tiles.
-// The row-operation instances of the decode step (RMSNorm or SwiGLU in the
-// prologue) gave the same step time with it (81.0-81.7 us per token for
-// any tile range, 85 with all of them) and keep the up-front form.
-constexpr int kLazyS = 4;
-constexpr int kLazyRL = 1;
+// waves per tile and laps in flight by tile count and laps per tile G, from
+// A/B runs on one box (us per call, against the row quantized into LDS up
+// front): 512-1023 tiles, 4 waves x 1 lap (688 tiles, [1,4096]x[4096,11008]:
+// 9.07-9.11 against 9.30-9.34; 8 waves 9.7-9.9, 16 waves 11.1); below 512
+// tiles 4 waves x 2 laps at G <= 16 (256 tiles, 4096 -> 4096: 5.07 against
+// 5.70) and 8 waves x 2 laps above (11008 -> 4096: 10.07-10.16 against
+// 10.62-10.78; 16 waves x 1 lap 10.05).  From 1024 tiles the up-front form
+// stays (2000 tiles, 4096 -> 32000: 22.3 against 21.6 with 4 x 1).  The
+// row-operation instances of the decode step (RMSNorm or SwiGLU in the
+// prologue) gave the same step time with it (81.0-81.7 us per token, 85
+// with all of them) and keep the up-front form.
 constexpr size_t kLazyMaxTiles = 1024;
 
 struct CfgQ8 {
@@ -458,20 +460,28 @@ inline int xr_large(int s) { return 48 / s; }
 CfgQ8 pick_q8(bool fused, size_t n_tiles, size_t m, size_t k, size_t kp, size_t G,
               bool ops = false) {
     CfgQ8 c;
-    if (fused && !ops && m == 1 && n_tiles >= 512 && n_tiles < kLazyMaxTiles) {
+    if (fused && !ops && m == 1 && n_tiles < kLazyMaxTiles) {
         CfgQ8 z;
-        z.s = kLazyS;
-        z.rl = kLazyRL;
+        z.s = n_tiles >= 512 || G <= 16 ? 4 : 8;
+        z.rl = n_tiles >= 512 ? 1 : 2;
         z.lazy = true;
         const size_t nx = ceil_div(k / 4, (size_t)z.s * kWave);
         z.xr = nx <= (size_t)xr_small(z.s) ? xr_small(z.s) : nx <= (size_t)xr_large(z.s) ? xr_large(z.s) : 0;
         if (z.xr != 0 && lds_q8(z.s, z.tpw, m, kp, G, true) <= kMaxLds) return z;
     }
+    // Below 512 tiles: the waves and laps of the lap-wise form above, so the
+    // two-kernel path adds the wave sums in the same order as the fused row
+    // (identical results; also faster at 4096 -> 4096, 5.51 against 5.72 us);
+    // the row-operation instances of the decode step keep 8 or 16 waves,
+    // which measured 1.6 us per token faster there.
     if (n_tiles >= 512) {
         c.s = 4;
         c.rl = 1;
-    } else {
+    } else if (ops) {
         c.s = G > 16 ? 16 : 8;
+        c.rl = 2;
+    } else {
+        c.s = G > 16 ? 8 : 4;
         c.rl = 2;
     }
     const size_t threads = (size_t)c.s * c.tpw * kWave;
@@ -506,21 +516,21 @@ void dispatch_q8(CfgQ8 c, ActIn in, size_t m, const float *sa_rows, const Q8Matr
                     : launch_q8<MR, S_, TPW_, RL_, XR_, FUSED, OPS, DEBUG, false>(         \
                           in, m, sa_rows, w, out, block_dots, st);
     if constexpr (FUSED && !OPS && MR == 1) {
+#define MRI_Q8L(S_, RL_, XR_)                                                              \
+    if (c.s == S_ && c.rl == RL_ && c.xr == XR_)                                           \
+        return w.w4 ? launch_q8<1, S_, 1, RL_, XR_, true, false, DEBUG, true, true>(       \
+                          in, m, sa_rows, w, out, block_dots, st)                          \
+                    : launch_q8<1, S_, 1, RL_, XR_, true, false, DEBUG, false, true>(      \
+                          in, m, sa_rows, w, out, block_dots, st);
         if (c.lazy) {
-            const int xs = xr_small(kLazyS), xl = xr_large(kLazyS);
-            if (c.xr == xs)
-                return w.w4 ? launch_q8<1, kLazyS, 1, kLazyRL, 16 / kLazyS, true, OPS, DEBUG, true, true>(
-                                  in, m, sa_rows, w, out, block_dots, st)
-                            : launch_q8<1, kLazyS, 1, kLazyRL, 16 / kLazyS, true, OPS, DEBUG, false, true>(
-                                  in, m, sa_rows, w, out, block_dots, st);
-            if (c.xr == xl)
-                return w.w4 ? launch_q8<1, kLazyS, 1, kLazyRL, 48 / kLazyS, true, OPS, DEBUG, true, true>(
-                                  in, m, sa_rows, w, out, block_dots, st)
-                            : launch_q8<1, kLazyS, 1, kLazyRL, 48 / kLazyS, true, OPS, DEBUG, false, true>(
-                                  in, m, sa_rows, w, out, block_dots, st);
+            MRI_Q8L(4, 1, 4) MRI_Q8L(4, 1, 12)
+            MRI_Q8L(4, 2, 4) MRI_Q8L(4, 2, 12)
+            MRI_Q8L(8, 2, 2) MRI_Q8L(8, 2, 6)
         }
+#undef MRI_Q8L
     }
     MRI_Q8(4, 1, 1, 4) MRI_Q8(4, 1, 1, 12)
+    MRI_Q8(4, 1, 2, 4) MRI_Q8(4, 1, 2, 12)
     MRI_Q8(8, 1, 2, 2) MRI_Q8(8, 1, 2, 6)
     MRI_Q8(16, 1, 2, 1) MRI_Q8(16, 1, 2, 3)
 #undef MRI_Q8
