@@ -57,7 +57,7 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     constexpr int LR = MR == 1 ? 1 : 2;       // rows per result lane
     constexpr int LG = (MR + 1) / 2;          // lane groups holding results
     static_assert(!FUSED || MR == 1, "the fused prologue quantizes one row");
-    static_assert(!LAZY || (FUSED && !OPS), "lap-wise quantization: the plain fused row");
+    static_assert(!LAZY || FUSED, "lap-wise quantization: the fused row");
     extern __shared__ v4i s_lds[];
     const int wl = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int tw_ = wl / S;                   // tile of the wave within the WG
@@ -428,10 +428,12 @@ __global__ __launch_bounds__(S * kWave) void k_gemv_w4a32(
 // 5.70) and 8 waves x 2 laps above (11008 -> 4096: 10.07-10.16 against
 // 10.62-10.78; 16 waves x 1 lap 10.05).  From 1024 tiles the up-front form
 // stays (2000 tiles, 4096 -> 32000: 22.3 against 21.6 with 4 x 1).  The
-// row-operation instances of the decode step (RMSNorm or SwiGLU in the
-// prologue) gave the same step time with it (81.0-81.7 us per token, 85
-// with all of them) and keep the up-front form.
+// row-operation instances of the decode step take it below 512 tiles (the
+// o projection with its residual add, down with the SwiGLU prologue: 80.7-
+// 80.9 against 81.4 us per token); from 512 tiles (q/k/v, gate/up and
+// lm_head, with the RMSNorm prologue) it gave the same step time.
 constexpr size_t kLazyMaxTiles = 1024;
+constexpr size_t kLazyMaxOpsTiles = 512;
 
 struct CfgQ8 {
     int s = 0, tpw = 1, rl = 1, xr = 0;  // s == 0: unsupported
@@ -460,7 +462,7 @@ inline int xr_large(int s) { return 48 / s; }
 CfgQ8 pick_q8(bool fused, size_t n_tiles, size_t m, size_t k, size_t kp, size_t G,
               bool ops = false) {
     CfgQ8 c;
-    if (fused && !ops && m == 1 && n_tiles < kLazyMaxTiles) {
+    if (fused && m == 1 && n_tiles < (ops ? kLazyMaxOpsTiles : kLazyMaxTiles)) {
         CfgQ8 z;
         z.s = n_tiles >= 512 || G <= 16 ? 4 : 8;
         z.rl = n_tiles >= 512 ? 1 : 2;
@@ -471,9 +473,10 @@ CfgQ8 pick_q8(bool fused, size_t n_tiles, size_t m, size_t k, size_t kp, size_t 
     }
     // Below 512 tiles: the waves and laps of the lap-wise form above, so the
     // two-kernel path adds the wave sums in the same order as the fused row
-    // (identical results; also faster at 4096 -> 4096, 5.51 against 5.72 us);
-    // the row-operation instances of the decode step keep 8 or 16 waves,
-    // which measured 1.6 us per token faster there.
+    // (identical results; also faster at 4096 -> 4096, 5.51 against 5.72 us).
+    // Row operations that cannot take the lap-wise form keep 8 or 16 waves
+    // (in the decode step's up-front form they measured 1.6 us per token
+    // faster than 4 or 8).
     if (n_tiles >= 512) {
         c.s = 4;
         c.rl = 1;
@@ -515,12 +518,12 @@ void dispatch_q8(CfgQ8 c, ActIn in, size_t m, const float *sa_rows, const Q8Matr
                           in, m, sa_rows, w, out, block_dots, st)                          \
                     : launch_q8<MR, S_, TPW_, RL_, XR_, FUSED, OPS, DEBUG, false>(         \
                           in, m, sa_rows, w, out, block_dots, st);
-    if constexpr (FUSED && !OPS && MR == 1) {
+    if constexpr (FUSED && MR == 1) {
 #define MRI_Q8L(S_, RL_, XR_)                                                              \
     if (c.s == S_ && c.rl == RL_ && c.xr == XR_)                                           \
-        return w.w4 ? launch_q8<1, S_, 1, RL_, XR_, true, false, DEBUG, true, true>(       \
+        return w.w4 ? launch_q8<1, S_, 1, RL_, XR_, true, OPS, DEBUG, true, true>(         \
                           in, m, sa_rows, w, out, block_dots, st)                          \
-                    : launch_q8<1, S_, 1, RL_, XR_, true, false, DEBUG, false, true>(      \
+                    : launch_q8<1, S_, 1, RL_, XR_, true, OPS, DEBUG, false, true>(        \
                           in, m, sa_rows, w, out, block_dots, st);
         if (c.lazy) {
             MRI_Q8L(4, 1, 4) MRI_Q8L(4, 1, 12)
