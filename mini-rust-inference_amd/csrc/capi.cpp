@@ -683,6 +683,16 @@ static mri_status matmul_int8_common(const char *fn, const int8_t *act_q, size_t
     mri_status st = current_device(&dev);
     if (st) return st;
     auto s = static_cast<hipStream_t>(stream);
+    if (m >= kGemmMinRows && gemm_rows_ok(m, d, act_q)) {
+        // prefill on the caller's rows as they are
+        void *ws = nullptr;
+        if (const size_t wsb = gemm_ws_bytes(m, d)) {
+            st = gemm_ws_get(s, wsb, &ws);
+            if (st) return st;
+        }
+        return launch_gemm_int8(act_q, m, sa_ptr, sa_stride, sa_value, d, out, acc_out, ws, s,
+                                true);
+    }
     if (m >= kGemmMinRows) {
         // prefill: repack the rows into the GEMM fragment layout
         void *base = nullptr;

@@ -309,9 +309,12 @@ size_t gemm_ws_bytes(size_t m, const QMatrixDev &w);
 bool gemm_q8_supported(size_t m, const Q8MatrixDev &w);
 mri_status launch_gemm_q8_0(const int8_t *act, size_t m, const float *sa_rows,
                             const Q8MatrixDev &w, float *out, hipStream_t s);
+// rows: act_packed is the caller's row-major [m][k] int8 (gemm_rows_ok).
 mri_status launch_gemm_int8(const int8_t *act_packed, size_t m, const float *sa_ptr,
                             int sa_stride, float sa_value, const QMatrixDev &w,
-                            float *out, int32_t *acc_out, void *ws, hipStream_t s);
+                            float *out, int32_t *acc_out, void *ws, hipStream_t s,
+                            bool rows = false);
+bool gemm_rows_ok(size_t m, const QMatrixDev &w, const void *act);
 // Per-(device, stream) GEMM workspace (capi.cpp), grow-only, zeroed when
 // (re)allocated.
 mri_status gemm_ws_get(hipStream_t stream, size_t bytes, void **ptr);

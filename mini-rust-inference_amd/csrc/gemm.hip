@@ -32,6 +32,13 @@
 // Workgroup -> tile mapping is XCD-aware: workgroups are dispatched to the
 // eight XCDs round-robin, and the M tiles that share a weight column block
 // are placed on the same XCD, so they share its L2.
+//
+// ROWS instances read the caller's row-major int8 rows directly (no repack
+// pass): an activation stage holds two K steps, 128 bytes of each of the
+// tile's rows, and each DMA instruction moves 8 rows x 128 bytes (whole
+// cache lines).  Piece i (16 bytes) of a row goes to slot i ^ (row % 8) of
+// its 128-byte LDS row, so the fragment reads (32 rows at one piece index)
+// spread over all banks.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -105,7 +112,28 @@ constexpr int kWaitVm0 = 0x0F70;       // s_waitcnt vmcnt(0), others untouched
 // epilogue and resets the counter to zero for the next call.  No workgroup
 // waits for another.  Splitting K puts more workgroups, and more loads in
 // flight, on products whose tiles alone would leave most CUs idle.
-template <int BM, int BN, int WM, int WN, int NSA, int NSB>
+// ROWS wait counts: the loads issued after the last one a step needs, at
+// the wait of step p (before it issues its own).  Issue order per step q:
+// activation stage q/2 + nsa - 1 (la2 loads, even q only), then weight step
+// q + nsb - 1 (lb loads).  A step needs activation stages <= sa_req and
+// weight steps <= sb_req (shift invariant: p is any large value of the
+// step's parity).
+constexpr int rows_wait(int p, int sa_req, int sb_req, int nsa, int nsb, int la2, int lb) {
+    int idx = 0, last = -1;
+    for (int q = p - 200; q < p; ++q) {
+        if ((q & 1) == 0) {
+            const int st = q / 2 + nsa - 1;
+            for (int j = 0; j < la2; ++j, ++idx)
+                if (st <= sa_req) last = idx;
+        }
+        const int bs = q + nsb - 1;
+        for (int j = 0; j < lb; ++j, ++idx)
+            if (bs <= sb_req) last = idx;
+    }
+    return idx - 1 - last;
+}
+
+template <int BM, int BN, int WM, int WN, int NSA, int NSB, bool ROWS = false>
 __global__ __launch_bounds__(WM * WN * kWave) void k_gemm_int8(
     const int8_t *__restrict__ act, int mg, const float *__restrict__ sa_ptr, int sa_stride,
     float sa_value, const int8_t *__restrict__ tiles, const float *__restrict__ wscales,
@@ -118,6 +146,8 @@ __global__ __launch_bounds__(WM * WN * kWave) void k_gemm_int8(
     static_assert(FA % NW == 0 && FB % NW == 0, "load split");
     constexpr int SA = FA * 1024, SB = FB * 1024;  // bytes of one A / B stage
     static_assert(NSA >= 3 && NSB >= 3, "ring depths");
+    // ROWS: NSA activation stages of two K steps (SA2 bytes, LA2 loads a wave)
+    constexpr int SA2 = 2 * SA, LA2 = 2 * LA;
     // Issue order per step q: A(q + NSA - 1), then B(q + NSB - 1).  Step p
     // of the loop needs the data of step p + 1 (its fragments are read into
     // registers while step p's MFMAs run); the younger of A(p+1), B(p+1) is
@@ -137,9 +167,11 @@ __global__ __launch_bounds__(WM * WN * kWave) void k_gemm_int8(
     const int tile = item / ks, sp = item - tile * ks;
     if (tile >= n_tiles_total) return;
     // K steps p0 .. p0 + PS - 1 of the tile (ks <= P, so PS >= 1)
-    const int kq = P / ks, kr = P - kq * ks;
-    const int p0 = sp * kq + min(sp, kr);
-    const int PS = kq + (sp < kr ? 1 : 0);
+    // (ROWS: the split is in step pairs, so ranges start on a stage)
+    const int PU = ROWS ? P / 2 : P;
+    const int kq = PU / ks, kr = PU - kq * ks;
+    const int p0 = (ROWS ? 2 : 1) * (sp * kq + min(sp, kr));
+    const int PS = (ROWS ? 2 : 1) * (kq + (sp < kr ? 1 : 0));
     const int mt = tile % n_mt, nt = tile / n_mt;
     const int m0 = mt * BM, T0 = nt * (BN / 16);  // first row, first 16-row weight tile
 
@@ -147,7 +179,7 @@ __global__ __launch_bounds__(WM * WN * kWave) void k_gemm_int8(
     const int wv = __builtin_amdgcn_readfirstlane(t >> 6), l = t & 63;
     const int wm = wv / WN, wn = wv % WN;
     const unsigned ldsA = __builtin_amdgcn_readfirstlane((unsigned)(size_t)s_buf);
-    const unsigned ldsB = ldsA + NSA * SA;
+    const unsigned ldsB = ldsA + NSA * (ROWS ? SA2 : SA);
 
     // This wave's loads.  Fragment f = wv + NW*j holds row group f/2, k half
     // f%2.  Activations are packed (see pack layout): fragment (p, g, h) is
@@ -155,13 +187,21 @@ __global__ __launch_bounds__(WM * WN * kWave) void k_gemm_int8(
     // groups of one K step are contiguous.  Weight lane: row 32*(f/2) + l%32
     // of the block, i.e. stored chunk T0 + 2*(f/2) + (l%32)/16 (clamped: rows
     // past N feed only discarded outputs), piece (2*(f%2) + l/32)*16 + l%16.
-    const int8_t *a_src[LA];
+    const int8_t *a_src[ROWS ? LA2 : LA];
     const int8_t *b_src[LB];
 #pragma unroll
-    for (int j = 0; j < LA; ++j) {
+    for (int j = 0; j < (ROWS ? LA2 : LA); ++j) {
         const int f = wv + NW * j;
-        const int g = min(m0 / 32 + (f >> 1), mg - 1);  // clamped: rows past M
-        a_src[j] = act + ((size_t)(2 * g + (f & 1)) * kWave + l) * 16;
+        if constexpr (ROWS) {
+            // rows of P * 64 bytes: load f covers tile rows 8f .. 8f + 7,
+            // eight lanes a row, lane l%8 bringing piece (l%8) ^ (row%8)
+            const int rl = 8 * f + (l >> 3);
+            const int row = min(m0 + rl, M - 1);  // clamped: rows past M
+            a_src[j] = act + (size_t)row * (size_t)P * 64 + 16 * ((l & 7) ^ (rl & 7));
+        } else {
+            const int g = min(m0 / 32 + (f >> 1), mg - 1);  // clamped: rows past M
+            a_src[j] = act + ((size_t)(2 * g + (f & 1)) * kWave + l) * 16;
+        }
     }
 #pragma unroll
     for (int j = 0; j < LB; ++j) {
@@ -184,6 +224,13 @@ __global__ __launch_bounds__(WM * WN * kWave) void k_gemm_int8(
 #pragma unroll
         for (int j = 0; j < LA; ++j) dma16(a_src[j] + off, st + (wv + NW * j) * 1024);
     };
+    // ROWS: activation stage t (steps 2t, 2t + 1) of the range into buffer t % NSA
+    auto issue_a2 = [&](int t) __attribute__((always_inline)) {
+        const unsigned st = ldsA + (unsigned)((t % NSA) * SA2);
+        const size_t off = (size_t)(p0 / 2 + min(t, PS / 2 - 1)) * 128;
+#pragma unroll
+        for (int j = 0; j < LA2; ++j) dma16(a_src[j] + off, st + (wv + NW * j) * 1024);
+    };
     auto issue_b = [&](int p) __attribute__((always_inline)) {
         const unsigned st = ldsB + (unsigned)((p % NSB) * SB);
         const size_t off = (size_t)kstep(p) * b_pitch;
@@ -201,12 +248,21 @@ __global__ __launch_bounds__(WM * WN * kWave) void k_gemm_int8(
     v4i fa[2][2][TM], fb[2][2][TN];  // [set][k half][tile]
     auto lds_read = [&](auto set, int p) __attribute__((always_inline)) {
         constexpr int S = decltype(set)::value;
-        const v4i *sa_ = s_buf + (size_t)(p % NSA) * (SA / 16) + l;
-        const v4i *sb_ = s_buf + (size_t)(NSA * SA + (p % NSB) * SB) / 16 + l;
+        const v4i *sa_ =
+            s_buf + (size_t)(ROWS ? ((p >> 1) % NSA) * (SA2 / 16) : (p % NSA) * (SA / 16)) + l;
+        const v4i *sb_ = s_buf + (size_t)(NSA * (ROWS ? SA2 : SA) + (p % NSB) * SB) / 16 + l;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
 #pragma unroll
-            for (int i = 0; i < TM; ++i) fa[S][h][i] = sa_[(2 * (wm * TM + i) + h) * kWave];
+            for (int i = 0; i < TM; ++i) {
+                if constexpr (ROWS) {  // row r, piece 4 (p % 2) + 2h + l/32 of its 128 bytes
+                    const int row = 32 * (wm * TM + i) + (l & 31);
+                    const int pc = 4 * (p & 1) + 2 * h + (l >> 5);
+                    fa[S][h][i] = sa_[row * 8 + (pc ^ (row & 7)) - l];
+                } else {
+                    fa[S][h][i] = sa_[(2 * (wm * TM + i) + h) * kWave];
+                }
+            }
 #pragma unroll
             for (int j = 0; j < TN; ++j) fb[S][h][j] = sb_[(2 * (wn * TN + j) + h) * kWave];
         }
@@ -226,20 +282,46 @@ __global__ __launch_bounds__(WM * WN * kWave) void k_gemm_int8(
     // The prologue replays the steady-state issue order for the steps
     // q = -(NMX-1) .. -1 (skipping loads of steps below 0), so the wait
     // count of every step is the same constant.
-    for (int q = -(NMX - 1); q < 0; ++q) {
-        if (q + NSA - 1 >= 0) issue_a(q + NSA - 1);
-        if (q + NSB - 1 >= 0) issue_b(q + NSB - 1);
+    // ROWS: an even step p needs stages <= p/2 and weight step p + 1, an odd
+    // one stage (p + 1)/2 as well; before the loop, stage 0 and step 0.
+    constexpr int WR_E = rows_wait(1000, 500, 1001, NSA, NSB, LA2, LB);
+    constexpr int WR_O = rows_wait(1001, 501, 1002, NSA, NSB, LA2, LB);
+    constexpr int WR_0 = rows_wait(1000, 500, 1000, NSA, NSB, LA2, LB);
+    if constexpr (ROWS) {
+        constexpr int QM = 2 * (NSA - 1) > NSB - 1 ? 2 * (NSA - 1) : NSB - 1;
+        for (int q = -QM; q < 0; ++q) {
+            if ((q & 1) == 0 && q / 2 + NSA - 1 >= 0) issue_a2(q / 2 + NSA - 1);
+            if (q + NSB - 1 >= 0) issue_b(q + NSB - 1);
+        }
+        wait_barrier<WR_0>();
+    } else {
+        for (int q = -(NMX - 1); q < 0; ++q) {
+            if (q + NSA - 1 >= 0) issue_a(q + NSA - 1);
+            if (q + NSB - 1 >= 0) issue_b(q + NSB - 1);
+        }
+        wait_barrier<WAIT0>();
     }
-    wait_barrier<WAIT0>();
     lds_read(std::integral_constant<int, 0>{}, 0);
     // Step p: wait for step p + 1's loads and barrier (all waves are past
     // step p - 1, whose buffers are refilled next), issue step p + NS - 1,
     // read step p + 1's fragments into the other register set, then the
     // MFMAs of step p (which run on while the next step waits).  The reads
     // past the last step touch a buffer no step reads; they are unused.
+    // (ROWS: the even steps, register set 0, issue the activation stage
+    // NSA - 1 ahead; stage t's buffer last held stage t - NSA, whose reads
+    // ended two steps earlier.)
     auto step = [&](int p, auto cur, auto nxt) __attribute__((always_inline)) {
-        wait_barrier<WAIT>();
-        issue_a(p + NSA - 1);
+        if constexpr (ROWS) {
+            if constexpr (decltype(cur)::value == 0) {
+                wait_barrier<WR_E>();
+                issue_a2(p / 2 + NSA - 1);
+            } else {
+                wait_barrier<WR_O>();
+            }
+        } else {
+            wait_barrier<WAIT>();
+            issue_a(p + NSA - 1);
+        }
         issue_b(p + NSB - 1);
         lds_read(nxt, p + 1);
         mfmas(cur);
@@ -775,15 +857,15 @@ __global__ __launch_bounds__(512) void k_gemm_sk(
 
 // ks > 1: K split in ks ranges per tile, with ws the stream-K workspace
 // (tile counters first, then the partial slots).
-template <int BM, int BN, int WM, int WN, int NSA, int NSB>
+template <int BM, int BN, int WM, int WN, int NSA, int NSB, bool ROWS = false>
 mri_status launch(const int8_t *act_packed, size_t m, const float *sa_ptr, int sa_stride,
                   float sa_value, const QMatrixDev &w, float *out, int32_t *acc_out,
                   hipStream_t s, int ks = 1, void *ws = nullptr) {
-    constexpr size_t lds = gemm_lds_bytes<BM, BN, NSA, NSB>();
+    constexpr size_t lds = gemm_lds_bytes<BM, BN, ROWS ? 2 * NSA : NSA, NSB>();
     static DeviceOnce attr;  // the attribute belongs to the function
     MRI_HIP(attr.run([&](int) {
         return hipFuncSetAttribute(
-            reinterpret_cast<const void *>(&k_gemm_int8<BM, BN, WM, WN, NSA, NSB>),
+            reinterpret_cast<const void *>(&k_gemm_int8<BM, BN, WM, WN, NSA, NSB, ROWS>),
             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     }));
     const size_t n_mt = (m + BM - 1) / BM;
@@ -794,7 +876,7 @@ mri_status launch(const int8_t *act_packed, size_t m, const float *sa_ptr, int s
     const size_t grid = (total * ks + kXcds - 1) / kXcds * kXcds;
     int *cnt = static_cast<int *>(ws);
     int32_t *part = ws ? reinterpret_cast<int32_t *>(cnt + kSkMaxTiles) : nullptr;
-    hipLaunchKernelGGL((k_gemm_int8<BM, BN, WM, WN, NSA, NSB>), dim3((unsigned)grid),
+    hipLaunchKernelGGL((k_gemm_int8<BM, BN, WM, WN, NSA, NSB, ROWS>), dim3((unsigned)grid),
                        dim3(WM * WN * kWave), lds, s, act_packed, (int)gemm_row_groups(m),
                        sa_ptr, sa_stride, sa_value, w.tiles, w.scales, (int)m, (int)w.n_out,
                        (int)w.n_tiles, (int)(w.kp / kChunkK), (int)n_mt, (int)total, out,
@@ -949,6 +1031,19 @@ size_t plan_ws_bytes(const GemmPlan &pl) {
 
 size_t gemm_ws_bytes(size_t m, const QMatrixDev &w) { return plan_ws_bytes(plan_gemm(m, w)); }
 
+// The caller's int8 rows ([m][k], 16-byte aligned) can feed the GEMM as they
+// are when the plan takes 128-row whole tiles and K is a whole number of
+// 128-byte stages with no padding; the other plans (256-row tiles, stream-K)
+// read the packed layout.  Measured against the repack pass plus the packed
+// kernel: the ROWS kernel takes 0.2-0.8 us more at these plans (512 x 11008:
+// 35.0 against 34.2-34.8; 128 x 11008: 16.8 against 16.6) and saves the
+// 4-5 us repack; at 256-row tiles it was 7 us slower (2048 x 11008).
+bool gemm_rows_ok(size_t m, const QMatrixDev &w, const void *act) {
+    if ((reinterpret_cast<uintptr_t>(act) & 15) || w.k_in != w.kp || w.kp % 128) return false;
+    const GemmKind k = plan_gemm(m, w).kind;
+    return k == GemmKind::T128x64 || k == GemmKind::T128x128 || k == GemmKind::T128x192;
+}
+
 // act_packed: activations in the GEMM fragment layout (gemm_pack_bytes).
 // ws: gemm_ws_bytes(m, w) bytes (may be null when that is 0); its first
 // kSkMaxTiles ints (the tile counters, at the same place for every shape)
@@ -956,7 +1051,7 @@ size_t gemm_ws_bytes(size_t m, const QMatrixDev &w) { return plan_ws_bytes(plan_
 // Without a workspace the plan falls back to whole tiles and no K split.
 mri_status launch_gemm_int8(const int8_t *act_packed, size_t m, const float *sa_ptr,
                             int sa_stride, float sa_value, const QMatrixDev &w,
-                            float *out, int32_t *acc_out, void *ws, hipStream_t s) {
+                            float *out, int32_t *acc_out, void *ws, hipStream_t s, bool rows) {
     if (w.n_tiles == 0 || m == 0) return MRI_OK;
     GemmPlan pl = plan_gemm(m, w);
     if (!ws) {
@@ -964,6 +1059,22 @@ mri_status launch_gemm_int8(const int8_t *act_packed, size_t m, const float *sa_
         if (pl.kind == GemmKind::SK128 || pl.kind == GemmKind::SK256) pl.kind = GemmKind::T256x128;
     }
     mri_status st = MRI_OK;
+    if (rows) {  // act_packed holds the caller's rows (gemm_rows_ok)
+        if (!gemm_rows_ok(m, w, act_packed))
+            return set_error(MRI_ERR_INVALID_ARGUMENT, "gemm: rows not usable for this plan");
+        if (pl.kind == GemmKind::T128x64)
+            st = launch<128, 64, 4, 1, 4, 8, true>(act_packed, m, sa_ptr, sa_stride, sa_value, w,
+                                                   out, acc_out, s, pl.ks, ws);
+        else if (pl.kind == GemmKind::T128x128)
+            st = launch<128, 128, 2, 2, 4, 8, true>(act_packed, m, sa_ptr, sa_stride, sa_value, w,
+                                                    out, acc_out, s, pl.ks, ws);
+        else
+            st = launch<128, 192, 2, 2, 3, 8, true>(act_packed, m, sa_ptr, sa_stride, sa_value, w,
+                                                    out, acc_out, s);
+        if (st) return st;
+        MRI_LAUNCHED("k_gemm_int8");
+        return MRI_OK;
+    }
     switch (pl.kind) {
         case GemmKind::SK256:
             return launch_sk<4>(act_packed, m, sa_ptr, sa_stride, sa_value, w, out, acc_out, ws,

@@ -155,7 +155,10 @@ def test_matmul_int8_bit_exact(m, n, k):
                                    # 256 x 128 whole (1280 x 11008), 256 x 256 stream-K
                                    # in whole passes (4096 x 4096)
                                    (768, 11008, 4096), (1536, 11008, 4096), (1280, 11008, 4096),
-                                   (4096, 4096, 4096)])
+                                   (4096, 4096, 4096),
+                                   # K a whole number of 64 but not of 128 bytes: the
+                                   # 128-row plans repack instead of reading the rows
+                                   (130, 200, 960), (512, 4096, 960)])
 def test_matmul_int8_prefill_closed_form(m, n, k):
     """Prefill-sized matmul_int8 (int8.rs:61-98) at full shapes: the int32
     accumulators against an exact float64 matmul (|sum| <= 127^2 * K < 2^53)
@@ -175,6 +178,31 @@ def test_matmul_int8_prefill_closed_form(m, n, k):
     mri().matmul_int8(dev(aq), sa, w, m, out, acc)
     assert np.array_equal(host(acc), acc0)
     assert_bits_equal(host(out), out0, "matmul_int8 prefill out")
+
+
+@pytest.mark.parametrize("m,n,k", [(128, 4096, 4096), (512, 11008, 4096), (256, 300, 4096)])
+def test_matmul_int8_prefill_misaligned_rows(m, n, k):
+    """Rows at an address that is not 16-byte aligned take the repack path;
+    the result equals the aligned call (which reads the rows as they are)
+    bit for bit, and the closed form."""
+    say(f"matmul_int8 prefill misaligned m={m} n={n} k={k}")
+    t = torch()
+    rng = np.random.default_rng(m + 5 * n + k)
+    wq = rng.integers(-127, 128, (n, k)).astype(np.int8)
+    ws = rng.uniform(1e-4, 1e-3, n).astype(F32)
+    aq = rng.integers(-127, 128, (m, k)).astype(np.int8)
+    acc0 = (aq.astype(np.float64) @ wq.astype(np.float64).T).astype(np.int32)
+    w = mri().QMatrix.from_host(wq, ws)
+    buf = dev(np.concatenate([np.zeros(4, np.int8), aq.ravel()]))
+    au = buf[4:]
+    assert au.data_ptr() % 16 != 0
+    out_u, acc_u = empty((m, n), t.float32), empty((m, n), t.int32)
+    mri().matmul_int8(au, F32(0.0173), w, m, out_u, acc_u)
+    out_a, acc_a = empty((m, n), t.float32), empty((m, n), t.int32)
+    mri().matmul_int8(dev(aq), F32(0.0173), w, m, out_a, acc_a)
+    assert np.array_equal(host(acc_u), acc0)
+    assert np.array_equal(host(acc_a), acc0)
+    assert_bits_equal(host(out_u), host(out_a), "matmul_int8 misaligned vs aligned rows")
 
 
 def test_matmul_int8_prefill_back_to_back():
