@@ -283,6 +283,9 @@ Q8_SHAPES = [
     # one row at 512-1023 tiles (the row quantized lap by lap in the GEMV): K with
     # padding blocks in its last lap, and K = 11008
     (1, 8200, 992), (1, 12000, 11008),
+    # two to four f32 rows quantized in the GEMV prologue (without block dots): 4 waves x
+    # 1 lap at 688 tiles, 4 x 2 below 512 tiles, 8 x 2 at K = 8192
+    (2, 11008, 4096), (4, 4096, 4096), (2, 4096, 8192),
     # prefill sizes: partial row and channel tiles, K with padding blocks in its last lap
     # (992), many laps (11008); from 256 rows and 8192 channels the LDS-tiled kernel,
     # with 64-channel (8192, 8200) and 128-channel (16400) tiles
@@ -320,7 +323,9 @@ def test_matmul_q8_0_direct_parity(m, n, k):
     assert np.array_equal(host(bd), bd0)
     q8_check(host(out), out0, bd0, sa0, raw, n, k, "q8_0 out", exact=m > 4)
     out2 = empty((m, n), t.float32)        # without the debug outputs
-    mri().matmul_q8_0_direct(dev(x), w, out2)
+    sa2 = empty(m, t.float32)
+    mri().matmul_q8_0_direct(dev(x), w, out2, act_scales_out=sa2)
+    assert np.array_equal(bits(host(sa2)), bits(sa0))
     if m >= 256 and n >= 8192:   # the LDS-tiled kernel: fused fold, within the contract
         q8_check(host(out2), out0, bd0, sa0, raw, n, k, "q8_0 out (prefill kernel)")
     else:

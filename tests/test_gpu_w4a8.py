@@ -32,7 +32,7 @@ W4A8_SHAPES = [
     (1, 16, 32), (1, 16, 256), (1, 50, 96), (1, 1024, 4096), (1, 11008, 4096),
     (1, 64, 11008), (1, 32000 // 8, 4096), (2, 33, 256), (3, 48, 1024), (4, 64, 4096),
     (5, 40, 512), (9, 24, 1024), (16, 272, 4096), (33, 48, 256), (100, 40, 1024),
-    (2, 32, 16384), (1, 48, 20480), (1, 8200, 992),
+    (2, 32, 16384), (1, 48, 20480), (1, 8200, 992), (4, 11008, 4096),
 ]
 
 
@@ -57,7 +57,9 @@ def test_w4a8_bit_exact(m, n, k, order):
     if m > 4:  # the kernels above four rows keep the reference's order
         assert_bits_equal(host(out), out0, "w4a8 out")
     out2 = empty((m, n), t.float32)          # without the debug outputs
-    mri().matmul_q4_0_w4a8(dev(x), w, out2)
+    sa2 = empty(m, t.float32)
+    mri().matmul_q4_0_w4a8(dev(x), w, out2, act_scales_out=sa2)
+    assert np.array_equal(bits(host(sa2)), bits(sa0))
     assert_bits_equal(host(out2), host(out), "w4a8 out (no debug outputs)")
 
 
