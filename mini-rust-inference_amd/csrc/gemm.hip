@@ -36,9 +36,13 @@
 // ROWS instances read the caller's row-major int8 rows directly (no repack
 // pass): an activation stage holds two K steps, 128 bytes of each of the
 // tile's rows, and each DMA instruction moves 8 rows x 128 bytes (whole
-// cache lines).  Piece i (16 bytes) of a row goes to slot i ^ (row % 8) of
-// its 128-byte LDS row, so the fragment reads (32 rows at one piece index)
-// spread over all banks.
+// cache lines).  Piece i (16 bytes) of a row goes to slot i ^ rows_swz(row)
+// of its 128-byte LDS row, so the fragment reads (32 rows at one piece
+// index) spread over all banks: any 8 consecutive rows use 8 different
+// slots, and so do the 8 even and the 8 odd rows of any 16 (rows r and
+// r + 8 share the banks of slot s; with i ^ (row % 8) alone, 16-lane groups
+// read those pairs from one bank and the counters showed a quarter of the
+// LDS cycles in bank conflicts).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -54,6 +58,9 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 constexpr int kWave = 64;
 constexpr int kXcds = 8;
+
+// LDS slot permutation of the ROWS stages for tile row r (bits 0-2 and 3).
+__device__ inline int rows_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
 template <typename F, int... I>
 __device__ inline void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
@@ -194,10 +201,11 @@ __global__ __launch_bounds__(WM * WN * kWave) void k_gemm_int8(
         const int f = wv + NW * j;
         if constexpr (ROWS) {
             // rows of P * 64 bytes: load f covers tile rows 8f .. 8f + 7,
-            // eight lanes a row, lane l%8 bringing piece (l%8) ^ (row%8)
+            // eight lanes a row, lane l%8 (slot l%8) bringing piece
+            // (l%8) ^ rows_swz(row)
             const int rl = 8 * f + (l >> 3);
             const int row = min(m0 + rl, M - 1);  // clamped: rows past M
-            a_src[j] = act + (size_t)row * (size_t)P * 64 + 16 * ((l & 7) ^ (rl & 7));
+            a_src[j] = act + (size_t)row * (size_t)P * 64 + 16 * ((l & 7) ^ rows_swz(rl));
         } else {
             const int g = min(m0 / 32 + (f >> 1), mg - 1);  // clamped: rows past M
             a_src[j] = act + ((size_t)(2 * g + (f & 1)) * kWave + l) * 16;
@@ -258,7 +266,7 @@ __global__ __launch_bounds__(WM * WN * kWave) void k_gemm_int8(
                 if constexpr (ROWS) {  // row r, piece 4 (p % 2) + 2h + l/32 of its 128 bytes
                     const int row = 32 * (wm * TM + i) + (l & 31);
                     const int pc = 4 * (p & 1) + 2 * h + (l >> 5);
-                    fa[S][h][i] = sa_[row * 8 + (pc ^ (row & 7)) - l];
+                    fa[S][h][i] = sa_[row * 8 + (pc ^ rows_swz(row)) - l];
                 } else {
                     fa[S][h][i] = sa_[(2 * (wm * TM + i) + h) * kWave];
                 }
