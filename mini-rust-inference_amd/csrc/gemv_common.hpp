@@ -305,14 +305,16 @@ __device__ inline void act_end(const ActIn &in, bool perm, v4i (&xr)[XR], const 
 // LAZY instances): the same arithmetic as act_end up to the row scale, but
 // the row (RMS-normalized when in.norm_w) goes to LDS as f32 (s_xf, K
 // floats) instead of being quantized; returns 1 / scale.  act_begin has run.
-template <int S, int XR, bool OPS>
+// STAGE false: the row stays in xr only (no norm; the caller quantizes from
+// its registers).
+template <int S, int XR, bool OPS, bool STAGE = true>
 __device__ inline float act_end_lazy(const ActIn &in, v4i (&xr)[XR], const v4i (&wn)[XR],
                                      float *s_xf, float *red, float &scale, bool writer) {
     const int t = threadIdx.x;
     const int K4 = in.K / 4;
     v4i *s_x4 = reinterpret_cast<v4i *>(s_xf);
     const bool norm = OPS && in.norm_w;
-    if (!norm) {
+    if (STAGE && !norm) {
 #pragma unroll
         for (int e = 0; e < XR; ++e)
             if (t + S * kWave * e < K4) s_x4[t + S * kWave * e] = xr[e];

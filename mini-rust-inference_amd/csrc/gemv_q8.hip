@@ -58,6 +58,14 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     constexpr int LG = (MR + 1) / 2;          // lane groups holding results
     static_assert(!FUSED || MR == 1, "the fused prologue quantizes one row");
     static_assert(!LAZY || FUSED, "lap-wise quantization: the fused row");
+    // the plain lap-wise row with one lap in flight and up to four staged
+    // pieces quantizes from the staging registers (0-0.06 us faster at
+    // [1,4096]x[4096,11008] on two boxes, 2 % at K = 992, same outputs);
+    // with two laps in flight the compiler indexed
+    // the pieces through scratch memory and the kernels ran 33-50 % slower,
+    // so those stage the row in LDS
+    constexpr bool kRegRow = LAZY && !OPS && RL == 1 && XR <= 4;
+    static_assert(!kRegRow || TPW == 1, "registers hold this wave's laps only with one tile");
     extern __shared__ v4i s_lds[];
     const int wl = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int tw_ = wl / S;                   // tile of the wave within the WG
@@ -139,24 +147,35 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
         // f32 row staged in LDS; each wave quantizes the laps it consumes
         // (quant_lap)
         act_begin<NW, XR, FUSED, OPS>(in, n16, xr, s_act, red);
-        inv = act_end_lazy<NW, XR, OPS>(in, xr, wn, reinterpret_cast<float *>(s_act), red, sa[0],
-                                        blockIdx.x == 0);
+        inv = act_end_lazy<NW, XR, OPS, !kRegRow>(in, xr, wn, reinterpret_cast<float *>(s_act),
+                                                  red, sa[0], blockIdx.x == 0);
     } else {
         act_begin<NW, XR, FUSED, OPS>(in, n16, xr, s_act, red);
         act_end<NW, XR, FUSED, OPS>(in, true, xr, wn, s_act, red, sa[0], blockIdx.x == 0);
     }
-    // LAZY: quantize lap q of the row (lane l: elements 256q + 4l .. + 3,
-    // zero past K) into this wave's 256-byte area, chunk-permuted
-    auto quant_lap = [&](int q) __attribute__((always_inline)) {
+    // LAZY: quantize lap q = L * S + w of the row (lane l: elements
+    // 256q + 4l .. + 3, zero past K) into this wave's 256-byte area,
+    // chunk-permuted.  kRegRow: those elements are this thread's staged
+    // piece L (piece e of thread 64w + l is float4 64 (w + S e) + l), so
+    // they come from registers instead of LDS.
+    auto quant_lap = [&](int L) __attribute__((always_inline)) {
+        const int q = L * S + w;
         const int kk = 256 * q + 4 * l;
-        const float4 v = kk < in.K ? reinterpret_cast<const float4 *>(s_act)[kk >> 2]
-                                   : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        float4 v = float4{0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (kRegRow) {
+            v4i pc = xr[0];
+#pragma unroll
+            for (int e = 1; e < XR; ++e) pc = L == e ? xr[e] : pc;
+            if (kk < in.K) v = __builtin_bit_cast(float4, pc);
+        } else {
+            if (kk < in.K) v = reinterpret_cast<const float4 *>(s_act)[kk >> 2];
+        }
         const int packed = (round_clamp_i8(v.x * inv) & 255) | ((round_clamp_i8(v.y * inv) & 255) << 8) |
                            ((round_clamp_i8(v.z * inv) & 255) << 16) | (round_clamp_i8(v.w * inv) << 24);
         *reinterpret_cast<int *>(s_lap + ((4 * l) & ~63) + q8_perm((4 * l) & 63)) = packed;
     };
     if constexpr (LAZY) {
-        if (nq > 0) quant_lap(w);
+        if (nq > 0) quant_lap(0);
     }
     float fs[LR];
 #pragma unroll
@@ -231,7 +250,7 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
         }
         if (refill) sr[U] = sp[(size_t)(q + RL * S) * LB];
         if constexpr (LAZY) {
-            if (L + 1 < nq) quant_lap(q + S);  // while the next laps are in flight
+            if (L + 1 < nq) quant_lap(L + 1);  // while the next laps are in flight
         }
     };
 
