@@ -15,10 +15,24 @@
  * ShapeMismatch are returned in the same situations and the same check order
  * as the reference; mri_last_error() returns the thread-local `reason`.
  *
- * Numerics contract: int32 accumulators are bit-exact.  The per-channel INT8
- * f32 epilogue ((f32)acc * s_a) * s_w and the Q8_0 block-ordered f32 sum are
- * bit-exact against the reference's evaluation order.  Q4_0 (W4A32) sums in
- * a different order and is within 1e-5 * max(|ref|, sum|terms|).
+ * Numerics contract, per path (m = rows of the call, n = n_out):
+ *  - Everything integer is bit-exact at every shape: quantized activations
+ *    and their scales, int32 accumulators, Q8_0 / W4A8 block dots.
+ *  - Per-channel INT8 f32 outputs ((f32)acc * s_a) * s_w are bit-exact at
+ *    every shape (matmul_int8, _rows, _from_f32).
+ *  - Q8_0 f32 outputs (matmul_q8_0_direct, its _noalloc variant) are the
+ *    block terms t_b = ((f32)dot_b * s_a) * d_b added in the reference's
+ *    left-to-right block order, bit-exact, for 5 <= m, except when
+ *    m >= 256, n >= 8192 and no block_dots_out is requested.  For m <= 4
+ *    (the decode GEMV adds per-wave partial sums) and in that prefill range
+ *    (an FMA fold, s_a applied once per output) they are within
+ *    1e-5 * max(|ref|, sum_b |t_b|) of the reference.
+ *    mri_matmul_q8_0_direct_exact keeps the block order at every m.
+ *  - W4A8 (extension) f32 outputs equal matmul_q8_0_direct's on the
+ *    expanded blocks: bit-exact for 5 <= m, within the Q8_0 bound for
+ *    m <= 4.
+ *  - Q4_0 W4A32 (matmul_q4_0_dequant and its handle form) sums in another
+ *    order than the reference and is within 1e-5 * max(|ref|, sum|x_k w_k|).
  *
  * Concurrency: calls are asynchronous on `stream`.  Handles are immutable
  * after creation and may be shared by calls on any stream.  Internal scratch
@@ -151,7 +165,14 @@ mri_status mri_matmul_int8_from_f32(const float *input, const size_t *dims,
 
 /* matmul_q8_0_direct, src/ops/matmul/q8_direct.rs:229-289: per-row
  * quantize_symmetric of `input` [m,k], per-block int32 dots, and
- *   out[m,n] = sum over b in block order of ((f32)dot[m,n,b]*s_a[m])*d[n,b].
+ *   out[m,n] = sum over b of t_b,  t_b = ((f32)dot[m,n,b]*s_a[m])*d[n,b].
+ * The reference adds the t_b left to right in block order.  Here the
+ * activation scales and block dots are bit-exact; out is bit-exact for
+ * 5 <= m outside the prefill range below, and otherwise within
+ * 1e-5 * max(|ref|, sum_b |t_b|): at m <= 4 (the decode GEMV splits K over
+ * waves and adds their partial sums) and at m >= 256, n_out >= 8192 without
+ * block_dots_out (the LDS-tiled GEMM folds fma((f32)dot, d, acc) and
+ * multiplies by s_a once).
  * InvalidShape unless ndim == 2; ShapeMismatch when dims[1] != k_in.
  * Optional outputs (nullable, device): block_dots_out [m, n_out, k_in/32]
  * int32, act_scales_out [m]. */
@@ -159,6 +180,17 @@ mri_status mri_matmul_q8_0_direct(const float *input, const size_t *dims,
                                   size_t ndim, const mri_q8_0_matrix *w,
                                   float *out, int32_t *block_dots_out,
                                   float *act_scales_out, void *stream);
+
+/* matmul_q8_0_direct (src/ops/matmul/q8_direct.rs:229-289) with the
+ * reference's evaluation order kept at every m: out is bit-identical to
+ * the left-to-right block sum of q8_direct.rs:269-282 (each output's terms
+ * are added by one lane in block order).  Same arguments, checks and
+ * optional outputs as mri_matmul_q8_0_direct; slower at m <= 4 and at
+ * prefill sizes, where that entry point uses the reordered kernels. */
+mri_status mri_matmul_q8_0_direct_exact(const float *input, const size_t *dims,
+                                        size_t ndim, const mri_q8_0_matrix *w,
+                                        float *out, int32_t *block_dots_out,
+                                        float *act_scales_out, void *stream);
 
 /* No counterpart in the reference.  For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
@@ -220,13 +252,6 @@ size_t mri_q4_0_matrix_k_in(const mri_q4_0_matrix *w);
 size_t mri_q4_0_matrix_device_bytes(const mri_q4_0_matrix *w);
 void mri_q4_0_matrix_destroy(mri_q4_0_matrix *w);
 
-/* Per-row quantize_symmetric of `input` [m,k] (src/quant/int8/symmetric.rs:
- * 42-57), per-block exact int32 dots with the quants, and
- *   out[m,n] = sum over b in block order of ((f32)dot[m,n,b]*s_a[m])*d[n,b],
- * i.e. mri_matmul_q8_0_direct on the blocks with quants nibble - 8.
- * InvalidShape unless ndim == 2; ShapeMismatch when dims[1] != k_in.
- * Optional outputs (nullable, device):
- * block_dots_out [m, n_out, k_in/32] int32, act_scales_out [m]. */
 /* matmul_q4_0_dequant (src/ops/matmul/q4_0.rs:94-181, W4A32: f32 inputs,
  * no activation quantization) on a device-resident Q4_0 handle instead of
  * raw blocks: the weights stay in the handle's 4-bit lap-block layout and
@@ -234,12 +259,24 @@ void mri_q4_0_matrix_destroy(mri_q4_0_matrix *w);
  * launch.  Same checks as mri_matmul_q4_0_dequant for the input (ndim != 2
  * -> InvalidShape, dims[1] != k_in -> ShapeMismatch); input rows 16-byte
  * aligned.  Outputs within 1e-5 * max(|out|, sum_k |x_k w_k|) of the
- * reference's sequential sum.  MRI_ERR_UNSUPPORTED when four f32 rows of
- * K do not fit the 64 KiB LDS staging (K > 4096 at four rows, > 16384 at
- * one). */
+ * reference's sequential sum.  Rows run in launches of 1, 2 or 4 (3 rows
+ * are staged as 4); MRI_ERR_UNSUPPORTED when a launch's f32 rows
+ * (rows * K' * 4 bytes, K' = k_in rounded up to 256) exceed 64 KiB of LDS,
+ * i.e. K > 4096 at three or four rows, > 8192 at two, > 16384 at one.  The
+ * kernel's LDS also holds up to 3.75 KiB of per-wave partial sums. */
 mri_status mri_matmul_q4_0_dequant_matrix(const float *input, const size_t *dims, size_t ndim,
                                           const mri_q4_0_matrix *w, float *out, void *stream);
 
+/* Per-row quantize_symmetric of `input` [m,k] (src/quant/int8/symmetric.rs:
+ * 42-57), per-block exact int32 dots with the quants, and
+ *   out[m,n] = sum over b of ((f32)dot[m,n,b]*s_a[m])*d[n,b],
+ * i.e. mri_matmul_q8_0_direct on the blocks with quants nibble - 8: block
+ * dots and activation scales bit-exact; out bit-exact for m >= 5 (block
+ * order) and within 1e-5 * max(|ref|, sum_b |t_b|) for m <= 4 (per-wave
+ * partial sums of the decode GEMV).
+ * InvalidShape unless ndim == 2; ShapeMismatch when dims[1] != k_in.
+ * Optional outputs (nullable, device):
+ * block_dots_out [m, n_out, k_in/32] int32, act_scales_out [m]. */
 mri_status mri_matmul_q4_0_w4a8(const float *input, const size_t *dims, size_t ndim,
                                 const mri_q4_0_matrix *w, float *out,
                                 int32_t *block_dots_out, float *act_scales_out,

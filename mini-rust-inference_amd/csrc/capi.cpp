@@ -804,12 +804,14 @@ static mri_status noalloc_scratch(void **ptr) {
     return MRI_OK;
 }
 
-// matmul_q8_0_direct's body, shared with the W4A8 entry point (d.w4) and
-// the no-allocation variant (fixed: staging in the file's device array).
+// matmul_q8_0_direct's body, shared with the W4A8 entry point (d.w4), the
+// no-allocation variant (fixed: staging in the file's device array) and the
+// block-ordered variant (exact: the skinny kernel, whose lanes add each
+// output's block terms in block order, at every m).
 static mri_status matmul_blocks(const char *name, const float *input, const size_t *dims,
                                 size_t ndim, const Q8MatrixDev &d, float *out,
                                 int32_t *block_dots_out, float *act_scales_out,
-                                void *stream, bool fixed = false) {
+                                void *stream, bool fixed = false, bool exact = false) {
     if (ndim && !dims) return set_error(MRI_ERR_INVALID_ARGUMENT, "dims is null");
     if (ndim != 2)
         return set_error(MRI_ERR_INVALID_SHAPE,
@@ -827,7 +829,7 @@ static mri_status matmul_blocks(const char *name, const float *input, const size
     mri_status st = current_device(&dev);
     if (st) return st;
     auto s = static_cast<hipStream_t>(stream);
-    if (d.n_out > 0 && gemv_fusable(m, k, input) &&
+    if (!exact && d.n_out > 0 && gemv_fusable(m, k, input) &&
         gemv_q8_supported(true, m, d.n_tiles, k, d.kp))
         return launch_gemv_q8_0(input, nullptr, m, nullptr, d, out, block_dots_out,
                                 act_scales_out, s);
@@ -852,6 +854,7 @@ static mri_status matmul_blocks(const char *name, const float *input, const size
     st = launch_quantize_rows(input, m, k, d.kp, true, act, nullptr, sc, s);
     if (st) return st;
     if (d.n_out == 0) return MRI_OK;
+    if (exact) return launch_skinny_q8_0(act, m, sc, d, out, block_dots_out, s);
     return run_q8(act, m, sc, d, out, block_dots_out, s);
 }
 
@@ -864,6 +867,15 @@ mri_status mri_matmul_q8_0_direct(const float *input, const size_t *dims, size_t
     if (!w) return set_error(MRI_ERR_INVALID_ARGUMENT, "null weight handle");
     return matmul_blocks("matmul_q8_0_direct", input, dims, ndim, w->d, out, block_dots_out,
                          act_scales_out, stream);
+}
+
+mri_status mri_matmul_q8_0_direct_exact(const float *input, const size_t *dims, size_t ndim,
+                                        const mri_q8_0_matrix *w, float *out,
+                                        int32_t *block_dots_out, float *act_scales_out,
+                                        void *stream) {
+    if (!w) return set_error(MRI_ERR_INVALID_ARGUMENT, "null weight handle");
+    return matmul_blocks("matmul_q8_0_direct", input, dims, ndim, w->d, out, block_dots_out,
+                         act_scales_out, stream, false, true);
 }
 
 mri_status mri_matmul_q8_0_direct_noalloc(const float *input, const size_t *dims, size_t ndim,

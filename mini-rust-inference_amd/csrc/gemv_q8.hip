@@ -566,34 +566,46 @@ void dispatch_q8_dbg(bool dbg, CfgQ8 c, ActIn in, size_t m, const float *sa_rows
 }
 
 // W4A32 on 4-bit lap blocks: rows in groups of up to four per launch,
-// four waves per tile from 512 tiles up, else 8 (K <= 4096) or 16.
+// four waves per tile from 512 tiles up, else 8 (K <= 4096) or 16.  LDS:
+// the MR f32 rows (at most kMaxLds) plus S - 1 waves' partial sums of MR x
+// 16 outputs (at most 3.75 KiB), so an instance may take more than 64 KiB
+// and declares its maximum once per device.
+template <int MR, int S>
+constexpr size_t w4a32_sum_bytes() { return (size_t)(S - 1) * MR * 16 * 4; }
+
 template <int MR, int S, int RL, int XR>
-void launch_w4a32_inst(const float *x, size_t m, size_t k, const Q8MatrixDev &w, float *out,
-                       hipStream_t st) {
-    const size_t lds = ((size_t)MR * w.kp + (size_t)(S - 1) * MR * 16) * 4;
+mri_status launch_w4a32_inst(const float *x, size_t m, size_t k, const Q8MatrixDev &w,
+                             float *out, hipStream_t st) {
+    const size_t lds = (size_t)MR * w.kp * 4 + w4a32_sum_bytes<MR, S>();
+    static DeviceOnce attr;
+    MRI_HIP(attr.run([](int) {
+        return hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemv_w4a32<MR, S, RL, XR>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   (int)(kMaxLds + w4a32_sum_bytes<MR, S>()));
+    }));
     hipLaunchKernelGGL((k_gemv_w4a32<MR, S, RL, XR>), dim3((unsigned)w.n_tiles), dim3(S * kWave),
                        lds, st, x, (int)m, (int)k, (int)w.kp, reinterpret_cast<const v4i *>(w.laps),
                        (int)w.n_out, (int)w.n_tiles, (int)groups_of(w), (int)w.n_blocks, out);
+    return MRI_OK;
 }
 
+// MRI_ERR_UNSUPPORTED when the MR f32 rows exceed kMaxLds.
 template <int MR>
-bool launch_w4a32_rows(const float *x, size_t m, size_t k, const Q8MatrixDev &w, float *out,
-                       hipStream_t st) {
+mri_status launch_w4a32_rows(const float *x, size_t m, size_t k, const Q8MatrixDev &w,
+                             float *out, hipStream_t st) {
     const size_t G = groups_of(w);
     const int s = w.n_tiles >= 512 ? 4 : G > 16 ? 16 : 8;
     const size_t n4 = (size_t)MR * w.kp / 4;
     const size_t per = ceil_div(n4, (size_t)s * kWave);  // float4s per thread
-    if ((size_t)MR * w.kp * 4 > kMaxLds) return false;
-#define MRI_W4A32(S_, RL_, XR_)                                                  \
-    if (s == S_ && per <= XR_) {                                                  \
-        launch_w4a32_inst<MR, S_, RL_, XR_>(x, m, k, w, out, st);                 \
-        return true;                                                             \
-    }
-    MRI_W4A32(4, 1, 4) MRI_W4A32(4, 1, 16)
-    MRI_W4A32(8, 2, 2) MRI_W4A32(8, 2, 8)
-    MRI_W4A32(16, 2, 1) MRI_W4A32(16, 2, 4)
+    if ((size_t)MR * w.kp * 4 <= kMaxLds) {
+#define MRI_W4A32(S_, RL_, XR_) \
+    if (s == S_ && per <= XR_) return launch_w4a32_inst<MR, S_, RL_, XR_>(x, m, k, w, out, st);
+        MRI_W4A32(4, 1, 4) MRI_W4A32(4, 1, 16)
+        MRI_W4A32(8, 2, 2) MRI_W4A32(8, 2, 8)
+        MRI_W4A32(16, 2, 1) MRI_W4A32(16, 2, 4)
 #undef MRI_W4A32
-    return false;
+    }
+    return set_error(MRI_ERR_UNSUPPORTED, "w4a32: K too large for the LDS staging");
 }
 
 }  // namespace
@@ -609,10 +621,10 @@ mri_status launch_gemv_w4a32(const float *x, size_t m, size_t k, const Q8MatrixD
         const size_t mc = std::min<size_t>(4, m - m0);
         const float *xs = x + m0 * k;
         float *os = out + m0 * w.n_out;
-        const bool ok = mc == 1   ? launch_w4a32_rows<1>(xs, mc, k, w, os, st)
-                        : mc == 2 ? launch_w4a32_rows<2>(xs, mc, k, w, os, st)
-                                  : launch_w4a32_rows<4>(xs, mc, k, w, os, st);
-        if (!ok) return set_error(MRI_ERR_UNSUPPORTED, "w4a32: K too large for the LDS staging");
+        const mri_status r = mc == 1   ? launch_w4a32_rows<1>(xs, mc, k, w, os, st)
+                             : mc == 2 ? launch_w4a32_rows<2>(xs, mc, k, w, os, st)
+                                       : launch_w4a32_rows<4>(xs, mc, k, w, os, st);
+        if (r) return r;
         MRI_LAUNCHED("k_gemv_w4a32");
     }
     return MRI_OK;

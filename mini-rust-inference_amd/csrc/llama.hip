@@ -774,8 +774,9 @@ __global__ __launch_bounds__(256) void k_argmax_keys(const unsigned long long *_
 // The candidates are stored and loaded with device-scope (sc1) accesses,
 // which reach the point of coherence of all XCDs, and each block waits for
 // its stores to complete before it counts.  The count is an acquire-release
-// read-modify-write at system scope (performed past every XCD's L2), so the
-// candidates happen-before the last block's reads in the memory model too.
+// read-modify-write at agent (device) scope, which covers every XCD of the
+// device, so the candidates happen-before the last block's reads in the
+// memory model too.
 constexpr int kArgSplit = 64;
 __global__ __launch_bounds__(256) void k_argmax_split(const float *__restrict__ v, int n,
                                                       uint32_t *__restrict__ idx,

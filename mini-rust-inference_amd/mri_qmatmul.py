@@ -54,6 +54,7 @@ _SIGS = {
     "mri_matmul_int8_rows": ([P, SZ, P, P, SZ, P, P, P], ST),
     "mri_matmul_int8_from_f32": ([P, P, SZ, P, P, P, P, P, P], ST),
     "mri_matmul_q8_0_direct": ([P, P, SZ, P, P, P, P, P], ST),
+    "mri_matmul_q8_0_direct_exact": ([P, P, SZ, P, P, P, P, P], ST),
     "mri_matmul_q8_0_direct_noalloc": ([P, P, SZ, P, P, P, P, P], ST),
     "mri_matmul_q4_0_dequant_matrix": ([P, P, SZ, P, P, P], ST),
     "mri_matmul_q4_0_dequant": ([P, P, SZ, P, SZ, SZ, SZ, P, P], ST),
@@ -316,6 +317,16 @@ def matmul_q8_0_direct(x, w: Q8Matrix, out, block_dots_out=None, act_scales_out=
     check(lib().mri_matmul_q8_0_direct(_ptr(x), dims, nd, w.h, _ptr(out),
                                        _ptr(block_dots_out), _ptr(act_scales_out),
                                        _stream(stream)))
+
+
+def matmul_q8_0_direct_exact(x, w: Q8Matrix, out, block_dots_out=None, act_scales_out=None,
+                             stream=None, shape=None):
+    """matmul_q8_0_direct with the reference's left-to-right block order kept
+    at every row count: f32 outputs bit-identical to q8_direct.rs:269-282."""
+    dims, nd = _dims(tuple(x.shape) if shape is None else shape)
+    check(lib().mri_matmul_q8_0_direct_exact(_ptr(x), dims, nd, w.h, _ptr(out),
+                                             _ptr(block_dots_out), _ptr(act_scales_out),
+                                             _stream(stream)))
 
 
 def matmul_q8_0_direct_noalloc(x, w: Q8Matrix, out, block_dots_out=None, act_scales_out=None,

@@ -96,3 +96,43 @@ def assert_q8_close(got, exp, terms_abs, what="", rel=1e-5):
             f"{what}: {bad.size} of {got.size} values outside {rel} * max(|ref|, sum|t_b|); "
             f"first at {np.unravel_index(i, got.shape)}: got {got.ravel()[i]!r} expected "
             f"{exp.ravel()[i]!r} (bound {bound.ravel()[i]:.3g})")
+
+
+_POOL = None
+
+
+def pool():
+    """Host threads for the oracle at full sizes (ctypes releases the GIL)."""
+    global _POOL
+    if _POOL is None:
+        import os
+        from concurrent.futures import ThreadPoolExecutor
+        _POOL = ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 4))
+    return _POOL
+
+
+def q8_oracle_sliced(x, raw, n, k, slice_rows=256):
+    """The oracle's matmul_q8_0_direct over slices of the weight rows, run on
+    host threads (each input row is quantized on its own, so the slices are
+    independent and the result equals one call's), with the contract's
+    sum_b |t_b| of every output computed from each slice's block dots.
+    Returns (out [M, N] f32, terms_abs [M, N] f64)."""
+    import closed_form as CF
+    import oracle_lib as O
+    x = np.ascontiguousarray(x, F32)
+    m = x.shape[0]
+    row = (k // 32) * 34
+    out = np.empty((m, n), F32)
+    terms = np.empty((m, n), np.float64)
+    cuts = list(range(0, n, slice_rows)) + [n]
+
+    def run(i):
+        a, b = cuts[i], cuts[i + 1]
+        part = raw[a * row:b * row]
+        o, bd, sa = O.matmul_q8_0_direct(x, part, b - a, k, want_block_dots=True)
+        d, _ = CF.q8_0_split(part, b - a, k)
+        out[:, a:b] = o
+        terms[:, a:b] = q8_terms_abs_sum(bd, sa, d)
+
+    list(pool().map(run, range(len(cuts) - 1)))
+    return out, terms

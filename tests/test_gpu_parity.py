@@ -3,8 +3,10 @@
 Integer results (quantized activations, int32 accumulators, block dots) and
 the per-channel INT8 f32 outputs must be bit-identical.  Q8_0 f32 outputs
 are within 1e-5 * max(|ref|, sum_b |t_b|) of the reference's left-to-right
-block sum (the decode GEMV, M <= 4, adds per-wave partial sums); above four
-rows, where the kernel keeps the reference's order, they are bit-identical.
+block sum where the kernel reorders it (the decode GEMV, M <= 4, adds
+per-wave partial sums; the LDS-tiled prefill GEMM, M >= 256 and N >= 8192
+without block dots, folds with FMAs) and bit-identical elsewhere (the
+skinny kernel, and the block-ordered entry point at every M).
 Q4_0 (W4A32) outputs are within 1e-5 * max(|ref|, sum_k |x_k w_k|).
 """
 import sys
@@ -15,7 +17,8 @@ import pytest
 import closed_form as CF
 import oracle_lib as O
 from gpu_util import (F32, assert_bits_equal, assert_q8_close, bits, dev, empty, host,
-                      q8_terms_abs_sum, synth_int8_weights, synth_q4_0, synth_q8_0, torch)
+                      q8_oracle_sliced, q8_terms_abs_sum, synth_int8_weights, synth_q4_0,
+                      synth_q8_0, torch)
 
 pytestmark = pytest.mark.gpu
 
@@ -249,6 +252,35 @@ def test_matmul_int8_rows_bit_exact(m, n, k):
     assert_bits_equal(host(out), out0, "matmul_int8_rows out")
 
 
+@pytest.mark.parametrize("m,n,k", [(128, 4096, 4096), (128, 11008, 4096), (512, 4096, 4096),
+                                   (512, 11008, 4096), (2048, 4096, 4096), (2048, 11008, 4096),
+                                   (768, 11008, 4096)])
+def test_matmul_int8_rows_prefill_closed_form(m, n, k):
+    """matmul_int8 with one activation scale per row (the per-row mode of the
+    prefill benchmark) at the prefill shapes (M = 128 / 512 / 2048, N = 4096 /
+    11008, K = 4096) and at 768 x 11008 (stream-K): int32 accumulators
+    against an exact float64 matmul, f32 outputs bit for bit against
+    ((f32)acc * s_a[m]) * s_w[n] in float32 (int8.rs:93 with s_a per row),
+    both with the int32 output and without it (the staged-tile epilogue)."""
+    say(f"matmul_int8_rows prefill m={m} n={n} k={k}")
+    t = torch()
+    rng = np.random.default_rng(m + 11 * n + k)
+    wq = rng.integers(-127, 128, (n, k)).astype(np.int8)
+    ws = rng.uniform(1e-4, 1e-3, n).astype(F32)
+    aq = rng.integers(-127, 128, (m, k)).astype(np.int8)
+    sas = rng.uniform(1e-3, 1e-1, m).astype(F32)
+    acc0 = (aq.astype(np.float64) @ wq.astype(np.float64).T).astype(np.int32)
+    out0 = (acc0.astype(F32) * sas[:, None]) * ws[None, :]
+    w = mri().QMatrix.from_host(wq, ws)
+    out, acc = empty((m, n), t.float32), empty((m, n), t.int32)
+    mri().matmul_int8_rows(dev(aq), dev(sas), w, m, out, acc)
+    assert np.array_equal(host(acc), acc0)
+    assert_bits_equal(host(out), out0, "matmul_int8_rows prefill out (with acc)")
+    out2 = empty((m, n), t.float32)
+    mri().matmul_int8_rows(dev(aq), dev(sas), w, m, out2)
+    assert_bits_equal(host(out2), out0, "matmul_int8_rows prefill out")
+
+
 @pytest.mark.parametrize("m,n,k", [(1, 11008, 4096), (4, 64, 4096), (32, 128, 4096),
                                    (3, 20, 96), (200, 48, 256), (300, 512, 4096),
                                    (64, 100, 96)])
@@ -330,6 +362,140 @@ def test_matmul_q8_0_direct_parity(m, n, k):
         q8_check(host(out2), out0, bd0, sa0, raw, n, k, "q8_0 out (prefill kernel)")
     else:
         assert_bits_equal(host(out2), host(out), "q8_0 out (no debug outputs)")
+
+
+@pytest.mark.parametrize("m,n,k", [(512, 12288, 4096), (512, 22016, 4096), (512, 32000, 4096)])
+def test_q8_0_prefill_gemm_full_shapes(m, n, k):
+    """The LDS-tiled Q8_0 GEMM (m >= 256, n >= 8192, no block dots) at the
+    shapes the decoder layer's prefill runs it at (fused q/k/v, fused
+    gate/up, lm_head; K = 4096): every output within the contract of the
+    oracle's sequential block sum (q8_direct.rs:229-289), and the activation
+    scales bit-exact."""
+    say(f"matmul_q8_0_direct prefill gemm m={m} n={n} k={k}")
+    t = torch()
+    rng = np.random.default_rng(m + n + k)
+    raw = synth_q8_0(rng, n, k, with_min=True)
+    x = rng.standard_normal((m, k)).astype(F32)
+    w = mri().Q8Matrix.from_raw_bytes(raw, n, k)
+    out = empty((m, n), t.float32)
+    sa = empty(m, t.float32)
+    mri().matmul_q8_0_direct(dev(x), w, out, act_scales_out=sa)
+    got, sa_got = host(out), host(sa)
+    out0, terms = q8_oracle_sliced(x, raw, n, k)
+    assert np.array_equal(bits(sa_got), bits(CF.quantize_rows(x)[1]))
+    assert_q8_close(got, out0, terms, f"q8_0 prefill gemm {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 11008, 4096), (2, 300, 256), (4, 4096, 4096),
+                                   (3, 64, 11008), (8, 48, 512), (256, 8192, 256),
+                                   (300, 8200, 512)])
+def test_matmul_q8_0_direct_exact(m, n, k):
+    """mri_matmul_q8_0_direct_exact keeps the reference's block order at
+    every row count: bit-identical to the oracle where the default entry
+    point reorders (m <= 4, and m >= 256 with n >= 8192), with and without
+    block dots."""
+    say(f"matmul_q8_0_direct_exact m={m} n={n} k={k}")
+    t = torch()
+    rng = np.random.default_rng(m * 13 + n + k)
+    raw = synth_q8_0(rng, n, k, with_min=True)
+    x = rng.standard_normal((m, k)).astype(F32)
+    out0, bd0, sa0 = O.matmul_q8_0_direct(x, raw, n, k, want_block_dots=True)
+    w = mri().Q8Matrix.from_raw_bytes(raw, n, k)
+    out, sa = empty((m, n), t.float32), empty(m, t.float32)
+    mri().matmul_q8_0_direct_exact(dev(x), w, out, act_scales_out=sa)
+    assert np.array_equal(bits(host(sa)), bits(sa0))
+    assert_bits_equal(host(out), out0, "q8_0 exact out")
+    out2, bd = empty((m, n), t.float32), empty((m, n, k // 32), t.int32)
+    mri().matmul_q8_0_direct_exact(dev(x), w, out2, bd)
+    assert np.array_equal(host(bd), bd0)
+    assert_bits_equal(host(out2), out0, "q8_0 exact out (with block dots)")
+
+
+# f16 block scales beyond the positive normals: subnormals (exact in f32,
+# m * 2^-24), both zeros, negative normals and subnormals, the extremes of
+# the normal range (f16_to_f32, quantization.rs:416-459)
+F16_SPECIAL = np.array([0x0001, 0x0002, 0x01FF, 0x0200, 0x03FF, 0x0000, 0x8000, 0x8001,
+                        0x83FF, 0x0400, 0x8400, 0x9C00, 0xA1A3, 0x7BFF, 0xFBFF, 0x2E66,
+                        0x1C00, 0x9400], np.uint16)
+
+
+def special_scale_blocks(rng, n, k):
+    q = rng.integers(-128, 128, (n, k)).astype(np.int8)
+    d = rng.choice(F16_SPECIAL, (n, k // 32)).astype(np.uint16)
+    return CF.q8_0_pack(d, q)
+
+
+# the M = 1 GEMV (fused quantization), the M = 3 GEMV on quantized rows, the
+# skinny kernel (8 and 40 rows), the LDS-tiled prefill GEMM (256 x 8192)
+SPECIAL_SHAPES = [(1, 4096, 4096), (1, 48, 992), (3, 64, 1024), (8, 48, 512), (40, 64, 256),
+                  (256, 8192, 256)]
+
+
+@pytest.mark.parametrize("m,n,k", SPECIAL_SHAPES)
+def test_q8_0_special_f16_scales(m, n, k):
+    """Subnormal, zero, negative and extreme f16 block scales through every
+    Q8_0 kernel: block dots bit-exact, f32 within the contract (bit-exact
+    where the kernel keeps the block order)."""
+    say(f"matmul_q8_0_direct special scales m={m} n={n} k={k}")
+    t = torch()
+    rng = np.random.default_rng(m * 5 + n + k)
+    raw = special_scale_blocks(rng, n, k)
+    x = rng.standard_normal((m, k)).astype(F32)
+    out0, bd0, sa0 = O.matmul_q8_0_direct(x, raw, n, k, want_block_dots=True)
+    w = mri().Q8Matrix.from_raw_bytes(raw, n, k)
+    out = empty((m, n), t.float32)
+    mri().matmul_q8_0_direct(dev(x), w, out)   # the kernel the shape dispatches to
+    q8_check(host(out), out0, bd0, sa0, raw, n, k, "q8_0 special scales")
+    bd = empty((m, n, k // 32), t.int32)
+    out2 = empty((m, n), t.float32)
+    mri().matmul_q8_0_direct(dev(x), w, out2, bd)
+    assert np.array_equal(host(bd), bd0)
+    q8_check(host(out2), out0, bd0, sa0, raw, n, k, "q8_0 special scales (block dots)",
+             exact=m > 4)
+
+
+def assert_same_class(got, exp, what):
+    """Where the reference is not finite, the same class: NaN for NaN, the
+    same infinity for an infinity."""
+    got, exp = np.asarray(got, F32), np.asarray(exp, F32)
+    en, gn = np.isnan(exp), np.isnan(got)
+    assert np.array_equal(en, gn), f"{what}: NaN positions differ ({int(en.sum())} expected)"
+    ei = np.isinf(exp)
+    assert np.array_equal(ei, np.isinf(got)), f"{what}: infinity positions differ"
+    assert np.array_equal(exp[ei], got[ei]), f"{what}: infinity signs differ"
+
+
+@pytest.mark.parametrize("m,n,k", SPECIAL_SHAPES)
+def test_q8_0_nonfinite_f16_scales(m, n, k):
+    """Infinite and NaN f16 block scales decode to inf / NaN
+    (quantization.rs:416-459), so the outputs they reach are inf or NaN in
+    every summation order: the GPU gives the same class at the same places,
+    and the finite outputs within the contract."""
+    say(f"matmul_q8_0_direct non-finite scales m={m} n={n} k={k}")
+    t = torch()
+    rng = np.random.default_rng(m * 3 + n + k + 1)
+    raw = special_scale_blocks(rng, n, k)
+    # one block of about a third of the weight rows gets +inf, -inf or a NaN
+    # (two payloads) as its scale
+    blk = np.asarray(raw, np.uint8).reshape(n, k // 32, 34).copy()
+    rows = np.flatnonzero(rng.random(n) < 0.35)
+    cols = rng.integers(0, k // 32, rows.size)
+    bad = rng.choice(np.array([0x7C00, 0xFC00, 0x7E00, 0xFD01], np.uint16), rows.size)
+    blk[rows, cols, 0] = bad & 0xFF
+    blk[rows, cols, 1] = bad >> 8
+    raw = blk.ravel()
+    x = rng.standard_normal((m, k)).astype(F32)
+    out0, bd0, sa0 = O.matmul_q8_0_direct(x, raw, n, k, want_block_dots=True)
+    w = mri().Q8Matrix.from_raw_bytes(raw, n, k)
+    out = empty((m, n), t.float32)
+    mri().matmul_q8_0_direct(dev(x), w, out)
+    got = host(out)
+    assert_same_class(got, out0, "q8_0 non-finite scales")
+    fin_out = np.isfinite(out0)
+    d2, _ = CF.q8_0_split(raw, n, k)
+    with np.errstate(invalid="ignore"):
+        terms = q8_terms_abs_sum(bd0, sa0, np.where(np.isfinite(d2), d2, 0.0))
+    assert_q8_close(got[fin_out], out0[fin_out], terms[fin_out], "q8_0 non-finite: finite outputs")
 
 
 def test_q8_0_reference_encoder_weights():

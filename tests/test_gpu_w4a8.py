@@ -38,7 +38,7 @@ W4A8_SHAPES = [
 
 @pytest.mark.parametrize("m,n,k", W4A8_SHAPES)
 @pytest.mark.parametrize("order", [0, 1])
-def test_w4a8_bit_exact(m, n, k, order):
+def test_w4a8_parity(m, n, k, order):
     say(f"matmul_q4_0_w4a8 m={m} n={n} k={k} order={order}")
     t = torch()
     rng = np.random.default_rng(m * 7 + n + k + order)

@@ -61,3 +61,42 @@ def test_noalloc_rejects_inputs_past_its_staging():
         mri().matmul_q8_0_direct_noalloc(x, w, out)
     assert e.value.kind == "Unsupported"
     assert "no-allocation" in str(e.value)
+
+
+def test_noalloc_allocates_nothing():
+    """On a stream the library has not seen, the allocating entry point grows
+    its per-stream staging (a hipMalloc of about 4 MiB here, which the
+    device's free-memory readout shows), while the no-allocation entry point
+    leaves the free device memory exactly as it was.  The fixed array itself
+    (MRI_NOALLOC_SCRATCH_BYTES, a file-scope device variable) is placed in
+    device memory by the HIP runtime when the first call looks up its
+    address, once per device and process; a first call before the
+    measurement makes sure of that.  A stream's first kernel also makes the
+    runtime set up per-queue device memory (kernel arguments), so both
+    streams run a small torch kernel before the readout starts."""
+    t = torch()
+    n, k, m = 64, 4096, 900          # staging m * 4096 + 4 * m bytes: 3.5 MiB
+    rng = np.random.default_rng(17)
+    w = mri().Q8Matrix.from_raw_bytes(synth_q8_0(rng, n, k), n, k)
+    x = dev(rng.standard_normal((m, k)).astype(F32))
+    outs = [empty((m, n), t.float32) for _ in range(2)]
+    mri().matmul_q8_0_direct_noalloc(x[:2], w, outs[1][:2])  # the array is in place
+    s_alloc, s_fixed = t.cuda.Stream(), t.cuda.Stream()
+    for st in (s_alloc, s_fixed):
+        with t.cuda.stream(st):
+            outs[0].zero_()
+    t.cuda.synchronize()
+    free0 = t.cuda.mem_get_info()[0]
+    with t.cuda.stream(s_alloc):
+        mri().matmul_q8_0_direct(x, w, outs[0])
+    t.cuda.synchronize()
+    free1 = t.cuda.mem_get_info()[0]
+    assert free0 - free1 >= 3 << 20, (free0, free1)  # the readout sees a staging allocation
+    with t.cuda.stream(s_fixed):
+        mri().matmul_q8_0_direct_noalloc(x, w, outs[1])
+        mri().matmul_q8_0_direct_noalloc(x[:5], w, outs[1][:5])
+    t.cuda.synchronize()
+    free2 = t.cuda.mem_get_info()[0]
+    assert free2 == free1, (free1, free2)
+    o0, o1 = host(outs[0]), host(outs[1])
+    assert np.array_equal(bits(o0), bits(o1))  # rows 0-4 recomputed from the same rows
