@@ -498,6 +498,70 @@ def test_q8_0_nonfinite_f16_scales(m, n, k):
     assert_q8_close(got[fin_out], out0[fin_out], terms[fin_out], "q8_0 non-finite: finite outputs")
 
 
+def test_q8_0_graph_replay_and_streams():
+    """matmul_q8_0_direct at several row counts (the quantize pass plus the
+    decode GEMV or the skinny kernel) captured in one HIP graph: every replay
+    agrees with the oracle for the input it sees (new data copied in between
+    replays, eager work and synchronizations between them), and so do calls
+    on two streams at once and back-to-back calls of different sizes."""
+    t = torch()
+    rng = np.random.default_rng(77)
+    n, k = 272, 1024
+    raw = synth_q8_0(rng, n, k, with_min=True)
+    w = mri().Q8Matrix.from_raw_bytes(raw, n, k)
+    sizes = [8, 3, 32, 17, 2]
+    xs = [dev(np.zeros((m, k), F32)) for m in sizes]
+    outs = [empty((m, n), t.float32) for m in sizes]
+
+    def calls():
+        for x, o in zip(xs, outs):
+            mri().matmul_q8_0_direct(x, w, o)
+
+    def check(host_xs, what):
+        for m, hx, o in zip(sizes, host_xs, outs):
+            out0, bd0, sa0 = O.matmul_q8_0_direct(hx, raw, n, k, want_block_dots=True)
+            q8_check(host(o), out0, bd0, sa0, raw, n, k, f"{what} m={m}")
+
+    s = t.cuda.Stream()
+    s.wait_stream(t.cuda.current_stream())
+    with t.cuda.stream(s):   # the stream's staging exists before capture
+        calls()
+    t.cuda.synchronize()
+    g = t.cuda.CUDAGraph()
+    with t.cuda.graph(g, stream=s):
+        calls()
+    for rep in range(4):
+        hx = [rng.standard_normal((m, k)).astype(F32) * (rep + 1) for m in sizes]
+        for x, h in zip(xs, hx):
+            x.copy_(dev(h))
+        for o in outs:
+            o.zero_()
+        t.cuda.synchronize()
+        g.replay()
+        t.cuda.synchronize()
+        check(hx, f"graph replay {rep}")
+        mri().matmul_q8_0_direct(xs[0], w, outs[0])   # eager work between replays
+        t.cuda.synchronize()
+    # two streams at once, then back-to-back sizes on the default stream
+    hx = [rng.standard_normal((m, k)).astype(F32) for m in sizes]
+    for x, h in zip(xs, hx):
+        x.copy_(dev(h))
+    t.cuda.synchronize()
+    s1, s2 = t.cuda.Stream(), t.cuda.Stream()
+    with t.cuda.stream(s1):
+        mri().matmul_q8_0_direct(xs[0], w, outs[0])
+        mri().matmul_q8_0_direct(xs[2], w, outs[2])
+    with t.cuda.stream(s2):
+        mri().matmul_q8_0_direct(xs[1], w, outs[1])
+        mri().matmul_q8_0_direct(xs[3], w, outs[3])
+        mri().matmul_q8_0_direct(xs[4], w, outs[4])
+    t.cuda.synchronize()
+    check(hx, "two streams")
+    calls()
+    calls()
+    check(hx, "back to back")
+
+
 def test_q8_0_reference_encoder_weights():
     """Weights built by create_q8_0_block (dequant.rs:389-421), as
     Q8_0WeightMatrix::from_f32_tensor does."""
