@@ -255,6 +255,15 @@ struct RowOps {
     // last of equal maxima, NaN never chosen; 0 for no candidate), and
     // launch_argmax_keys reduces them.
     unsigned long long *arg_keys = nullptr;
+    // The row is row t of the table x points at, t the greedy token of the
+    // previous decode step: the largest of the n_in_keys keys in_keys (the
+    // previous step's arg_keys; argmax_key order, the index in the low
+    // word, 0 when every key is 0).  The kernel reduces the keys in its
+    // prologue, before it loads the row, and workgroup 0 stores t to
+    // tok_out (what launch_argmax_keys computes).
+    const unsigned long long *in_keys = nullptr;
+    int n_in_keys = 0;
+    uint32_t *tok_out = nullptr;
     // RoPE (ops/rope.rs) on output channels [0, rope_n): the pairs
     // (2i, 2i+1) of each head of hd channels rotate by the table entries
     // i % (hd/2) of rope_cos / rope_sin (one position's rows).
@@ -265,7 +274,8 @@ struct RowOps {
     int seg1 = INT_MAX, seg2 = INT_MAX;
     float *out1 = nullptr, *out2 = nullptr;
     bool any() const {
-        return norm_w || x_out || accum || up || arg_keys || rope_n > 0 || out1 || out2;
+        return norm_w || x_out || accum || up || arg_keys || in_keys || rope_n > 0 || out1 ||
+               out2;
     }
 };
 bool gemv_int8_supported(bool fused, size_t m, size_t n_tiles, size_t k, size_t kp);

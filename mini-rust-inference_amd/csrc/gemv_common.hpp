@@ -104,12 +104,50 @@ struct ActIn {
     const float *rope_cos = nullptr, *rope_sin = nullptr;
     int rope_n = 0, hd = 2, seg1 = INT_MAX, seg2 = INT_MAX;
     float *out1 = nullptr, *out2 = nullptr;
+    const unsigned long long *in_keys = nullptr;  // x is a table row picked by keys (RowOps)
+    int n_in_keys = 0;
+    uint32_t *tok_out = nullptr;
 
     ActIn(const float *x_, const int8_t *act_, int k, int8_t *aq, float *so, const RowOps &o)
         : x(x_), act(act_), K(k), act_q_out(aq), scale_out(so), norm_w(o.norm_w), eps(o.eps),
           x_out(o.x_out), up(o.up), arg_keys(o.arg_keys), accum(o.accum ? 1 : 0), rope_cos(o.rope_cos), rope_sin(o.rope_sin),
-          rope_n(o.rope_n), hd(o.hd), seg1(o.seg1), seg2(o.seg2), out1(o.out1), out2(o.out2) {}
+          rope_n(o.rope_n), hd(o.hd), seg1(o.seg1), seg2(o.seg2), out1(o.out1), out2(o.out2),
+          in_keys(o.in_keys), n_in_keys(o.n_in_keys), tok_out(o.tok_out) {}
 };
+
+// The fused row of a decode step whose token is still on the device as the
+// previous step's argmax keys (ActIn::in_keys): the workgroup reduces the
+// keys (each thread a strided share, then the wave, then the NW waves
+// through LDS), takes the index of the largest (0 when every key is 0, as
+// launch_argmax_keys does), stores it to tok_out from workgroup 0 and
+// returns that row of the table in.x.  Without keys, in.x itself.  Called
+// by every thread of the workgroup (it has a barrier).
+template <int NW>
+__device__ inline const float *row_of_keys(const ActIn &in) {
+    if (!in.in_keys) return in.x;
+    __shared__ unsigned long long s_key[NW];
+    const int t = threadIdx.x;
+    unsigned long long k = 0;
+#pragma unroll 4
+    for (int i = t; i < in.n_in_keys; i += NW * kWave) {
+        const unsigned long long v = in.in_keys[i];
+        k = v > k ? v : k;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const unsigned lo = __shfl_xor((unsigned)k, o), hi = __shfl_xor((unsigned)(k >> 32), o);
+        const unsigned long long ok = ((unsigned long long)hi << 32) | lo;
+        k = ok > k ? ok : k;
+    }
+    if ((t & 63) == 0) s_key[t >> 6] = k;
+    __syncthreads();
+    k = s_key[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) k = s_key[w] > k ? s_key[w] : k;
+    const uint32_t tok = k ? (uint32_t)k : 0u;
+    if (blockIdx.x == 0 && t == 0 && in.tok_out) *in.tok_out = tok;
+    return in.x + (size_t)tok * in.K;
+}
 
 // Epilogue of the row operations for output channel n of the row with value
 // v, where pv is the value of channel n ^ 1: RoPE below rope_n, as

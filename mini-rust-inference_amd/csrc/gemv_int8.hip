@@ -50,7 +50,9 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_int8(
 
     v4i xr[XR];
     const int n16 = FUSED ? in.K / 4 : M * kp / 16;
-    stage_load<NW, XR>(FUSED ? reinterpret_cast<const v4i *>(in.x)
+    const float *xrow = in.x;
+    if constexpr (FUSED && OPS) xrow = row_of_keys<NW>(in);  // the step's token row
+    stage_load<NW, XR>(FUSED ? reinterpret_cast<const v4i *>(xrow)
                              : reinterpret_cast<const v4i *>(in.act),
                        n16, xr);
     v4i wn[XR];  // RMS norm weights (row operations)
@@ -205,7 +207,9 @@ bool row_ops_ok(const float *x, const RowOps &o) {
                       o.seg1 <= o.seg2 && o.seg1 >= 0;
     const bool glu = !o.up || (al(o.up) && !o.norm_w && !o.x_out);
     const bool arg = !o.arg_keys || (reinterpret_cast<uintptr_t>(o.arg_keys) & 7) == 0;
-    return x && al(o.norm_w) && al(o.x_out) && glu && arg && rope && segs;
+    const bool keys = !o.in_keys || ((reinterpret_cast<uintptr_t>(o.in_keys) & 7) == 0 &&
+                                     o.n_in_keys > 0 && !o.up);
+    return x && al(o.norm_w) && al(o.x_out) && glu && arg && keys && rope && segs;
 }
 
 bool gemv_fusable(size_t m, size_t k, const float *x) {

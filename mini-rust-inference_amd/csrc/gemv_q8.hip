@@ -109,7 +109,9 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     v4i sr[RL];
     v4i xr[XR];
     const int n16 = FUSED ? in.K / 4 : M * kp / 16;
-    stage_load<NW, XR>(FUSED ? reinterpret_cast<const v4i *>(in.x)
+    const float *xrow = in.x;
+    if constexpr (FUSED && OPS) xrow = row_of_keys<NW>(in);  // the step's token row
+    stage_load<NW, XR>(FUSED ? reinterpret_cast<const v4i *>(xrow)
                              : reinterpret_cast<const v4i *>(in.act),
                        n16, xr);
     v4i wn[XR];  // RMS norm weights (row operations)

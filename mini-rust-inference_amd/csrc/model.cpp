@@ -64,6 +64,12 @@ struct mri_llama {
     int qform = -1;
     size_t qld = 0;
     int row_path = -1;            // decode rows take the folded path (-1: not yet known)
+    // A decode row whose token is still the previous step's argmax keys: the
+    // block's first projection reduces them, reads that embedding row and
+    // copies it into x (RowOps in_keys); set by run_rows for one block call.
+    const unsigned long long *in_keys = nullptr;
+    int n_in_keys = 0;
+    uint32_t *tok_out = nullptr;
     std::vector<void *> allocs;
 };
 
@@ -333,18 +339,31 @@ mri_status block(mri_llama *m, size_t li, size_t rows, size_t start, mri_kv_cach
     // xrow, the attention input and then the residual stream)
     const float *xrow = x_in;
     bool copy_x = fold && x_in != m->x;
+    // the first projection of the block copies the row it reads into x (and,
+    // with in_keys, first finds it from the previous step's argmax keys);
+    // the later ones read x
     auto norm_ops = [&](const float *norm) {
         RowOps o;
         o.norm_w = norm;
         o.eps = g.eps;
-        if (copy_x) o.x_out = m->x;
+        if (copy_x) {
+            o.x_out = m->x;
+            o.in_keys = m->in_keys;
+            o.n_in_keys = m->n_in_keys;
+            o.tok_out = m->tok_out;
+            m->in_keys = nullptr;
+            m->tok_out = nullptr;
+        }
         copy_x = false;
         return o;
     };
     auto in_proj = [&](const mri_weight_ref &w, const float *norm, float *out) {
         if (!fold) return m->fuse_norm ? proj_normed(m, w, rows, out, s)
                                        : proj(w, m->normed, rows, out, s);
-        return row_proj(w, xrow, norm_ops(norm), out, s);
+        const RowOps o = norm_ops(norm);
+        const float *src = xrow;
+        if (o.in_keys) xrow = m->x;
+        return row_proj(w, src, o, out, s);
     };
     // projections whose output is added to the residual stream
     // (up: in is a SwiGLU gate row, applied in the projection; one row only)
@@ -391,8 +410,11 @@ mri_status block(mri_llama *m, size_t li, size_t rows, size_t start, mri_kv_cach
         } else {
             RowOps ok = o, ov = o;
             ok.x_out = ov.x_out = nullptr;  // copied by the first
+            ok.in_keys = ov.in_keys = nullptr;
+            ok.tok_out = ov.tok_out = nullptr;
             o.rope_n = (int)m->qd;
             TRY(row_proj(L.w[0], xrow, o, q, s));
+            if (o.in_keys) xrow = m->x;  // the row the first found and copied
             ok.rope_n = (int)m->kvd;
             TRY(row_proj(L.w[1], xrow, ok, krow, s));
             ov.rope_n = 0;
@@ -443,8 +465,10 @@ mri_status block(mri_llama *m, size_t li, size_t rows, size_t start, mri_kv_cach
 // already on the device.
 // Where a single folded row's embedding comes from: gathered from the ids
 // on the device (kDevice), read in place at an id the host knows (kHost),
-// or already in m->x (kInX, written by the previous step's argmax).
-enum class Emb { kDevice, kHost, kInX };
+// already in m->x (kInX, written by the previous step's argmax), or read in
+// place at the id the first projection finds in the previous step's argmax
+// keys (kKeys: m->in_keys, which the caller sets; needs a layer).
+enum class Emb { kDevice, kHost, kInX, kKeys };
 
 // arg: for a folded row, the greedy argmax (and next embedding row) that the
 // output projection's epilogue computes (the RowOps arg_* fields).
@@ -456,6 +480,7 @@ mri_status run_rows(mri_llama *m, const uint32_t *tok_dev, size_t rows, size_t s
     const float *first = g.n_layers ? m->layers[0].attn_norm : m->out_norm;
     const float *x_in = m->x;
     if (fold && emb == Emb::kHost) x_in = m->embd + (size_t)host_tok * g.dim;
+    else if (fold && emb == Emb::kKeys && g.n_layers) x_in = m->embd;  // row found in-kernel
     else if (fold && emb == Emb::kInX) {}
     else if (fold) TRY(launch_embed(m->embd, tok_dev, 1, g.dim, m->x, s));
     else if (m->fuse_norm) {
@@ -706,15 +731,31 @@ mri_status mri_llama_generate_greedy(mri_llama *m, const uint32_t *prompt, size_
     const size_t n_keys = (V + kTileN - 1) / kTileN;
     if (fold && n_steps) TRY(argmax_ws_get(s, &aws, kArgmaxWsBytes + n_keys * 8));
     auto *keys = reinterpret_cast<unsigned long long *>(static_cast<char *>(aws) + kArgmaxWsBytes);
+    // With a layer, step i > 0 takes its token from step i - 1's keys in its
+    // first projection's prologue (which also stores it to gen[i]); the last
+    // step's keys are reduced by launch_argmax_keys.  Without layers a
+    // separate reduction gathers each next embedding row.
+    const bool keys_in = fold && m->cfg.n_layers > 0;
     for (size_t i = 0; i < n_steps; ++i) {
         float *lg = logits_out ? logits_out + (i + 1) * V : m->logits_buf;
         if (fold) {
             RowOps arg;
             arg.arg_keys = keys;
-            TRY(run_rows(m, m->gen + i, 1, n_prompt + i, c, lg, s, Emb::kInX, 0, &arg));
+            Emb emb = Emb::kInX;
+            if (keys_in && i > 0) {
+                m->in_keys = keys;
+                m->n_in_keys = (int)n_keys;
+                m->tok_out = m->gen + i;
+                emb = Emb::kKeys;
+            }
+            const mri_status st = run_rows(m, m->gen + i, 1, n_prompt + i, c, lg, s, emb, 0, &arg);
+            m->in_keys = nullptr;
+            m->tok_out = nullptr;
+            TRY(st);
             const bool next = i + 1 < n_steps;
-            TRY(launch_argmax_keys(keys, n_keys, m->gen + i + 1, next ? m->embd : nullptr,
-                                   m->cfg.dim, m->x, s));
+            if (!keys_in || !next)
+                TRY(launch_argmax_keys(keys, n_keys, m->gen + i + 1, next ? m->embd : nullptr,
+                                       m->cfg.dim, m->x, s));
         } else {
             TRY(run_rows(m, m->gen + i, 1, n_prompt + i, c, lg, s, Emb::kInX));
             TRY(pick(lg, m->gen + i + 1, i + 1 < n_steps));
