@@ -372,31 +372,42 @@ __global__ __launch_bounds__(256) void k_attention(
 // acquire count at device scope writes back and invalidates the XCD's L2 in
 // every workgroup: 14.4 against 10.5 us a call at 512-575 keys.)
 // cnt: one word per head, zero between calls.
+__device__ inline float attn_part_load(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Output element d of a head from its nch chunk partials at ph: m = max_c m_c,
+// then l = sum_c l_c exp(m_c - m) and o = sum_c o_c[d] exp(m_c - m) in chunk
+// order, out[d] = o / l.  The first 16 chunks' (m_c, l_c, o_c[d]) are loaded
+// together, before the first use, so the combine costs one memory round trip
+// up to 16 chunks (1024 keys).
 template <int HD>
-__device__ inline void attn_combine(const float *ph, int nch, int d, float *s_m, float *s_l,
-                                    float *out) {
-    for (int c = d; c < nch; c += HD) {
-        s_m[c] = __hip_atomic_load(ph + c * (HD + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_l[c] = __hip_atomic_load(ph + c * (HD + 2) + 1, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
+__device__ inline void attn_combine(const float *ph, int nch, int d, float *out) {
     if (d >= HD) return;
+    constexpr int B = 16;
+    float mv[B], lv[B], ov[B];
+    auto batch = [&](int c0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+            const float *pc = ph + (size_t)min(c0 + u, nch - 1) * (HD + 2);
+            mv[u] = attn_part_load(pc);
+            lv[u] = attn_part_load(pc + 1);
+            ov[u] = attn_part_load(pc + 2 + d);
+        }
+    };
+    batch(0);
     float m = -INFINITY;
-    for (int c = 0; c < nch; ++c) m = fmaxf(m, s_m[c]);
+#pragma unroll
+    for (int u = 0; u < B; ++u)
+        if (u < nch) m = fmaxf(m, mv[u]);
+    for (int c = B; c < nch; ++c) m = fmaxf(m, attn_part_load(ph + (size_t)c * (HD + 2)));
     float l = 0.0f, o = 0.0f;
-    for (int c0 = 0; c0 < nch; c0 += 16) {
-        float ov[16];
+    for (int c0 = 0; c0 < nch; c0 += B) {
+        if (c0 > 0) batch(c0);
 #pragma unroll
-        for (int u = 0; u < 16; ++u)
-            ov[u] = c0 + u < nch ? __hip_atomic_load(ph + (c0 + u) * (HD + 2) + 2 + d,
-                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                 : 0.0f;
-#pragma unroll
-        for (int u = 0; u < 16; ++u) {
+        for (int u = 0; u < B; ++u) {
             if (c0 + u < nch) {
-                const float f = expf(s_m[c0 + u] - m);
-                l = l + s_l[c0 + u] * f;
+                const float f = expf(mv[u] - m);
+                l = l + lv[u] * f;
                 o = o + ov[u] * f;
             }
         }
@@ -415,7 +426,6 @@ __global__ __launch_bounds__(256) void k_attn_decode_part(
     __shared__ float s_s[4][64];
     __shared__ float s_w[64];
     __shared__ float s_o[4][HD];
-    __shared__ float s_m[1024], s_l[1024];
     __shared__ int s_last;
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     const int c = blockIdx.x, h = blockIdx.y, kh = h / groups, nch = gridDim.x;
@@ -492,7 +502,7 @@ __global__ __launch_bounds__(256) void k_attn_decode_part(
                  nch - 1;
     __syncthreads();
     if (!s_last) return;
-    attn_combine<HD>(part + (size_t)h * nch * (HD + 2), nch, t, s_m, s_l, out + (size_t)h * HD);
+    attn_combine<HD>(part + (size_t)h * nch * (HD + 2), nch, t, out + (size_t)h * HD);
     if (t == 0) __hip_atomic_store(&cnt[h], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
