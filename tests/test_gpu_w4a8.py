@@ -63,6 +63,33 @@ def test_w4a8_parity(m, n, k, order):
     assert_bits_equal(host(out2), host(out), "w4a8 out (no debug outputs)")
 
 
+@pytest.mark.parametrize("m,n,k", [(1, 11008, 4096), (1, 50, 96), (3, 48, 1024),
+                                   (4, 64, 4096), (9, 24, 1024), (40, 272, 4096),
+                                   (256, 8192, 256)])
+def test_w4a8_equals_q8_0_on_expanded_blocks(m, n, k):
+    """W4A8 runs the Q8_0 kernels with a 4-bit B operand, so its outputs
+    equal matmul_q8_0_direct's on the same blocks expanded to Q8_0 (quants
+    nibble - 8, the same f16 scale bits) bit for bit, at every row count:
+    the GEMV's wave order at 1-4 rows included.  From 256 rows at N >= 8192
+    the Q8_0 entry point takes the LDS-tiled GEMM, which W4A8 does not; there
+    the comparison is with the block-ordered entry point (the skinny kernel
+    both run)."""
+    say(f"w4a8 vs q8_0 on expanded blocks m={m} n={n} k={k}")
+    t = torch()
+    rng = np.random.default_rng(m * 5 + n + k)
+    raw = synth_q4_0(rng, n, k)
+    x = rng.standard_normal((m, k)).astype(F32)
+    w4 = mri().Q4Matrix.from_raw_bytes(raw, n, k, 0)
+    w8 = mri().Q8Matrix.from_raw_bytes(CF.q4_0_to_q8_0(raw, n, k), n, k)
+    o4, o8 = empty((m, n), t.float32), empty((m, n), t.float32)
+    mri().matmul_q4_0_w4a8(dev(x), w4, o4)
+    if m >= 256 and n >= 8192:
+        mri().matmul_q8_0_direct_exact(dev(x), w8, o8)
+    else:
+        mri().matmul_q8_0_direct(dev(x), w8, o8)
+    assert_bits_equal(host(o4), host(o8), "w4a8 vs q8_0 on the expanded blocks")
+
+
 def test_w4a8_ggml_file_order_matches_reference_order():
     """The same weights uploaded from GGML-order bytes and from
     interleaved-order bytes give the same outputs."""
