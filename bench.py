@@ -541,7 +541,7 @@ def main():
         secondary["q8_0_skinny_4096x11008"] = skinny
 
         # prefill-sized Q8_0 products of the 7B layer (M = 512): the LDS-tiled
-        # kernel from N = 8192 up, the skinny kernel below
+        # kernel (from 128 rows once M * N > 2^20: all four shapes here)
         q8pre = {}
         for (kk, nn) in [(4096, 12288), (4096, 22016), (4096, 4096), (11008, 4096)]:
             ms2, _, _, _, _ = bench_q8(torch, M, T, 512, nn, kk, max(5, steps2 // 20),
@@ -549,7 +549,7 @@ def main():
             tops = 2 * 512 * nn * kk / (ms2 * 1e-3) / 1e12
             q8pre[f"512x{kk}x{nn}"] = {
                 "us": round(ms2 * 1e3, 1), "TOPS": round(tops, 1),
-                "kernel": "k_gemm_q8_0" if nn >= 8192 else "k_skinny_q8_0"}
+                "kernel": "k_gemm_q8_0" if 512 * nn > (1 << 20) else "k_skinny_q8_0"}
             log(f"q8_0 prefill M=512 {kk}->{nn}: {ms2*1e3:.1f} us {tops:.0f} TOPS")
         secondary["q8_0_prefill_m512"] = q8pre
 

@@ -23,15 +23,15 @@
  *  - Q8_0 f32 outputs (matmul_q8_0_direct, its _noalloc variant) are the
  *    block terms t_b = ((f32)dot_b * s_a) * d_b added in the reference's
  *    left-to-right block order, bit-exact, for 5 <= m, except when
- *    m >= 256, n >= 8192 and no block_dots_out is requested.  For m <= 4
+ *    m >= 128, m * n > 2^20 and no block_dots_out is requested.  For m <= 4
  *    (the decode GEMV adds per-wave partial sums) and in that prefill range
  *    (an FMA fold, s_a applied once per output) they are within
  *    1e-5 * max(|ref|, sum_b |t_b|) of the reference.
  *    mri_matmul_q8_0_direct_exact keeps the block order at every m.
  *  - W4A8 (extension) f32 outputs equal, bit for bit, those of
  *    mri_matmul_q8_0_direct on the expanded blocks (quant = nibble - 8,
- *    the same scale bits); for m >= 256 and n >= 8192 they equal those of
- *    mri_matmul_q8_0_direct_exact instead.  Against the reference's order
+ *    the same scale bits); for m >= 128 and m * n > 2^20 they equal those
+ *    of mri_matmul_q8_0_direct_exact instead.  Against the reference's order
  *    that is bit-exact for 5 <= m and within the Q8_0 bound for m <= 4.
  *  - Q4_0 W4A32 (matmul_q4_0_dequant and its handle form) sums in another
  *    order than the reference and is within 1e-5 * max(|ref|, sum|x_k w_k|).
@@ -172,8 +172,8 @@ mri_status mri_matmul_int8_from_f32(const float *input, const size_t *dims,
  * activation scales and block dots are bit-exact; out is bit-exact for
  * 5 <= m outside the prefill range below, and otherwise within
  * 1e-5 * max(|ref|, sum_b |t_b|): at m <= 4 (the decode GEMV splits K over
- * waves and adds their partial sums) and at m >= 256, n_out >= 8192 without
- * block_dots_out (the LDS-tiled GEMM folds fma((f32)dot, d, acc) and
+ * waves and adds their partial sums) and at m >= 128, m * n_out > 2^20
+ * without block_dots_out (the LDS-tiled GEMM folds fma((f32)dot, d, acc) and
  * multiplies by s_a once).
  * InvalidShape unless ndim == 2; ShapeMismatch when dims[1] != k_in.
  * Optional outputs (nullable, device): block_dots_out [m, n_out, k_in/32]

@@ -9,8 +9,8 @@
 // per (row, channel, block), against one MFMA per 16 x 16 x 32 block.  The
 // reference rounds ((f32)dot * s_a) * d per block and adds in block order
 // (two multiplies and an add); here each term is one fused multiply-add
-// onto the running sum (a convert and an FMA) and s_a multiplies once at the
-// end.  The int32 block dots are exact; the f32 result differs from the
+// onto the running sum (the dot's f32 value and an FMA) and s_a multiplies
+// once at the end.  The int32 block dots are exact; the f32 result differs from the
 // reference's only by those roundings, within 1e-5 * max(|out|, sum |t_b|)
 // of it.  Half the VALU work of the reference's order is what makes this
 // kernel twice as fast as keeping that order would be.
@@ -22,14 +22,15 @@
 //     v_mfma_i32_16x16x32_i8 for both blocks of the chunk;
 //   * weights: lap blocks of 16 channels x 256 k (4 chunks of 1 KiB in the
 //     same permutation, then 16 rows x 8 f16 scales), tile-major.
-// A workgroup computes 128 rows x 128 channels (4 x 4 sub-tiles of 32 x 32);
-// each K step is one lap (8 blocks): per lap it stages 32 KiB of activation
-// fragments, 32 KiB of weight chunks and 2 KiB of scales in LDS by
-// global_load_lds (16 bytes per lane, each lane its own address, so a
-// fragment of 16 rows x 64 bytes is gathered straight from the row-major
-// activations), double-buffered: the loads of lap q + 1 fly while lap q is
-// folded.  Eight waves (2 x 4) each own 64 rows x 32 channels, two waves per
-// SIMD, so that the MFMA results, sums and operands all stay in VGPRs.
+// A workgroup computes BM rows x BN channels (128 x 64: 4 x 2 sub-tiles of
+// 32 x 32); each ring stage is half a lap (4 blocks): per stage it stages
+// BM x 128 bytes of activation fragments, BN x 128 bytes of weight chunks
+// and the lap's scales in LDS by global_load_lds (16 bytes per lane, each
+// lane its own address, so a fragment of 16 rows x 64 bytes is gathered
+// straight from the row-major activations), NS stages deep: the loads of
+// the next stages fly while one is folded.  Each of the 8 waves (4 x 2) owns
+// 32 rows x 32 channels; two workgroups share a CU, four waves per SIMD, and
+// the MFMA results, sums and operands all stay in VGPRs.
 //
 // Per block, v_mfma_i32_32x32x32_i8 gives the exact dots of 32 rows x 32
 // channels; its output register e of lane l holds row 8 * (e / 4) +
@@ -48,6 +49,8 @@ namespace {
 typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr int kQWave = 64;
+constexpr int kDotBias = 0x4B400000;      // the bits of 1.5 * 2^23
+constexpr float kDotBiasF = 12582912.0f;  // 1.5 * 2^23
 constexpr int kQXcds = 8;
 template <typename F, int... I>
 __device__ inline void q_static_for_impl(F &&f, std::integer_sequence<int, I...>) {
@@ -111,11 +114,19 @@ __device__ inline void q8_wait_lds(v4i (&a)[2][RG][2], v4i (&b)[2][TT][2]) {
     }
 }
 
+// Scale fragments of a stage: one per 16-channel weight tile, at least one
+// per wave (every wave issues the same loads; waves past the tile count
+// reload the last tile's scales into a slot nothing reads).
+template <int BN, int NW>
+constexpr int q8_scale_slots() {
+    return BN / 16 > NW ? BN / 16 : NW;
+}
+
 // Bytes of one ring stage (half a lap: 2 chunks, 4 blocks) of a BM x BN tile:
 // activation fragments, weight chunks, and the lap's weight scales.
-template <int BM, int BN>
+template <int BM, int BN, int NW>
 constexpr int q8_stage_bytes() {
-    return BM * 128 + BN * 128 + BN * 16;
+    return BM * 128 + BN * 128 + q8_scale_slots<BN, NW>() * 256;
 }
 
 template <int BM, int BN, int WM, int WN, int NS>
@@ -125,14 +136,14 @@ __global__ __launch_bounds__(WM * WN * kQWave) void k_gemm_q8_0(
     float *__restrict__ out) {
     constexpr int NW = WM * WN;
     constexpr int RG = BM / 32 / WM, TT = BN / 32 / WN;  // 32 x 32 sub-tiles per wave
-    constexpr int FA = BM / 8, FB = BN / 8, FS = BN / 16;  // loads of a stage
+    constexpr int FA = BM / 8, FB = BN / 8, FS = q8_scale_slots<BN, NW>();  // loads of a stage
     constexpr int LA = FA / NW, LB = FB / NW, LS = FS / NW;  // ... per wave
     static_assert(RG >= 1 && TT >= 1 && FA % NW == 0 && FB % NW == 0 && FS % NW == 0,
                   "wave split");
     static_assert(NS >= 2, "ring depth");
     constexpr int L = LA + LB + LS;  // loads per wave and stage, the same for every wave
     constexpr int SA = BM * 128, SB = BN * 128;
-    constexpr int STAGE = q8_stage_bytes<BM, BN>();
+    constexpr int STAGE = q8_stage_bytes<BM, BN, NW>();
     extern __shared__ v4i s_buf[];
 
     // XCD-aware tile index: workgroups go to the 8 XCDs round-robin; the M
@@ -152,7 +163,8 @@ __global__ __launch_bounds__(WM * WN * kQWave) void k_gemm_q8_0(
     // region: 16-row group f / 2, chunk f % 2 of the half lap; rows past M
     // read row M - 1 (their outputs are not stored).  Fragment f of the B
     // region: weight tile f / 2, chunk f % 2; tiles past the end read the
-    // last.  Scales: tile wv + NW * j, 4 bytes per lane (its 256 bytes).
+    // last.  Scales: tile wv + NW * j (waves past the tile count: the last
+    // tile, into a slot nothing reads), 4 bytes per lane (its 256 bytes).
     // Step s adds 128 s bytes to an activation source, and lap s / 2 (plus
     // 2 KiB for the second half) to a weight source.
     const int8_t *a_src[LA];
@@ -173,7 +185,7 @@ __global__ __launch_bounds__(WM * WN * kQWave) void k_gemm_q8_0(
     }
 #pragma unroll
     for (int j = 0; j < LS; ++j) {
-        const int T = min(BN / 16 * nt + wv + NW * j, n_tiles - 1);
+        const int T = min(BN / 16 * nt + min(wv + NW * j, BN / 16 - 1), n_tiles - 1);
         s_src[j] = laps + (size_t)T * G * lap_bytes + 4096 + 4 * l;
     }
     // loads of step s (clamped to the last: the loads past the end re-read
@@ -209,7 +221,14 @@ __global__ __launch_bounds__(WM * WN * kQWave) void k_gemm_q8_0(
         for (int j = 0; j < TT; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) fs[i][j][e] = 0.0f;
-    const v16i zero = {};
+    // Each block's MFMAs start from the bits of 1.5 * 2^23 rather than from
+    // zero, so that an output register, read as f32, is 12582912 + dot
+    // exactly (|dot| <= 32 * 128 * 127 < 2^22 keeps it in [2^23, 2^24),
+    // where the f32 spacing is 1): one full-rate subtract then gives
+    // (f32)dot, where v_cvt_f32_i32 issues at half rate.
+    v16i bias;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) bias[e] = kDotBias;
 
 #pragma unroll
     for (int s = 0; s < NS - 1; ++s) issue(s);
@@ -260,7 +279,7 @@ __global__ __launch_bounds__(WM * WN * kQWave) void k_gemm_q8_0(
 #pragma unroll
                 for (int j = 0; j < TT; ++j)
                     d[k % 2][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[c][i][h], b[c][j][h],
-                                                                         zero, 0, 0, 0);
+                                                                         bias, 0, 0, 0);
         };
         auto fold = [&](auto kk) __attribute__((always_inline)) {
             constexpr int k = decltype(kk)::value, c = k / 2, h = k % 2;
@@ -275,8 +294,11 @@ __global__ __launch_bounds__(WM * WN * kQWave) void k_gemm_q8_0(
 #pragma unroll
                 for (int i = 0; i < RG; ++i)
 #pragma unroll
-                    for (int e = 0; e < 16; ++e)
-                        fs[i][j][e] = __builtin_fmaf((float)d[k % 2][i][j][e], ds, fs[i][j][e]);
+                    for (int e = 0; e < 16; ++e) {
+                        const int biased = d[k % 2][i][j][e];
+                        fs[i][j][e] = __builtin_fmaf(__int_as_float(biased) - kDotBiasF, ds,
+                                                     fs[i][j][e]);
+                    }
             }
         };
         dots(std::integral_constant<int, 0>{});
@@ -313,7 +335,7 @@ __global__ __launch_bounds__(WM * WN * kQWave) void k_gemm_q8_0(
 template <int BM, int BN, int WM, int WN, int NS>
 mri_status launch_q8_inst(const int8_t *act, size_t m, const float *sa_rows,
                           const Q8MatrixDev &w, float *out, hipStream_t s) {
-    constexpr size_t lds = (size_t)NS * q8_stage_bytes<BM, BN>();
+    constexpr size_t lds = (size_t)NS * q8_stage_bytes<BM, BN, WM * WN>();
     static DeviceOnce attr;
     MRI_HIP(attr.run([&](int) {
         return hipFuncSetAttribute(
@@ -335,28 +357,32 @@ mri_status launch_q8_inst(const int8_t *act, size_t m, const float *sa_rows,
 }  // namespace
 
 // Where this kernel is used instead of the skinny kernel (which keeps the
-// reference's per-block rounding bit for bit).  Both are bound by the f32
-// fold; this one stages operand tiles in LDS and halves the fold's VALU
-// work.  Measured on MI355X at K = 4096: 125 vs 155 us at M = 512,
-// N = 12288, 184 vs 258 us at N = 22016; at M <= 128, or N = 4096 (M = 512,
-// K = 4096 or 11008), the two are within 5 % of each other, and the skinny
-// kernel is kept.
+// reference's per-block rounding bit for bit): from 128 rows once the
+// product has more than 2^20 outputs.  The skinny kernel's waves then no
+// longer fit one pass of the SIMDs, while this kernel's time has a floor of
+// its K loop's latency (about 39 us at K = 4096).  Measured at K = 4096
+// (us, skinny / this kernel): 64 x 4096 31.0 / 38.7, 128 x 4096 33.0 /
+// 39.5, 256 x 4096 35.6 / 41.0, 512 x 2048 36.7 / 42.5 (all 2^20 outputs or
+// fewer); 128 x 11008 58.5 / 42.2, 256 x 11008 57.5 / 57.7, 512 x 4096
+// 61.5 / 45.0, 512 x 12288 155 / 101.7, 512 x 22016 258 / 171; at
+// K = 11008, 512 x 4096 148.7 / 108 and 256 x 4096 80 / 112.
 bool gemm_q8_supported(size_t m, const Q8MatrixDev &w) {
-    return !w.w4 && m >= 256 && w.n_out >= 8192 && m * w.kp < (1ull << 31) &&
+    return !w.w4 && m >= 128 && m * w.n_out > (1ull << 20) && m * w.kp < (1ull << 31) &&
            m * w.n_out < (1ull << 31);
 }
 
 // act: quantized rows [m][w.kp], chunk-permuted (launch_quantize_rows with
 // the Q8_0 layout); sa_rows: their scales.
-// Tiles of 128 rows: 128 channels and 8 waves of 64 x 32 from 16384
-// channels up (184 vs 197 us at M = 512, N = 22016), else 64 channels and 4
-// waves of 64 x 32 (about 77 KiB of LDS: two workgroups per CU), which keeps
-// the fold balanced over the CUs when the wide tiles would come in 1.5
-// passes (768 workgroups against 384 at N = 12288).
+// Tiles of 128 rows x 64 channels, 8 waves of 32 x 32 (about 78 KiB of LDS:
+// two workgroups per CU, four waves per SIMD).  With the MFMA results in
+// VGPRs (see the build flags) 128 x 64 tiles beat 128 x 128 tiles of 8
+// waves at every N measured (M = 512, K = 4096: 164.5 against 176.4 us at
+// N = 22016, 223.5 against 234 at N = 32000); 8 waves of 32 x 32 rather
+// than 4 of 64 x 32 halve each wave's serial fold per step and took the
+// latency floor from 43 to 39 us (512 x 11008 -> 4096: 108 against 117).
 mri_status launch_gemm_q8_0(const int8_t *act, size_t m, const float *sa_rows,
                             const Q8MatrixDev &w, float *out, hipStream_t s) {
-    if (w.n_out >= 16384) return launch_q8_inst<128, 128, 2, 4, 4>(act, m, sa_rows, w, out, s);
-    return launch_q8_inst<128, 64, 2, 2, 3>(act, m, sa_rows, w, out, s);
+    return launch_q8_inst<128, 64, 4, 2, 3>(act, m, sa_rows, w, out, s);
 }
 
 }  // namespace mri

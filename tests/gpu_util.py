@@ -81,6 +81,13 @@ def q8_terms_abs_sum(bd, sa, d):
     return np.einsum("mnb,nb->mn", bd, d) * sa[:, None]
 
 
+def q8_gemm_range(m, n):
+    """Shapes at which matmul_q8_0_direct without block dots runs the
+    LDS-tiled prefill GEMM (an FMA fold, s_a applied once: within the
+    contract, not in the reference's order): m >= 128 and m * n > 2^20."""
+    return m >= 128 and m * n > (1 << 20)
+
+
 def assert_q8_close(got, exp, terms_abs, what="", rel=1e-5):
     """The Q8_0 f32 contract: |got - exp| <= rel * max(|exp|, sum_b |t_b|)
     per element (the block terms may be added in another order than the

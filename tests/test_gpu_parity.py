@@ -4,7 +4,7 @@ Integer results (quantized activations, int32 accumulators, block dots) and
 the per-channel INT8 f32 outputs must be bit-identical.  Q8_0 f32 outputs
 are within 1e-5 * max(|ref|, sum_b |t_b|) of the reference's left-to-right
 block sum where the kernel reorders it (the decode GEMV, M <= 4, adds
-per-wave partial sums; the LDS-tiled prefill GEMM, M >= 256 and N >= 8192
+per-wave partial sums; the LDS-tiled prefill GEMM, M >= 128 and M * N > 2^20
 without block dots, folds with FMAs) and bit-identical elsewhere (the
 skinny kernel, and the block-ordered entry point at every M).
 Q4_0 (W4A32) outputs are within 1e-5 * max(|ref|, sum_k |x_k w_k|).
@@ -16,7 +16,7 @@ import pytest
 
 import closed_form as CF
 import oracle_lib as O
-from gpu_util import (F32, assert_bits_equal, assert_q8_close, bits, dev, empty, host,
+from gpu_util import (q8_gemm_range, F32, assert_bits_equal, assert_q8_close, bits, dev, empty, host,
                       q8_oracle_sliced, q8_terms_abs_sum, synth_int8_weights, synth_q4_0,
                       synth_q8_0, torch)
 
@@ -319,10 +319,12 @@ Q8_SHAPES = [
     # 1 lap at 688 tiles, 4 x 2 below 512 tiles, 8 x 2 at K = 8192
     (2, 11008, 4096), (4, 4096, 4096), (2, 4096, 8192),
     # prefill sizes: partial row and channel tiles, K with padding blocks in its last lap
-    # (992), many laps (11008); from 256 rows and 8192 channels the LDS-tiled kernel,
-    # with 64-channel (8192, 8200) and 128-channel (16400) tiles
+    # (992), many laps (11008); from 128 rows and more than 2^20 outputs the LDS-tiled
+    # kernel (partial 128-row and 64-channel tiles), at 2^20 outputs the skinny kernel
     (128, 1000, 4096), (130, 520, 992), (200, 264, 11008), (64, 2048, 2048),
     (256, 8192, 256), (300, 8200, 512), (260, 16400, 256), (257, 8192, 992),
+    (128, 8200, 512), (129, 8200, 256), (128, 8192, 256), (512, 2048, 256), (512, 2056, 256),
+    (300, 4100, 1024),
 ]
 
 
@@ -333,7 +335,7 @@ def q8_check(got, out0, bd0, sa0, raw, n, k, what, exact=None):
     d, _ = CF.q8_0_split(raw, n, k)
     assert_q8_close(got, out0, q8_terms_abs_sum(bd0, sa0, d), what)
     if exact is None:
-        exact = got.shape[0] > 4 and not (got.shape[0] >= 256 and n >= 8192)
+        exact = got.shape[0] > 4 and not q8_gemm_range(got.shape[0], n)
     if exact:
         assert_bits_equal(got, out0, what)
 
@@ -358,17 +360,18 @@ def test_matmul_q8_0_direct_parity(m, n, k):
     sa2 = empty(m, t.float32)
     mri().matmul_q8_0_direct(dev(x), w, out2, act_scales_out=sa2)
     assert np.array_equal(bits(host(sa2)), bits(sa0))
-    if m >= 256 and n >= 8192:   # the LDS-tiled kernel: fused fold, within the contract
+    if q8_gemm_range(m, n):   # the LDS-tiled kernel: fused fold, within the contract
         q8_check(host(out2), out0, bd0, sa0, raw, n, k, "q8_0 out (prefill kernel)")
     else:
         assert_bits_equal(host(out2), host(out), "q8_0 out (no debug outputs)")
 
 
-@pytest.mark.parametrize("m,n,k", [(512, 12288, 4096), (512, 22016, 4096), (512, 32000, 4096)])
+@pytest.mark.parametrize("m,n,k", [(512, 12288, 4096), (512, 22016, 4096), (512, 32000, 4096),
+                                   (512, 4096, 4096), (512, 4096, 11008)])
 def test_q8_0_prefill_gemm_full_shapes(m, n, k):
-    """The LDS-tiled Q8_0 GEMM (m >= 256, n >= 8192, no block dots) at the
-    shapes the decoder layer's prefill runs it at (fused q/k/v, fused
-    gate/up, lm_head; K = 4096): every output within the contract of the
+    """The LDS-tiled Q8_0 GEMM (m >= 128, m * n > 2^20, no block dots) at
+    the shapes the decoder layer's prefill runs it at (fused q/k/v, fused
+    gate/up, lm_head, o and down at 512 rows): every output within the contract of the
     oracle's sequential block sum (q8_direct.rs:229-289), and the activation
     scales bit-exact."""
     say(f"matmul_q8_0_direct prefill gemm m={m} n={n} k={k}")
@@ -388,11 +391,11 @@ def test_q8_0_prefill_gemm_full_shapes(m, n, k):
 
 @pytest.mark.parametrize("m,n,k", [(1, 11008, 4096), (2, 300, 256), (4, 4096, 4096),
                                    (3, 64, 11008), (8, 48, 512), (256, 8192, 256),
-                                   (300, 8200, 512)])
+                                   (300, 8200, 512), (128, 8200, 512), (512, 4096, 1024)])
 def test_matmul_q8_0_direct_exact(m, n, k):
     """mri_matmul_q8_0_direct_exact keeps the reference's block order at
     every row count: bit-identical to the oracle where the default entry
-    point reorders (m <= 4, and m >= 256 with n >= 8192), with and without
+    point reorders (m <= 4, and m >= 128 with m * n > 2^20), with and without
     block dots."""
     say(f"matmul_q8_0_direct_exact m={m} n={n} k={k}")
     t = torch()

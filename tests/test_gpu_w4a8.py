@@ -12,7 +12,7 @@ import pytest
 
 import closed_form as CF
 import oracle_lib as O
-from gpu_util import (F32, assert_bits_equal, assert_q8_close, bits, dev, empty, host,
+from gpu_util import (q8_gemm_range, F32, assert_bits_equal, assert_q8_close, bits, dev, empty, host,
                       q8_terms_abs_sum, synth_q4_0, torch)
 
 pytestmark = pytest.mark.gpu
@@ -70,10 +70,10 @@ def test_w4a8_equals_q8_0_on_expanded_blocks(m, n, k):
     """W4A8 runs the Q8_0 kernels with a 4-bit B operand, so its outputs
     equal matmul_q8_0_direct's on the same blocks expanded to Q8_0 (quants
     nibble - 8, the same f16 scale bits) bit for bit, at every row count:
-    the GEMV's wave order at 1-4 rows included.  From 256 rows at N >= 8192
-    the Q8_0 entry point takes the LDS-tiled GEMM, which W4A8 does not; there
-    the comparison is with the block-ordered entry point (the skinny kernel
-    both run)."""
+    the GEMV's wave order at 1-4 rows included.  From 128 rows and more than
+    2^20 outputs the Q8_0 entry point takes the LDS-tiled GEMM, which W4A8
+    does not; there the comparison is with the block-ordered entry point
+    (the skinny kernel both run)."""
     say(f"w4a8 vs q8_0 on expanded blocks m={m} n={n} k={k}")
     t = torch()
     rng = np.random.default_rng(m * 5 + n + k)
@@ -83,7 +83,7 @@ def test_w4a8_equals_q8_0_on_expanded_blocks(m, n, k):
     w8 = mri().Q8Matrix.from_raw_bytes(CF.q4_0_to_q8_0(raw, n, k), n, k)
     o4, o8 = empty((m, n), t.float32), empty((m, n), t.float32)
     mri().matmul_q4_0_w4a8(dev(x), w4, o4)
-    if m >= 256 and n >= 8192:
+    if q8_gemm_range(m, n):
         mri().matmul_q8_0_direct_exact(dev(x), w8, o8)
     else:
         mri().matmul_q8_0_direct(dev(x), w8, o8)

@@ -9,7 +9,7 @@ sizes past the staging limit (a clear error, nothing launched)."""
 import numpy as np
 import pytest
 
-from gpu_util import F32, bits, dev, empty, host, synth_q8_0, torch
+from gpu_util import F32, bits, dev, empty, host, q8_gemm_range, synth_q8_0, torch
 
 pytestmark = pytest.mark.gpu
 
@@ -36,7 +36,7 @@ def run_both(w, x, n, k):
     assert np.array_equal(b0, b1)
     assert np.array_equal(bits(s0), bits(s1))
     assert np.array_equal(bits(p0), bits(p1))
-    if not (m >= 256 and n >= 8192):  # else the call without block dots runs the LDS-tiled kernel
+    if not q8_gemm_range(m, n):  # else the call without block dots runs the LDS-tiled kernel
         assert np.array_equal(bits(p0), bits(o0))
 
 
