@@ -49,8 +49,6 @@ namespace {
 typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr int kQWave = 64;
-constexpr int kDotBias = 0x4B400000;      // the bits of 1.5 * 2^23
-constexpr float kDotBiasF = 12582912.0f;  // 1.5 * 2^23
 constexpr int kQXcds = 8;
 template <typename F, int... I>
 __device__ inline void q_static_for_impl(F &&f, std::integer_sequence<int, I...>) {

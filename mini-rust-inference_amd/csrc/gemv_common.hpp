@@ -41,6 +41,13 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 constexpr int kMaxM = 4;
+// An int8 MFMA whose accumulator starts from kDotBias, the bits of
+// kDotBiasF = 1.5 * 2^23, leaves the bits of the f32 number kDotBiasF + dot
+// for any |dot| < 2^22 (the f32 spacing in [2^23, 2^24) is 1): subtracting
+// kDotBiasF gives (f32)dot exactly, at full rate, where v_cvt_f32_i32 issues
+// at half rate.  A Q8_0 block dot is at most 32 * 128 * 127 < 2^22.
+constexpr int kDotBias = 0x4B400000;
+constexpr float kDotBiasF = 12582912.0f;
 constexpr size_t kMaxLds = 64 * 1024;
 
 inline size_t ceil_div(size_t a, size_t b) { return (a + b - 1) / b; }

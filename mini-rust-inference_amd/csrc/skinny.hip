@@ -219,6 +219,11 @@ __global__ __launch_bounds__(TPW * kWave) void k_skinny_q8_0(
         for (int t = 0; t < NT; ++t) sr[u][t] = sp[t][(size_t)q * LB];
     }
     const v4i zero = {0, 0, 0, 0};
+    // Without W4 each block's MFMA starts from the bits of 1.5 * 2^23, so an
+    // output register read as f32 is 12582912 + dot exactly (|dot| < 2^22);
+    // one full-rate subtract gives (f32)dot, bit for bit what the half-rate
+    // v_cvt_f32_i32 gives.
+    const v4i cinit = W4 ? zero : v4i{kDotBias, kDotBias, kDotBias, kDotBias};
 
     // Lap L in ring slot U.  REFILL: lap L + RL exists and is loaded into
     // the slot; CHECK: skip padding blocks past nb (last laps only).
@@ -244,7 +249,7 @@ __global__ __launch_bounds__(TPW * kWave) void k_skinny_q8_0(
 #pragma unroll
                     for (int a = 0; a < AG; ++a) {
                         d[h][a][t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
-                            h ? hi8(xr[U][c][a]) : lo8(xr[U][c][a]), bv, zero, 0, 0, 0);
+                            h ? hi8(xr[U][c][a]) : lo8(xr[U][c][a]), bv, cinit, 0, 0, 0);
                         if constexpr (W4) {
 #pragma unroll
                             for (int i = 0; i < 4; ++i) d[h][a][t][i] >>= 4;
@@ -276,7 +281,9 @@ __global__ __launch_bounds__(TPW * kWave) void k_skinny_q8_0(
                         for (int a = 0; a < AG; ++a) {
 #pragma unroll
                             for (int i = 0; i < 4; ++i) {
-                                float tm = (float)d[h][a][t][i] * sa[a][i];
+                                const int dv = d[h][a][t][i];
+                                float tm = (W4 ? (float)dv : __int_as_float(dv) - kDotBiasF) *
+                                           sa[a][i];
                                 tm = tm * ds;
                                 fs[a][t][i] = fs[a][t][i] + tm;
                             }
@@ -286,7 +293,7 @@ __global__ __launch_bounds__(TPW * kWave) void k_skinny_q8_0(
                                     const int m = 16 * (a0 + a) + 4 * g + i;
                                     if (m < M && n[t] < N)
                                         block_dots[((size_t)m * N + n[t]) * nb + b] =
-                                            d[h][a][t][i];
+                                            W4 ? d[h][a][t][i] : d[h][a][t][i] - kDotBias;
                                 }
                             }
                         }
