@@ -38,8 +38,9 @@
  *
  * Concurrency: calls are asynchronous on `stream`.  Handles are immutable
  * after creation and may be shared by calls on any stream.  Internal scratch
- * (activation quantization) is kept per (device, stream), so concurrent calls
- * on different streams do not interfere.
+ * (activation quantization, the prefill GEMMs' partial tiles and tile
+ * counters) is kept per (device, stream), so concurrent calls on different
+ * streams do not interfere.
  */
 #ifndef MRI_QMATMUL_H
 #define MRI_QMATMUL_H

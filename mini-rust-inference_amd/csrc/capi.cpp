@@ -186,11 +186,19 @@ mri_status run_int8(const int8_t *act, size_t m, const float *sa_ptr,
 // matmul_q8_0_direct dispatch on quantized rows [m][kp] (chunk-permuted).
 mri_status run_q8(const int8_t *act, size_t m, const float *sa_rows,
                          const Q8MatrixDev &w, float *out, int32_t *block_dots,
-                         hipStream_t s) {
+                         hipStream_t s, bool may_alloc) {
     if (gemv_q8_supported(false, m, w.n_tiles, w.k_in, w.kp))
         return launch_gemv_q8_0(nullptr, act, m, sa_rows, w, out, block_dots, nullptr, s);
     // prefill sizes: the LDS-tiled kernel (it has no block-dot output)
-    if (!block_dots && gemm_q8_supported(m, w)) return launch_gemm_q8_0(act, m, sa_rows, w, out, s);
+    if (!block_dots && gemm_q8_supported(m, w)) {
+        void *ws = nullptr;
+        const size_t wsb = may_alloc ? gemm_q8_ws_bytes(m, w) : 0;
+        if (wsb) {
+            const mri_status st = gemm_ws_get(s, wsb, &ws);
+            if (st) return st;
+        }
+        return launch_gemm_q8_0(act, m, sa_rows, w, out, ws, s);
+    }
     return launch_skinny_q8_0(act, m, sa_rows, w, out, block_dots, s);
 }
 
@@ -855,7 +863,7 @@ static mri_status matmul_blocks(const char *name, const float *input, const size
     if (st) return st;
     if (d.n_out == 0) return MRI_OK;
     if (exact) return launch_skinny_q8_0(act, m, sc, d, out, block_dots_out, s);
-    return run_q8(act, m, sc, d, out, block_dots_out, s);
+    return run_q8(act, m, sc, d, out, block_dots_out, s, !fixed);
 }
 
 extern "C" {

@@ -315,10 +315,16 @@ __host__ __device__ inline size_t gemm_pack_offset(size_t m, size_t k, size_t mg
 // one): int32 partial tiles plus per-tile counters.  The counters must be
 // zero when the workspace is first used; every call leaves them zero.
 size_t gemm_ws_bytes(size_t m, const QMatrixDev &w);
-// gemm_q8.hip: prefill-sized matmul_q8_0_direct on LDS-staged MFMA tiles
+// Tile counters at the start of the GEMM workspace (gemm_ws_get), shared by
+// the INT8 and Q8_0 GEMMs: zero between calls.
+constexpr int kGemmWsCounters = 65536;
+// gemm_q8.hip: prefill-sized matmul_q8_0_direct on LDS-staged MFMA tiles.
+// ws: gemm_q8_ws_bytes(m, w) bytes of the GEMM workspace for the K split,
+// or null (no K split; nothing allocated).
 bool gemm_q8_supported(size_t m, const Q8MatrixDev &w);
+size_t gemm_q8_ws_bytes(size_t m, const Q8MatrixDev &w);
 mri_status launch_gemm_q8_0(const int8_t *act, size_t m, const float *sa_rows,
-                            const Q8MatrixDev &w, float *out, hipStream_t s);
+                            const Q8MatrixDev &w, float *out, void *ws, hipStream_t s);
 // rows: act_packed is the caller's row-major [m][k] int8 (gemm_rows_ok).
 mri_status launch_gemm_int8(const int8_t *act_packed, size_t m, const float *sa_ptr,
                             int sa_stride, float sa_value, const QMatrixDev &w,
@@ -373,8 +379,9 @@ mri_status launch_norm_quant(int form, const float *x, const float *w, const flo
 mri_status run_int8(const int8_t *act, size_t m, const float *sa_ptr, int sa_stride,
                     float sa_value, const QMatrixDev &w, float *out, int32_t *acc_out,
                     hipStream_t s);
+// may_alloc false: no workspace is allocated (no K split in the GEMM).
 mri_status run_q8(const int8_t *act, size_t m, const float *sa_rows, const Q8MatrixDev &w,
-                  float *out, int32_t *block_dots, hipStream_t s);
+                  float *out, int32_t *block_dots, hipStream_t s, bool may_alloc = true);
 mri_status launch_add_rmsnorm(float *x, const float *delta, size_t rows, size_t d,
                               const float *w, float eps, float *out, hipStream_t s);
 // RoPE of q in place; rotated k and v rows into the cache at start_pos + s.

@@ -495,7 +495,7 @@ constexpr size_t gemm_lds_bytes() {
 // ---------------------------------------------------------------------------
 constexpr int kSkNs = 4;                        // ring stages
 constexpr int kSkTileInts = 256 * 256;          // int32 of one partial tile
-constexpr int kSkMaxTiles = 65536;              // tile counters at the workspace start
+constexpr int kSkMaxTiles = kGemmWsCounters;    // tile counters at the workspace start
 
 // Split of `iters` iterations into nwg ranges: q = iters / nwg each, the
 // first rem = iters % nwg ranges one more.  Neither query divides by more

@@ -49,6 +49,7 @@ namespace {
 typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr int kQWave = 64;
+constexpr int kQWaitVm0 = 0x0F70;  // s_waitcnt vmcnt(0), others untouched
 constexpr int kQXcds = 8;
 template <typename F, int... I>
 __device__ inline void q_static_for_impl(F &&f, std::integer_sequence<int, I...>) {
@@ -130,8 +131,8 @@ constexpr int q8_stage_bytes() {
 template <int BM, int BN, int WM, int WN, int NS>
 __global__ __launch_bounds__(WM * WN * kQWave) void k_gemm_q8_0(
     const int8_t *__restrict__ act, int M, int kp, const float *__restrict__ sa_rows,
-    const int8_t *__restrict__ laps, int N, int n_tiles, int G, int n_mt, int n_total,
-    float *__restrict__ out) {
+    const int8_t *__restrict__ laps, int N, int n_tiles, int G, int n_mt, int n_total, int ks,
+    float *__restrict__ out, float *__restrict__ part, int *__restrict__ cnt) {
     constexpr int NW = WM * WN;
     constexpr int RG = BM / 32 / WM, TT = BN / 32 / WN;  // 32 x 32 sub-tiles per wave
     constexpr int FA = BM / 8, FB = BN / 8, FS = q8_scale_slots<BN, NW>();  // loads of a stage
@@ -146,9 +147,12 @@ __global__ __launch_bounds__(WM * WN * kQWave) void k_gemm_q8_0(
 
     // XCD-aware tile index: workgroups go to the 8 XCDs round-robin; the M
     // tiles of one weight column block run on one XCD and share its L2.
+    // With a K split the ks parts of a tile are adjacent items, each a
+    // contiguous range [s0, s1) of the K steps.
     const int per_xcd = (int)(gridDim.x / kQXcds);
-    const int tile = (int)(blockIdx.x % kQXcds) * per_xcd + (int)(blockIdx.x / kQXcds);
-    if (tile >= n_total) return;
+    const int item = (int)(blockIdx.x % kQXcds) * per_xcd + (int)(blockIdx.x / kQXcds);
+    if (item >= n_total * ks) return;
+    const int tile = item / ks, kpart = item - tile * ks;
     const int mt = tile % n_mt, nt = tile / n_mt;
 
     const int t = threadIdx.x;
@@ -156,6 +160,7 @@ __global__ __launch_bounds__(WM * WN * kQWave) void k_gemm_q8_0(
     const int wm = wv / WN, wn = wv % WN;
     const unsigned lds0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)s_buf);
     const int S = 2 * G;  // ring steps: half laps
+    const int s0 = split_lo(S, ks, kpart), s1 = split_lo(S, ks, kpart + 1);
 
     // This wave's loads of a stage.  Fragment f = wv + NW * j of the A
     // region: 16-row group f / 2, chunk f % 2 of the half lap; rows past M
@@ -189,7 +194,7 @@ __global__ __launch_bounds__(WM * WN * kQWave) void k_gemm_q8_0(
     // loads of step s (clamped to the last: the loads past the end re-read
     // it into a stage no later step reads, so every wait count is constant)
     auto issue = [&](int s) __attribute__((always_inline)) {
-        const int sc = min(s, S - 1);
+        const int sc = min(s, s1 - 1);
         const unsigned base = lds0 + (unsigned)((s % NS) * STAGE);
         const size_t ao = (size_t)sc * 128;
         const size_t bo = (size_t)(sc >> 1) * lap_bytes + (size_t)(sc & 1) * 2048;
@@ -229,13 +234,13 @@ __global__ __launch_bounds__(WM * WN * kQWave) void k_gemm_q8_0(
     for (int e = 0; e < 16; ++e) bias[e] = kDotBias;
 
 #pragma unroll
-    for (int s = 0; s < NS - 1; ++s) issue(s);
+    for (int s = s0; s < s0 + NS - 1; ++s) issue(s);
     // Step s: wait for its loads and for every wave to be done with step
     // s - 1, whose stage the loads of step s + NS - 1 refill; then its 4
     // blocks, software-pipelined: the MFMAs of block k + 1 (into registers
     // of their own) are issued before the fold of block k, so the MFMA pipe
     // and the VALU work side by side.
-    for (int s = 0; s < S; ++s) {
+    for (int s = s0; s < s1; ++s) {
         asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"((NS - 2) * L) : "memory");
         issue(s + NS - 1);
         const v4i *ss_ = s_buf + ((size_t)(s % NS) * STAGE + SA + SB) / 16;
@@ -309,6 +314,60 @@ __global__ __launch_bounds__(WM * WN * kQWave) void k_gemm_q8_0(
     // the clamped loads past the end may still be writing LDS
     asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
 
+    if (ks > 1) {
+        // K split: every part but the last to arrive leaves its partial sums
+        // in its slot (register e of sub-tile (i, j) of wave wv at word
+        // ((wv * RG * TT + i * TT + j) * 16 + e) * 64 + l) and counts itself
+        // on the tile's counter; the last adds the parts in part order, so
+        // the result does not depend on the order of arrival.  The slots are
+        // written with device-scope (sc1) stores, complete at vmcnt(0)
+        // before the barrier and the count, and read with device-scope
+        // loads, which do not hit lines this XCD's L2 cached before.
+        __shared__ int s_last;
+        const size_t wbase = (size_t)wv * RG * TT * 16 * 64 + l;
+        float *mine = part + ((size_t)tile * ks + kpart) * (BM * BN) + wbase;
+#pragma unroll
+        for (int i = 0; i < RG; ++i)
+#pragma unroll
+            for (int j = 0; j < TT; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                    __hip_atomic_store(mine + ((i * TT + j) * 16 + e) * 64, fs[i][j][e],
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(kQWaitVm0);
+        __syncthreads();
+        if (t == 0)
+            s_last = __hip_atomic_fetch_add(&cnt[tile], 1, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT) == ks - 1;
+        __syncthreads();
+        if (!s_last) return;
+        float tot[RG][TT][16];
+        for (int p = 0; p < ks; ++p) {
+            const float *src = part + ((size_t)tile * ks + p) * (BM * BN) + wbase;
+#pragma unroll
+            for (int i = 0; i < RG; ++i)
+#pragma unroll
+                for (int j = 0; j < TT; ++j)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const float v = p == kpart ? fs[i][j][e]
+                                                   : __hip_atomic_load(
+                                                         src + ((i * TT + j) * 16 + e) * 64,
+                                                         __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT);
+                        tot[i][j][e] = p == 0 ? v : tot[i][j][e] + v;
+                    }
+        }
+#pragma unroll
+        for (int i = 0; i < RG; ++i)
+#pragma unroll
+            for (int j = 0; j < TT; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) fs[i][j][e] = tot[i][j][e];
+        if (t == 0)  // ready for the next call on this stream
+            __hip_atomic_store(&cnt[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
     // register e of sub-tile (i, j): row 32 i + 8 (e / 4) + 4 u + e % 4 of the
     // wave's rows, channel 32 j + l % 32 of its channels
 #pragma unroll
@@ -330,9 +389,28 @@ __global__ __launch_bounds__(WM * WN * kQWave) void k_gemm_q8_0(
     }
 }
 
+constexpr int kQ8BM = 128, kQ8BN = 64;  // the tile of the launched instance
+
+// Tiles of the launched instance for m rows, and its K split: 2-way when
+// the tiles fill at most one of the two workgroup slots of every CU, each
+// part keeping at least 8 half-lap steps.  (The GEMM's range, m * n > 2^20,
+// always has more than 128 tiles of 128 x 64, so a 4-way split would leave
+// CUs idle no less.)
+size_t q8_tiles(size_t m, const Q8MatrixDev &w) {
+    return ((m + kQ8BM - 1) / kQ8BM) * ((w.n_tiles + kQ8BN / 16 - 1) / (kQ8BN / 16));
+}
+int q8_ks(size_t m, const Q8MatrixDev &w) {
+    const size_t cus = (size_t)std::max(device_cus(), 0), tiles = q8_tiles(m, w);
+    const size_t S = 2 * w.laps_per_tile();
+    int ks = 1;
+    if (cus > 0 && tiles <= cus && S >= 16) ks = 2;
+    if (tiles * (size_t)ks > (size_t)kGemmWsCounters) ks = 1;
+    return ks;
+}
+
 template <int BM, int BN, int WM, int WN, int NS>
 mri_status launch_q8_inst(const int8_t *act, size_t m, const float *sa_rows,
-                          const Q8MatrixDev &w, float *out, hipStream_t s) {
+                          const Q8MatrixDev &w, float *out, void *ws, hipStream_t s) {
     constexpr size_t lds = (size_t)NS * q8_stage_bytes<BM, BN, WM * WN>();
     static DeviceOnce attr;
     MRI_HIP(attr.run([&](int) {
@@ -343,11 +421,14 @@ mri_status launch_q8_inst(const int8_t *act, size_t m, const float *sa_rows,
     const size_t n_mt = (m + BM - 1) / BM;
     const size_t n_nt = (w.n_tiles + BN / 16 - 1) / (BN / 16);
     const size_t total = n_mt * n_nt;
-    const size_t grid = (total + kQXcds - 1) / kQXcds * kQXcds;
+    const int ks = ws ? q8_ks(m, w) : 1;
+    int *cnt = static_cast<int *>(ws);
+    float *part = ws ? reinterpret_cast<float *>(cnt + kGemmWsCounters) : nullptr;
+    const size_t grid = (total * ks + kQXcds - 1) / kQXcds * kQXcds;
     hipLaunchKernelGGL((k_gemm_q8_0<BM, BN, WM, WN, NS>), dim3((unsigned)grid),
                        dim3(WM * WN * kQWave), lds, s, act, (int)m, (int)w.kp, sa_rows, w.laps,
                        (int)w.n_out, (int)w.n_tiles, (int)w.laps_per_tile(), (int)n_mt,
-                       (int)total, out);
+                       (int)total, ks, out, part, cnt);
     MRI_LAUNCHED("k_gemm_q8_0");
     return MRI_OK;
 }
@@ -379,8 +460,17 @@ bool gemm_q8_supported(size_t m, const Q8MatrixDev &w) {
 // than 4 of 64 x 32 halve each wave's serial fold per step and took the
 // latency floor from 43 to 39 us (512 x 11008 -> 4096: 108 against 117).
 mri_status launch_gemm_q8_0(const int8_t *act, size_t m, const float *sa_rows,
-                            const Q8MatrixDev &w, float *out, hipStream_t s) {
-    return launch_q8_inst<128, 64, 4, 2, 3>(act, m, sa_rows, w, out, s);
+                            const Q8MatrixDev &w, float *out, void *ws, hipStream_t s) {
+    return launch_q8_inst<kQ8BM, kQ8BN, 4, 2, 3>(act, m, sa_rows, w, out, ws, s);
+}
+
+// [tile counters (kGemmWsCounters ints, shared with the INT8 GEMM's)]
+// [f32 partial tiles: ks slots per tile]; 0 without a K split.
+size_t gemm_q8_ws_bytes(size_t m, const Q8MatrixDev &w) {
+    const int ks = q8_ks(m, w);
+    if (ks == 1) return 0;
+    return (size_t)kGemmWsCounters * sizeof(int) +
+           q8_tiles(m, w) * (size_t)ks * kQ8BM * kQ8BN * sizeof(float);
 }
 
 }  // namespace mri

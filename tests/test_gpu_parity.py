@@ -565,6 +565,66 @@ def test_q8_0_graph_replay_and_streams():
     check(hx, "back to back")
 
 
+def test_q8_0_gemm_k_split():
+    """The LDS-tiled Q8_0 GEMM with its K split (2 parts per tile when the
+    tiles would fill at most one workgroup slot per CU: 200 x 4096 x 6000
+    and 128 x 2048 x 8256 here): within the contract of the oracle,
+    deterministic (the parts are added in part order, whatever the order of
+    arrival: the same input gives the same bits on every call), the tile
+    counters reset between back-to-back calls of different shapes, HIP graph
+    replays equal eager calls, and the no-allocation entry point (no K split)
+    is within the contract too."""
+    t = torch()
+    rng = np.random.default_rng(91)
+    cases = [(200, 6000, 4096), (128, 8256, 2048)]
+    ws, xs, outs, raws = [], [], [], []
+    for m, n, k in cases:
+        raw = synth_q8_0(rng, n, k, with_min=True)
+        raws.append(raw)
+        ws.append(mri().Q8Matrix.from_raw_bytes(raw, n, k))
+        xs.append(dev(rng.standard_normal((m, k)).astype(F32)))
+        outs.append(empty((m, n), t.float32))
+
+    def calls():
+        for x, w, o in zip(xs, ws, outs):
+            mri().matmul_q8_0_direct(x, w, o)
+
+    calls()
+    t.cuda.synchronize()
+    first = [host(o).copy() for o in outs]
+    for (m, n, k), raw, x, got in zip(cases, raws, xs, first):
+        say(f"q8_0 gemm k split m={m} n={n} k={k}")
+        out0, terms = q8_oracle_sliced(host(x), raw, n, k)
+        assert_q8_close(got, out0, terms, f"k split {m}x{n}x{k}")
+        na = empty((m, n), t.float32)
+        mri().matmul_q8_0_direct_noalloc(x, ws[cases.index((m, n, k))], na)
+        assert_q8_close(host(na), out0, terms, f"no-alloc {m}x{n}x{k}")
+    calls()   # back to back: the counters were left at zero
+    for o, f in zip(outs, first):
+        assert_bits_equal(host(o), f, "k split, second call")
+    s = t.cuda.Stream()
+    s.wait_stream(t.cuda.current_stream())
+    with t.cuda.stream(s):   # the stream's staging and workspace exist before capture
+        calls()
+    t.cuda.synchronize()
+    g = t.cuda.CUDAGraph()
+    with t.cuda.graph(g, stream=s):
+        calls()
+    for rep in range(3):
+        for x, (m, n, k) in zip(xs, cases):
+            x.copy_(dev(rng.standard_normal((m, k)).astype(F32) * (rep + 1)))
+        for o in outs:
+            o.zero_()
+        t.cuda.synchronize()
+        g.replay()
+        t.cuda.synchronize()
+        replayed = [host(o).copy() for o in outs]
+        calls()   # eager work between replays, on the same inputs
+        t.cuda.synchronize()
+        for o, r in zip(outs, replayed):
+            assert_bits_equal(r, host(o), f"graph replay {rep} vs eager")
+
+
 def test_q8_0_reference_encoder_weights():
     """Weights built by create_q8_0_block (dequant.rs:389-421), as
     Q8_0WeightMatrix::from_f32_tensor does."""
