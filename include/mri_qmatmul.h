@@ -30,9 +30,9 @@
  *    mri_matmul_q8_0_direct_exact keeps the block order at every m.
  *  - W4A8 (extension) f32 outputs equal, bit for bit, those of
  *    mri_matmul_q8_0_direct on the expanded blocks (quant = nibble - 8,
- *    the same scale bits); for m >= 128 and m * n > 2^20 they equal those
- *    of mri_matmul_q8_0_direct_exact instead.  Against the reference's order
- *    that is bit-exact for 5 <= m and within the Q8_0 bound for m <= 4.
+ *    the same scale bits) at every m: the same kernels in the same order.
+ *    Against the reference's order that is bit-exact where matmul_q8_0_direct
+ *    is, and within the Q8_0 bound elsewhere.
  *  - Q4_0 W4A32 (matmul_q4_0_dequant and its handle form) sums in another
  *    order than the reference and is within 1e-5 * max(|ref|, sum|x_k w_k|).
  *

@@ -121,28 +121,45 @@ constexpr int q8_scale_slots() {
     return BN / 16 > NW ? BN / 16 : NW;
 }
 
-// Bytes of one ring stage (half a lap: 2 chunks, 4 blocks) of a BM x BN tile:
-// activation fragments, weight chunks, and the lap's weight scales.
-template <int BM, int BN, int NW>
-constexpr int q8_stage_bytes() {
-    return BM * 128 + BN * 128 + q8_scale_slots<BN, NW>() * 256;
+// Weight fragments (1 KiB each) of a stage: Q8_0, one per 16-channel tile
+// and chunk; W4, one quant piece (the half lap's two chunks) per tile, at
+// least one per wave (waves past the tile count reload the last tile's
+// piece into a slot nothing reads).
+template <int BN, int NW, bool W4>
+constexpr int q8_b_slots() {
+    return W4 ? (BN / 16 > NW ? BN / 16 : NW) : BN / 8;
 }
 
-template <int BM, int BN, int WM, int WN, int NS>
+// The same wait for the W4 instance (RG = TT = 1): the activation quads and
+// the weight quant pieces.
+__device__ inline void q8_wait_lds_w4(v4i (&a)[2][1][2], v4i (&bw)[1][2]) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(a[0][0][0]), "+v"(a[0][0][1]), "+v"(a[1][0][0]), "+v"(a[1][0][1]),
+                   "+v"(bw[0][0]), "+v"(bw[0][1]));
+}
+
+// Bytes of one ring stage (half a lap: 2 chunks, 4 blocks) of a BM x BN tile:
+// activation fragments, weight chunks, and the lap's weight scales.
+template <int BM, int BN, int NW, bool W4>
+constexpr int q8_stage_bytes() {
+    return BM * 128 + q8_b_slots<BN, NW, W4>() * 1024 + q8_scale_slots<BN, NW>() * 256;
+}
+
+template <int BM, int BN, int WM, int WN, int NS, bool W4>
 __global__ __launch_bounds__(WM * WN * kQWave) void k_gemm_q8_0(
     const int8_t *__restrict__ act, int M, int kp, const float *__restrict__ sa_rows,
     const int8_t *__restrict__ laps, int N, int n_tiles, int G, int n_mt, int n_total, int ks,
     float *__restrict__ out, float *__restrict__ part, int *__restrict__ cnt) {
     constexpr int NW = WM * WN;
     constexpr int RG = BM / 32 / WM, TT = BN / 32 / WN;  // 32 x 32 sub-tiles per wave
-    constexpr int FA = BM / 8, FB = BN / 8, FS = q8_scale_slots<BN, NW>();  // loads of a stage
+    constexpr int FA = BM / 8, FB = q8_b_slots<BN, NW, W4>(), FS = q8_scale_slots<BN, NW>();
     constexpr int LA = FA / NW, LB = FB / NW, LS = FS / NW;  // ... per wave
     static_assert(RG >= 1 && TT >= 1 && FA % NW == 0 && FB % NW == 0 && FS % NW == 0,
                   "wave split");
     static_assert(NS >= 2, "ring depth");
     constexpr int L = LA + LB + LS;  // loads per wave and stage, the same for every wave
-    constexpr int SA = BM * 128, SB = BN * 128;
-    constexpr int STAGE = q8_stage_bytes<BM, BN, NW>();
+    constexpr int SA = BM * 128, SB = FB * 1024;
+    constexpr int STAGE = q8_stage_bytes<BM, BN, NW, W4>();
     extern __shared__ v4i s_buf[];
 
     // XCD-aware tile index: workgroups go to the 8 XCDs round-robin; the M
@@ -173,7 +190,8 @@ __global__ __launch_bounds__(WM * WN * kQWave) void k_gemm_q8_0(
     const int8_t *a_src[LA];
     const int8_t *b_src[LB];
     const int8_t *s_src[LS];
-    const size_t lap_bytes = kQ8LapBytes;
+    const size_t lap_bytes = W4 ? kQ4LapBytes : kQ8LapBytes;
+    constexpr int kScaleOff = W4 ? 2048 : 4096;  // the lap's scales in its block
 #pragma unroll
     for (int j = 0; j < LA; ++j) {
         const int f = wv + NW * j;
@@ -183,13 +201,18 @@ __global__ __launch_bounds__(WM * WN * kQWave) void k_gemm_q8_0(
 #pragma unroll
     for (int j = 0; j < LB; ++j) {
         const int f = wv + NW * j;
-        const int T = min(BN / 16 * nt + (f >> 1), n_tiles - 1);
-        b_src[j] = laps + (size_t)T * G * lap_bytes + 1024 * (f & 1) + 16 * l;
+        if constexpr (W4) {  // the tile's quant piece of the half lap
+            const int T = min(BN / 16 * nt + min(f, BN / 16 - 1), n_tiles - 1);
+            b_src[j] = laps + (size_t)T * G * lap_bytes + 16 * l;
+        } else {
+            const int T = min(BN / 16 * nt + (f >> 1), n_tiles - 1);
+            b_src[j] = laps + (size_t)T * G * lap_bytes + 1024 * (f & 1) + 16 * l;
+        }
     }
 #pragma unroll
     for (int j = 0; j < LS; ++j) {
         const int T = min(BN / 16 * nt + min(wv + NW * j, BN / 16 - 1), n_tiles - 1);
-        s_src[j] = laps + (size_t)T * G * lap_bytes + 4096 + 4 * l;
+        s_src[j] = laps + (size_t)T * G * lap_bytes + kScaleOff + 4 * l;
     }
     // loads of step s (clamped to the last: the loads past the end re-read
     // it into a stage no later step reads, so every wait count is constant)
@@ -197,7 +220,7 @@ __global__ __launch_bounds__(WM * WN * kQWave) void k_gemm_q8_0(
         const int sc = min(s, s1 - 1);
         const unsigned base = lds0 + (unsigned)((s % NS) * STAGE);
         const size_t ao = (size_t)sc * 128;
-        const size_t bo = (size_t)(sc >> 1) * lap_bytes + (size_t)(sc & 1) * 2048;
+        const size_t bo = (size_t)(sc >> 1) * lap_bytes + (size_t)(sc & 1) * (W4 ? 1024 : 2048);
         const size_t so = (size_t)(sc >> 1) * lap_bytes;
 #pragma unroll
         for (int j = 0; j < LA; ++j) q_dma16(a_src[j] + ao, base + (wv + NW * j) * 1024);
@@ -255,6 +278,7 @@ __global__ __launch_bounds__(WM * WN * kQWave) void k_gemm_q8_0(
         // that takes every operand as its own in-out operand, so that no use
         // can be scheduled before it.
         v4i a[2][RG][2], b[2][TT][2];
+        v4i bw[TT][2];  // W4: the quant pieces of lane' and lane' + 16
         const unsigned st = lds0 + (unsigned)((s % NS) * STAGE) + (unsigned)(16 * (32 * u + r16));
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
@@ -266,23 +290,52 @@ __global__ __launch_bounds__(WM * WN * kQWave) void k_gemm_q8_0(
             }
 #pragma unroll
             for (int j = 0; j < TT; ++j) {
-                const unsigned ad =
-                    st + (unsigned)(SA + ((2 * (wn * TT + j) + half) * 2 + c) * 1024);
-                asm volatile("ds_read2_b64 %0, %1 offset1:32" : "=v"(b[c][j][0]) : "v"(ad));
-                asm volatile("ds_read2_b64 %0, %1 offset0:1 offset1:33" : "=v"(b[c][j][1]) : "v"(ad));
+                if constexpr (W4) {
+                    // one 16-byte piece per lane' holds the half lap's 4
+                    // block words: read it once, at c = 0
+                    if (c == 0) {
+                        const unsigned ad = st + (unsigned)(SA + (2 * (wn * TT + j) + half) * 1024);
+                        asm volatile("ds_read_b128 %0, %1" : "=v"(bw[j][0]) : "v"(ad));
+                        asm volatile("ds_read_b128 %0, %1 offset:256" : "=v"(bw[j][1]) : "v"(ad));
+                    }
+                } else {
+                    const unsigned ad =
+                        st + (unsigned)(SA + ((2 * (wn * TT + j) + half) * 2 + c) * 1024);
+                    asm volatile("ds_read2_b64 %0, %1 offset1:32" : "=v"(b[c][j][0]) : "v"(ad));
+                    asm volatile("ds_read2_b64 %0, %1 offset0:1 offset1:33"
+                                 : "=v"(b[c][j][1])
+                                 : "v"(ad));
+                }
             }
         }
         static_assert(RG * 4 + TT * 4 <= 24, "operands of the wait");
-        q8_wait_lds(a, b);
+        if constexpr (W4) {
+            static_assert(RG == 1 && TT == 1, "W4 wave tile");
+            q8_wait_lds_w4(a, bw);
+        } else {
+            q8_wait_lds(a, b);
+        }
         v16i d[2][RG][TT];  // block dots of block k in set k % 2
         auto dots = [&](auto kk) __attribute__((always_inline)) {
             constexpr int k = decltype(kk)::value, c = k / 2, h = k % 2;
 #pragma unroll
             for (int i = 0; i < RG; ++i)
 #pragma unroll
-                for (int j = 0; j < TT; ++j)
-                    d[k % 2][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[c][i][h], b[c][j][h],
-                                                                         bias, 0, 0, 0);
+                for (int j = 0; j < TT; ++j) {
+                    v4i bv;
+                    if constexpr (W4) {
+                        // word 2c + h of each piece: block h of chunk c, 8
+                        // elements as nibbles; each moved to the high half of
+                        // its byte reads as 16 * quant (k order as in Q8_0)
+                        constexpr int kHi = (int)0xF0F0F0F0u;
+                        const int w0 = bw[j][0][2 * c + h], w1 = bw[j][1][2 * c + h];
+                        bv = v4i{(w0 << 4) & kHi, w0 & kHi, (w1 << 4) & kHi, w1 & kHi};
+                    } else {
+                        bv = b[c][j][h];
+                    }
+                    d[k % 2][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[c][i][h], bv, bias,
+                                                                         0, 0, 0);
+                }
         };
         auto fold = [&](auto kk) __attribute__((always_inline)) {
             constexpr int k = decltype(kk)::value, c = k / 2, h = k % 2;
@@ -294,6 +347,10 @@ __global__ __launch_bounds__(WM * WN * kQWave) void k_gemm_q8_0(
                 // full-rate v_fma_f32 rather than a mixed-precision FMA
                 float ds;
                 asm("v_cvt_f32_f16_e32 %0, %1" : "=v"(ds) : "v"(h ? (word >> 16) : word));
+                // W4: the dots are 16 * dot (exact, < 2^22), so the scale
+                // takes the 1/16 (exact: a power of two on a normal f32), and
+                // fma(16 dot, d / 16, s) == fma(dot, d, s) bit for bit
+                if constexpr (W4) ds = ds * 0.0625f;
 #pragma unroll
                 for (int i = 0; i < RG; ++i)
 #pragma unroll
@@ -408,14 +465,14 @@ int q8_ks(size_t m, const Q8MatrixDev &w) {
     return ks;
 }
 
-template <int BM, int BN, int WM, int WN, int NS>
+template <int BM, int BN, int WM, int WN, int NS, bool W4>
 mri_status launch_q8_inst(const int8_t *act, size_t m, const float *sa_rows,
                           const Q8MatrixDev &w, float *out, void *ws, hipStream_t s) {
-    constexpr size_t lds = (size_t)NS * q8_stage_bytes<BM, BN, WM * WN>();
+    constexpr size_t lds = (size_t)NS * q8_stage_bytes<BM, BN, WM * WN, W4>();
     static DeviceOnce attr;
     MRI_HIP(attr.run([&](int) {
         return hipFuncSetAttribute(
-            reinterpret_cast<const void *>(&k_gemm_q8_0<BM, BN, WM, WN, NS>),
+            reinterpret_cast<const void *>(&k_gemm_q8_0<BM, BN, WM, WN, NS, W4>),
             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     }));
     const size_t n_mt = (m + BM - 1) / BM;
@@ -425,7 +482,7 @@ mri_status launch_q8_inst(const int8_t *act, size_t m, const float *sa_rows,
     int *cnt = static_cast<int *>(ws);
     float *part = ws ? reinterpret_cast<float *>(cnt + kGemmWsCounters) : nullptr;
     const size_t grid = (total * ks + kQXcds - 1) / kQXcds * kQXcds;
-    hipLaunchKernelGGL((k_gemm_q8_0<BM, BN, WM, WN, NS>), dim3((unsigned)grid),
+    hipLaunchKernelGGL((k_gemm_q8_0<BM, BN, WM, WN, NS, W4>), dim3((unsigned)grid),
                        dim3(WM * WN * kQWave), lds, s, act, (int)m, (int)w.kp, sa_rows, w.laps,
                        (int)w.n_out, (int)w.n_tiles, (int)w.laps_per_tile(), (int)n_mt,
                        (int)total, ks, out, part, cnt);
@@ -446,7 +503,7 @@ mri_status launch_q8_inst(const int8_t *act, size_t m, const float *sa_rows,
 // 61.5 / 45.0, 512 x 12288 155 / 101.7, 512 x 22016 258 / 171; at
 // K = 11008, 512 x 4096 148.7 / 108 and 256 x 4096 80 / 112.
 bool gemm_q8_supported(size_t m, const Q8MatrixDev &w) {
-    return !w.w4 && m >= 128 && m * w.n_out > (1ull << 20) && m * w.kp < (1ull << 31) &&
+    return m >= 128 && m * w.n_out > (1ull << 20) && m * w.kp < (1ull << 31) &&
            m * w.n_out < (1ull << 31);
 }
 
@@ -461,7 +518,8 @@ bool gemm_q8_supported(size_t m, const Q8MatrixDev &w) {
 // latency floor from 43 to 39 us (512 x 11008 -> 4096: 108 against 117).
 mri_status launch_gemm_q8_0(const int8_t *act, size_t m, const float *sa_rows,
                             const Q8MatrixDev &w, float *out, void *ws, hipStream_t s) {
-    return launch_q8_inst<kQ8BM, kQ8BN, 4, 2, 3>(act, m, sa_rows, w, out, ws, s);
+    if (w.w4) return launch_q8_inst<kQ8BM, kQ8BN, 4, 2, 3, true>(act, m, sa_rows, w, out, ws, s);
+    return launch_q8_inst<kQ8BM, kQ8BN, 4, 2, 3, false>(act, m, sa_rows, w, out, ws, s);
 }
 
 // [tile counters (kGemmWsCounters ints, shared with the INT8 GEMM's)]

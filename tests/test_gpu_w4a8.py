@@ -3,8 +3,10 @@ mri_matmul_q4_0_w4a8) against the oracle's orc_matmul_q4_0_w4a8, which is
 pinned to matmul_q8_0_direct on the expanded blocks
 (tests/test_oracle_closed_form.py).  Block dots and activation scales must
 be bit-identical, in both nibble orders; f32 outputs are within
-1e-5 * max(|ref|, sum_b |t_b|) of the block-ordered sum (the decode GEMV,
-M <= 4, adds per-wave partial sums) and bit-identical above four rows."""
+1e-5 * max(|ref|, sum_b |t_b|) of the block-ordered sum where the kernel
+reorders it (the decode GEMV, M <= 4, adds per-wave partial sums; the
+LDS-tiled GEMM, M >= 128 and M * N > 2^20 without block dots, folds with
+FMAs) and bit-identical elsewhere."""
 import sys
 
 import numpy as np
@@ -33,6 +35,8 @@ W4A8_SHAPES = [
     (1, 64, 11008), (1, 32000 // 8, 4096), (2, 33, 256), (3, 48, 1024), (4, 64, 4096),
     (5, 40, 512), (9, 24, 1024), (16, 272, 4096), (33, 48, 256), (100, 40, 1024),
     (2, 32, 16384), (1, 48, 20480), (1, 8200, 992), (4, 11008, 4096),
+    # prefill sizes on the LDS-tiled GEMM (128 rows and more than 2^20 outputs)
+    (128, 8200, 512), (300, 4100, 1024),
 ]
 
 
@@ -56,6 +60,11 @@ def test_w4a8_parity(m, n, k, order):
     assert_q8_close(host(out), out0, q8_terms_abs_sum(bd0, sa0, d), "w4a8 out")
     if m > 4:  # the kernels above four rows keep the reference's order
         assert_bits_equal(host(out), out0, "w4a8 out")
+    if q8_gemm_range(m, n):  # without block dots: the LDS-tiled GEMM, within the contract
+        out3 = empty((m, n), t.float32)
+        mri().matmul_q4_0_w4a8(dev(x), w, out3)
+        assert_q8_close(host(out3), out0, q8_terms_abs_sum(bd0, sa0, d), "w4a8 out (gemm)")
+        return
     out2 = empty((m, n), t.float32)          # without the debug outputs
     sa2 = empty(m, t.float32)
     mri().matmul_q4_0_w4a8(dev(x), w, out2, act_scales_out=sa2)
@@ -65,15 +74,14 @@ def test_w4a8_parity(m, n, k, order):
 
 @pytest.mark.parametrize("m,n,k", [(1, 11008, 4096), (1, 50, 96), (3, 48, 1024),
                                    (4, 64, 4096), (9, 24, 1024), (40, 272, 4096),
-                                   (256, 8192, 256)])
+                                   (256, 8192, 256), (200, 6000, 4096), (512, 4096, 1024)])
 def test_w4a8_equals_q8_0_on_expanded_blocks(m, n, k):
     """W4A8 runs the Q8_0 kernels with a 4-bit B operand, so its outputs
     equal matmul_q8_0_direct's on the same blocks expanded to Q8_0 (quants
     nibble - 8, the same f16 scale bits) bit for bit, at every row count:
-    the GEMV's wave order at 1-4 rows included.  From 128 rows and more than
-    2^20 outputs the Q8_0 entry point takes the LDS-tiled GEMM, which W4A8
-    does not; there the comparison is with the block-ordered entry point
-    (the skinny kernel both run)."""
+    the GEMV's wave order at 1-4 rows, the skinny kernel's block order, and
+    the LDS-tiled GEMM from 128 rows and more than 2^20 outputs (16 * dot
+    folded with d / 16, K split included at 200 x 6000 x 4096)."""
     say(f"w4a8 vs q8_0 on expanded blocks m={m} n={n} k={k}")
     t = torch()
     rng = np.random.default_rng(m * 5 + n + k)
@@ -83,10 +91,7 @@ def test_w4a8_equals_q8_0_on_expanded_blocks(m, n, k):
     w8 = mri().Q8Matrix.from_raw_bytes(CF.q4_0_to_q8_0(raw, n, k), n, k)
     o4, o8 = empty((m, n), t.float32), empty((m, n), t.float32)
     mri().matmul_q4_0_w4a8(dev(x), w4, o4)
-    if q8_gemm_range(m, n):
-        mri().matmul_q8_0_direct_exact(dev(x), w8, o8)
-    else:
-        mri().matmul_q8_0_direct(dev(x), w8, o8)
+    mri().matmul_q8_0_direct(dev(x), w8, o8)
     assert_bits_equal(host(o4), host(o8), "w4a8 vs q8_0 on the expanded blocks")
 
 
