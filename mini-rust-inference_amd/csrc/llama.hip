@@ -921,6 +921,12 @@ constexpr float kAmMove = 12.0f;                      // P <= 2^12 between moves
 static_assert((size_t)kAmMlOff + 2 * 4 * kAmQ * sizeof(float) <= kAmLds,
               "combine partials, m and l alias the staged tiles and the queries");
 
+// The loads below write M0 themselves; no code of this file keeps a value
+// in M0 across them (gfx9 LDS instructions do not use it, and the generated
+// code has no other M0 write), so clobbering the reserved register is safe
+// here.  s_nop 0 covers the M0 -> LDS DMA hazard.
+#pragma clang diagnostic ignored "-Winline-asm"
+
 // 16 bytes per lane from a per-lane address into LDS at lds + 16 * lane
 __device__ inline void am_dma16(const void *g, unsigned lds) {
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
