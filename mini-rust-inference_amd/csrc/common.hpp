@@ -188,6 +188,11 @@ mri_status launch_quantize_rows(const float *x, size_t m, size_t k,
                                 size_t ld_out, bool q8_perm_layout,
                                 int8_t *q_pad, int8_t *q_plain,
                                 float *scales, hipStream_t s);
+// The same for rows of 2k, [gate | up]: quantizes their SwiGLU, silu(g) * u
+// (the values the prefill SwiGLU kernel writes), into q_pad [m][ld_out].
+mri_status launch_swiglu_quantize_rows(const float *gu, size_t m, size_t k, size_t ld_out,
+                                       bool q8_perm_layout, int8_t *q_pad, float *scales,
+                                       hipStream_t s);
 mri_status launch_quantize_per_channel(const float *w, size_t n, size_t k,
                                        int8_t *data, float *scales,
                                        hipStream_t s);

@@ -365,6 +365,17 @@ mri_status block(mri_llama *m, size_t li, size_t rows, size_t start, mri_kv_cach
         if (o.in_keys) xrow = m->x;
         return row_proj(w, src, o, out, s);
     };
+    // rows path: m->tmp (a projection's output) added to the residual stream,
+    // fused with the RMSNorm that follows
+    auto out_tail = [&](const float *norm) {
+        if (m->fuse_norm) {
+            m->norm_w = norm;
+            m->qform = -1;
+            return launch_rmsnorm_stats(2, m->x, m->tmp, nullptr, m->x, rows, g.dim, norm, g.eps,
+                                        m->nstats, s);
+        }
+        return launch_add_rmsnorm(m->x, m->tmp, rows, g.dim, norm, g.eps, m->normed, s);
+    };
     // projections whose output is added to the residual stream
     // (up: in is a SwiGLU gate row, applied in the projection; one row only)
     auto out_proj = [&](const mri_weight_ref &w, const float *in, const float *norm,
@@ -376,13 +387,7 @@ mri_status block(mri_llama *m, size_t li, size_t rows, size_t start, mri_kv_cach
             return row_proj(w, in, o, m->x, s);
         }
         TRY(proj(w, in, rows, m->tmp, s));
-        if (m->fuse_norm) {
-            m->norm_w = norm;
-            m->qform = -1;
-            return launch_rmsnorm_stats(2, m->x, m->tmp, nullptr, m->x, rows, g.dim, norm, g.eps,
-                                        m->nstats, s);
-        }
-        return launch_add_rmsnorm(m->x, m->tmp, rows, g.dim, norm, g.eps, m->normed, s);
+        return out_tail(norm);
     };
     float *kc = c->k + li * c->max_seq * c->kvd, *vc = c->v + li * c->max_seq * c->kvd;
     float *q, *k, *v;
@@ -452,6 +457,24 @@ mri_status block(mri_llama *m, size_t li, size_t rows, size_t start, mri_kv_cach
     }
     if (fold) return out_proj(L.w[6], m->gu, next_norm, m->gu + g.ffn_dim);
     float *act = m->gu;
+    const mri_weight_ref &wd = L.w[6];
+    if (L.gu.ptr && (wd.format == MRI_WEIGHT_Q8_0 || wd.format == MRI_WEIGHT_Q4_0_W4A8)) {
+        // Q8_0 / W4A8 down projection: the SwiGLU rows are quantized as they
+        // are formed (the rows, scales and products of launch_swiglu_rows
+        // followed by matmul_q8_0_direct's own per-row quantization)
+        const Q8MatrixDev &dv =
+            wd.format == MRI_WEIGHT_Q8_0 ? handle_dev(static_cast<const mri_q8_0_matrix *>(wd.ptr))
+                                         : handle_dev(static_cast<const mri_q4_0_matrix *>(wd.ptr));
+        if (dv.k_in != g.ffn_dim)
+            return set_error(MRI_ERR_SHAPE_MISMATCH, "down projection: k_in != ffn_dim");
+        if (dv.n_out) {
+            TRY(launch_swiglu_quantize_rows(m->gu, rows, g.ffn_dim, dv.kp, true, m->qact,
+                                            m->qscale, s));
+            m->qform = -1;  // qact no longer holds the normalized rows
+            TRY(run_q8(m->qact, rows, m->qscale, dv, m->tmp, nullptr, s));
+        }
+        return out_tail(next_norm);
+    }
     if (L.gu.ptr) {
         act = m->act;
         TRY(launch_swiglu_rows(m->gu, rows, g.ffn_dim, act, s));
@@ -572,7 +595,8 @@ mri_status mri_llama_create(const mri_llama_config *cfg, const float *token_embd
         (st = dalloc_t(m, R * m->qd, &m->attn)) || (st = dalloc_t(m, R * 2 * g.ffn_dim, &m->gu)) ||
         (st = dalloc_t(m, R * g.ffn_dim, &m->act)) || (st = dalloc_t(m, R, &m->tok)) ||
         (st = dalloc_t(m, 2 * R, &m->nstats)) || (st = dalloc_t(m, R, &m->qscale)) ||
-        (st = dalloc_t(m, round_up(R, 32) * round_up(g.dim, 256), &m->qact)) ||
+        (st = dalloc_t(m, round_up(R, 32) * round_up(std::max(g.dim, g.ffn_dim), 256),
+                       &m->qact)) ||
         (st = dalloc_t(m, R + 1, &m->gen)) ||
         (st = dalloc_t(m, attention_part_floats(g.n_heads, hd, R), &m->attn_part)))
         return fail(st);

@@ -108,29 +108,57 @@ __device__ inline size_t row_pos(size_t kk, int perm) {
     return perm ? (kk & ~(size_t)63) + q8_perm((int)(kk & 63)) : kk;
 }
 
+// SwiGLU of one element, silu(g) * u (activation/swiglu.rs, silu.rs:23-26),
+// in the expression of the prefill SwiGLU kernel (k_swiglu_rows4), so that
+// the values are its own.
+__device__ inline float swiglu_elem(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
 // One block per row: quantize_symmetric of each row separately.  NV > 0:
 // the row (16-byte aligned, k % 4 == 0, k <= NV * 4 * kThreads, 4-byte
 // aligned outputs) is loaded once as float4 into registers, NV loads in
 // flight per thread, and written four int8 at a time.  NV == 0: element-wise
-// path for every other shape.
-template <int NV>
-__global__ __launch_bounds__(kThreads) void k_quantize_rows(
+// path for every other shape.  GLU: x holds rows of 2k, [gate | up], and
+// the quantized row is their SwiGLU (what k_swiglu_rows4 writes, quantized
+// as the separate pass would quantize it).
+template <int NV, bool GLU = false, int TH = kThreads>
+__global__ __launch_bounds__(TH) void k_quantize_rows(
     const float *__restrict__ x, size_t k, size_t ld, int perm,
     int8_t *__restrict__ q_pad, int8_t *__restrict__ q_plain,
     float *__restrict__ scales) {
-    __shared__ float red[kThreads / 64];
+    __shared__ float red[TH / 64];
     const size_t r = blockIdx.x;
-    const float *row = x + r * k;
+    const float *row = x + r * (GLU ? 2 * k : k);
+    const float *urow = row + k;  // GLU: the up half
     const size_t t = threadIdx.x;
     float mx = 0.0f;
     if constexpr (NV > 0) {
         const float4 *r4 = reinterpret_cast<const float4 *>(row);
         const size_t k4 = k / 4;
         float4 v[NV];
+        if constexpr (GLU) {
+            // unconditional loads at an in-row index (no branches, so all of
+            // them are in flight at once); lanes past the row are zeroed
+            const float4 *u4 = reinterpret_cast<const float4 *>(urow);
+            float4 u[NV];
 #pragma unroll
-        for (int j = 0; j < NV; ++j) {
-            const size_t i = t + (size_t)j * kThreads;
-            v[j] = i < k4 ? r4[i] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int j = 0; j < NV; ++j) {
+                const size_t i = min(t + (size_t)j * TH, k4 - 1);
+                v[j] = r4[i];
+                u[j] = u4[i];
+            }
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                const bool in = t + (size_t)j * TH < k4;
+                v[j] = in ? float4{swiglu_elem(v[j].x, u[j].x), swiglu_elem(v[j].y, u[j].y),
+                                   swiglu_elem(v[j].z, u[j].z), swiglu_elem(v[j].w, u[j].w)}
+                          : float4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                const size_t i = t + (size_t)j * TH;
+                v[j] = i < k4 ? r4[i] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
         }
 #pragma unroll
         for (int j = 0; j < NV; ++j) mx = absmax4(mx, v[j]);
@@ -140,7 +168,7 @@ __global__ __launch_bounds__(kThreads) void k_quantize_rows(
         if (t == 0 && scales) scales[r] = scale;
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
-            const size_t kk = 4 * (t + (size_t)j * kThreads);
+            const size_t kk = 4 * (t + (size_t)j * TH);
             if (kk < k) {
                 const int packed = ((int)round_clamp_i8(v[j].x * inv) & 255) |
                                    (((int)round_clamp_i8(v[j].y * inv) & 255) << 8) |
@@ -152,10 +180,11 @@ __global__ __launch_bounds__(kThreads) void k_quantize_rows(
         }
         // zero padding of the output row
         if (q_pad)
-            for (size_t kk = k + 4 * t; kk < ld; kk += 4 * kThreads)
+            for (size_t kk = k + 4 * t; kk < ld; kk += 4 * TH)
                 *reinterpret_cast<int *>(q_pad + r * ld + row_pos(kk, perm)) = 0;
     } else {
-        for (size_t i = t; i < k; i += blockDim.x) mx = fmaxf(mx, fabsf(row[i]));
+        auto elem = [&](size_t i) { return GLU ? swiglu_elem(row[i], urow[i]) : row[i]; };
+        for (size_t i = t; i < k; i += blockDim.x) mx = fmaxf(mx, fabsf(elem(i)));
         mx = block_max(mx, red);
         const float scale = scale_of(mx);
         const float inv = __fdiv_rn(1.0f, scale);
@@ -163,7 +192,7 @@ __global__ __launch_bounds__(kThreads) void k_quantize_rows(
         for (size_t kk = t; kk < ld; kk += blockDim.x) {
             int8_t q = 0;
             if (kk < k) {
-                q = round_clamp_i8(row[kk] * inv);
+                q = round_clamp_i8(elem(kk) * inv);
                 if (q_plain) q_plain[r * k + kk] = q;
             }
             if (q_pad) q_pad[r * ld + row_pos(kk, perm)] = q;
@@ -171,24 +200,31 @@ __global__ __launch_bounds__(kThreads) void k_quantize_rows(
     }
 }
 
-// float4s per thread of the register-resident row path for k (0: none).
+// float4s per thread of the register-resident row path for k with th
+// threads per row (0: none).
 inline int rows_nv(const float *x, size_t k, size_t ld, const int8_t *q_pad,
-                   const int8_t *q_plain) {
+                   const int8_t *q_plain, size_t th = kThreads) {
     if ((k & 3) || (ld & 3) || (reinterpret_cast<uintptr_t>(x) & 15) ||
         (reinterpret_cast<uintptr_t>(q_pad) & 3) || (reinterpret_cast<uintptr_t>(q_plain) & 3))
         return 0;
-    const size_t per = (k / 4 + kThreads - 1) / kThreads;
+    const size_t per = (k / 4 + th - 1) / th;
     return per <= 4 ? 4 : per <= 8 ? 8 : per <= 16 ? 16 : 0;
 }
 
+// GLU rows (two loads per element) run 1024 threads per row: with 256 the
+// 512 rows of a prefill leave too few loads in flight (512 x 11008: 16.7 us
+// at 256 threads, 13.0 us at 1024, against 11.7 + 13.0 us for the SwiGLU
+// kernel followed by the separate pass).
+template <bool GLU>
 void launch_rows(const float *x, size_t m, size_t k, size_t ld, int perm, int8_t *q_pad,
                  int8_t *q_plain, float *scales, hipStream_t s) {
-    const dim3 grid((unsigned)m), block(kThreads);
-    switch (rows_nv(x, k, ld, q_pad, q_plain)) {
-    case 4: hipLaunchKernelGGL(k_quantize_rows<4>, grid, block, 0, s, x, k, ld, perm, q_pad, q_plain, scales); break;
-    case 8: hipLaunchKernelGGL(k_quantize_rows<8>, grid, block, 0, s, x, k, ld, perm, q_pad, q_plain, scales); break;
-    case 16: hipLaunchKernelGGL(k_quantize_rows<16>, grid, block, 0, s, x, k, ld, perm, q_pad, q_plain, scales); break;
-    default: hipLaunchKernelGGL(k_quantize_rows<0>, grid, block, 0, s, x, k, ld, perm, q_pad, q_plain, scales); break;
+    constexpr int TH = GLU ? 1024 : kThreads;
+    const dim3 grid((unsigned)m), block(TH);
+    switch (rows_nv(x, k, ld, q_pad, q_plain, TH)) {
+    case 4: hipLaunchKernelGGL((k_quantize_rows<4, GLU, TH>), grid, block, 0, s, x, k, ld, perm, q_pad, q_plain, scales); break;
+    case 8: hipLaunchKernelGGL((k_quantize_rows<8, GLU, TH>), grid, block, 0, s, x, k, ld, perm, q_pad, q_plain, scales); break;
+    case 16: hipLaunchKernelGGL((k_quantize_rows<16, GLU, TH>), grid, block, 0, s, x, k, ld, perm, q_pad, q_plain, scales); break;
+    default: hipLaunchKernelGGL((k_quantize_rows<0, GLU, TH>), grid, block, 0, s, x, k, ld, perm, q_pad, q_plain, scales); break;
     }
 }
 
@@ -486,8 +522,18 @@ mri_status launch_quantize_rows(const float *x, size_t m, size_t k,
                                 int8_t *q_pad, int8_t *q_plain,
                                 float *scales, hipStream_t s) {
     if (m == 0) return MRI_OK;
-    launch_rows(x, m, k, q_pad ? ld_out : k, q8_perm_layout ? 1 : 0, q_pad, q_plain, scales, s);
+    launch_rows<false>(x, m, k, q_pad ? ld_out : k, q8_perm_layout ? 1 : 0, q_pad, q_plain,
+                       scales, s);
     MRI_LAUNCHED("k_quantize_rows");
+    return MRI_OK;
+}
+
+mri_status launch_swiglu_quantize_rows(const float *gu, size_t m, size_t k, size_t ld_out,
+                                       bool q8_perm_layout, int8_t *q_pad, float *scales,
+                                       hipStream_t s) {
+    if (m == 0) return MRI_OK;
+    launch_rows<true>(gu, m, k, ld_out, q8_perm_layout ? 1 : 0, q_pad, nullptr, scales, s);
+    MRI_LAUNCHED("k_quantize_rows(swiglu)");
     return MRI_OK;
 }
 
@@ -495,7 +541,7 @@ mri_status launch_quantize_per_channel(const float *w, size_t n, size_t k,
                                        int8_t *data, float *scales,
                                        hipStream_t s) {
     if (n == 0) return MRI_OK;
-    launch_rows(w, n, k, k, 0, data, nullptr, scales, s);
+    launch_rows<false>(w, n, k, k, 0, data, nullptr, scales, s);
     MRI_LAUNCHED("k_quantize_rows(per_channel)");
     return MRI_OK;
 }

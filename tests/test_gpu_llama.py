@@ -117,6 +117,20 @@ def test_llama_prefill_and_decode_logits(fmt):
         close(host(one), oracle.forward_decode(toks[p], p), TOL[fmt])
 
 
+@pytest.mark.parametrize("fmt", ["q8_0", "w4a8"])
+def test_llama_prefill_wide_ffn(fmt):
+    """An FFN of 65568 (over 16384 float4 per row): the prefill rows'
+    SwiGLU and the down projection's row quantization, done in one pass,
+    take the element-wise path there instead of the register-resident one."""
+    t = torch()
+    oracle, gpu, rng = build(fmt, seed=31, d=128, nh=2, nkv=2, ffn=65568, max_seq=16,
+                             n_layers=1)
+    toks = rng.integers(0, 300, 7).tolist()
+    lg = empty((7, 300), t.float32)
+    gpu.forward_cached(toks, 0, gpu.kv_cache(), lg)
+    close(host(lg), oracle.forward_cached(toks, 0), TOL[fmt])
+
+
 def test_llama_mixed_formats():
     """A different weight format per projection role: q/k/v and gate/up
     cannot be concatenated, so decode rows run three q/k/v projections, each
