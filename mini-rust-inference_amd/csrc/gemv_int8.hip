@@ -5,6 +5,14 @@
 // segment; with S > 1 the S partial accumulators are added through LDS and
 // wave 0 of the tile applies ((f32)acc * s_a) * s_w (int8.rs:93).  Each wave
 // keeps D chunk loads in flight in a ring of registers.
+//
+// LAZY (the fused row without a quantized-row output, below 1024 tiles, or
+// below 512 with the decode step's row operations): the
+// prologue stages the f32 row in LDS and reduces max|x| without quantizing
+// it; each wave then quantizes one lap (its next D chunks, 64 D values, D/4
+// float4 a lane) into an LDS area of its own after the previous lap's MFMAs,
+// while the lap's loads are in flight.  Same scale, same rounding: the int8
+// values, int32 sums and outputs are those of the up-front quantization.
 #include "gemv_common.hpp"
 
 namespace mri {
@@ -14,12 +22,13 @@ namespace {
 // ---------------------------------------------------------------------------
 // Per-channel INT8.
 // ---------------------------------------------------------------------------
-template <int NI, int S, int TPW, int D, int XR, bool FUSED, bool OPS>
+template <int NI, int S, int TPW, int D, int XR, bool FUSED, bool OPS, bool LAZY = false>
 __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_int8(
     ActIn in, int M, int kp, const float *__restrict__ sa_ptr, int sa_stride,
     float sa_value, const v4i *__restrict__ tiles, const float *__restrict__ wscales,
     int N, int n_tiles, int P, float *__restrict__ out, int32_t *__restrict__ acc_out) {
     constexpr int NW = S * TPW;
+    static_assert(!LAZY || (FUSED && NI == 1 && D % 4 == 0), "lap-wise: the fused row");
     extern __shared__ v4i s_lds[];
     // wave index as a scalar: segment bounds and loop guards stay uniform, so
     // no MFMA ever sits under a partial EXEC mask.
@@ -37,13 +46,18 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_int8(
     const size_t pitch = (size_t)n_tiles * kWave;  // v4i per slab of chunks
     const v4i *wp = tiles + (size_t)Tc * kWave + l;
 
-    // LDS: [act M*kp][red NW floats][partials TPW x (S-1) x 64 v4i]
+    // LDS: [act M*kp, or with LAZY the f32 row (kp floats)][red NW floats]
+    // [partials TPW x (S-1) x 64 v4i][LAZY: one quantized lap (64 D bytes) per wave]
     int8_t *s_act = reinterpret_cast<int8_t *>(s_lds);
-    float *red = reinterpret_cast<float *>(s_act + (size_t)M * kp);
+    float *red = reinterpret_cast<float *>(s_act + (size_t)(LAZY ? 4 : M) * kp);
     v4i *part = reinterpret_cast<v4i *>(red + 4 * NW) + (size_t)tw_ * (S - 1) * kWave;
+    int8_t *s_lap = reinterpret_cast<int8_t *>(reinterpret_cast<v4i *>(red + 4 * NW) +
+                                               (size_t)TPW * (S - 1) * kWave) +
+                    (size_t)wl * 64 * D;
 
     const bool aval = r < M;
-    const v4i *ap = reinterpret_cast<const v4i *>(s_act + (size_t)(aval ? r : 0) * kp) + g;
+    const v4i *ap = LAZY ? reinterpret_cast<const v4i *>(s_lap) + g
+                         : reinterpret_cast<const v4i *>(s_act + (size_t)(aval ? r : 0) * kp) + g;
     const v4i zero = {0, 0, 0, 0};
     v4i acc = zero;
     v4i wr[D];
@@ -69,11 +83,36 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_int8(
         if (in.up) act_swiglu<NW, XR>(in, xr, wn);
     }
     act_begin<NW, XR, FUSED, OPS>(in, n16, xr, s_act, red);
-    act_end<NW, XR, FUSED, OPS>(in, false, xr, wn, s_act, red, sa_value, blockIdx.x == 0);
+    float inv = 0.0f;  // LAZY: 1 / scale of the row
+    if constexpr (LAZY)
+        inv = act_end_lazy<NW, XR, OPS>(in, xr, wn, reinterpret_cast<float *>(s_act), red,
+                                        sa_value, blockIdx.x == 0);
+    else
+        act_end<NW, XR, FUSED, OPS>(in, false, xr, wn, s_act, red, sa_value, blockIdx.x == 0);
     if constexpr (FUSED) sa_ptr = nullptr;
 
+    // LAZY: quantize lap L (chunks c0 + L*D ..; lane l: values 256 e + 4 l of
+    // the lap, zero past K) into this wave's area, in plain order
+    auto quant_lap = [&](int L) __attribute__((always_inline)) {
+        const float4 *xf = reinterpret_cast<const float4 *>(s_act);
+        const int base = 64 * (c0 + L * D);
+#pragma unroll
+        for (int e = 0; e < D / 4; ++e) {
+            const int kk = base + 256 * e + 4 * l;
+            float4 v = float4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (kk < in.K) v = xf[kk >> 2];
+            const int packed = (round_clamp_i8(v.x * inv) & 255) |
+                               ((round_clamp_i8(v.y * inv) & 255) << 8) |
+                               ((round_clamp_i8(v.z * inv) & 255) << 16) |
+                               (round_clamp_i8(v.w * inv) << 24);
+            *reinterpret_cast<int *>(s_lap + 256 * e + 4 * l) = packed;
+        }
+    };
+    if constexpr (LAZY) {
+        if (nc > 0) quant_lap(0);
+    }
     auto mfma = [&](int s, int i) __attribute__((always_inline)) {
-        const v4i a = aval ? ap[(size_t)(c0 + i) * 4] : zero;
+        const v4i a = aval ? ap[(size_t)(LAZY ? s : c0 + i) * 4] : zero;
         acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, wr[s], acc, 0, 0, 0);
     };
     // full laps with refills: chunk i is consumed from slot i % D, then the
@@ -86,6 +125,7 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_int8(
             mfma(s, i);
             wr[s] = __builtin_nontemporal_load(wp + (size_t)(c0 + i + D) * pitch);
         }
+        if constexpr (LAZY) quant_lap(lap + 1);  // after this lap's reads of the area
     }
     // last full lap: refill only the slots of the remaining nc % D chunks
     const int rem = nc - laps * D;
@@ -96,6 +136,9 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_int8(
             mfma(s, i);
             if (s < rem)
                 wr[s] = __builtin_nontemporal_load(wp + (size_t)(c0 + i + D) * pitch);
+        }
+        if constexpr (LAZY) {
+            if (rem > 0) quant_lap(laps);
         }
     }
 #pragma unroll
@@ -142,10 +185,12 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_int8(
 
 struct CfgI8 {
     int s = 0, tpw = 1, d = 4, xr = 0;  // s == 0: unsupported
+    bool lazy = false;                    // lap-wise quantization of the fused row
 };
 
-size_t lds_i8(int s, int tpw, size_t m, size_t kp) {
-    return m * kp + (size_t)s * tpw * 16 + (size_t)tpw * (s - 1) * kWave * 16;
+size_t lds_i8(int s, int tpw, size_t m, size_t kp, int d = 4, bool lazy = false) {
+    return (lazy ? 4 : m) * kp + (size_t)s * tpw * 16 + (size_t)tpw * (s - 1) * kWave * 16 +
+           (lazy ? (size_t)s * tpw * 64 * d : 0);
 }
 
 // Configuration by the number of 16-row tiles (measured on MI355X): about
@@ -153,7 +198,12 @@ size_t lds_i8(int s, int tpw, size_t m, size_t kp) {
 // Many tiles: one wave per tile, 8 tiles per workgroup; otherwise the K
 // split keeps enough waves.  The activation staging must fit XR pieces per
 // thread (4, 8 or 12 of 16 bytes).
-CfgI8 pick_i8(bool fused, size_t n_tiles, size_t m, size_t k, size_t kp) {
+// lazy_ok: the fused row without a quantized-row output, which then takes
+// the lap-wise quantization below 1024 tiles.  Measured on MI355X (us per
+// call, same box): 4096 -> 11008 9.0 -> 8.85, 4096 -> 4096 5.25 -> 5.04,
+// 11008 -> 4096 10.4 -> 10.1; 2-8 waves with 4-16 chunks in flight at 688
+// tiles were slower than the configuration below (8.84-10.6 us).
+CfgI8 pick_i8(bool fused, size_t n_tiles, size_t m, size_t k, size_t kp, bool lazy_ok = false) {
     CfgI8 c;
     if (n_tiles >= 1024) { c.s = 1; c.tpw = 8; c.d = 8; }
     else if (n_tiles >= 512) { c.s = 4; c.d = 4; }
@@ -163,15 +213,19 @@ CfgI8 pick_i8(bool fused, size_t n_tiles, size_t m, size_t k, size_t kp) {
     const size_t nx = ceil_div(fused ? k / 4 : m * kp / 16, threads);
     c.xr = nx <= 4 ? 4 : nx <= 8 ? 8 : nx <= 12 ? 12 : 0;
     if (c.xr == 0 || lds_i8(c.s, c.tpw, m, kp) > kMaxLds) c.s = 0;
+    if (c.s && fused && lazy_ok && m == 1 && c.tpw == 1 &&
+        lds_i8(c.s, c.tpw, m, kp, c.d, true) <= kMaxLds)
+        c.lazy = true;
     return c;
 }
 
-template <int NI, int S, int TPW, int D, int XR, bool FUSED, bool OPS>
+template <int NI, int S, int TPW, int D, int XR, bool FUSED, bool OPS, bool LAZY = false>
 void launch_i8(ActIn in, size_t m, const float *sa_ptr, int sa_stride, float sa_value,
                const QMatrixDev &w, float *out, int32_t *acc_out, hipStream_t st) {
-    hipLaunchKernelGGL((k_gemv_int8<NI, S, TPW, D, XR, FUSED, OPS>),
+    hipLaunchKernelGGL((k_gemv_int8<NI, S, TPW, D, XR, FUSED, OPS, LAZY>),
                        dim3((unsigned)ceil_div(w.n_tiles, TPW)), dim3(S * TPW * kWave),
-                       lds_i8(S, TPW, m, w.kp), st, in, (int)m, (int)w.kp, sa_ptr, sa_stride,
+                       lds_i8(S, TPW, m, w.kp, D, LAZY), st, in, (int)m, (int)w.kp, sa_ptr,
+                       sa_stride,
                        sa_value, reinterpret_cast<const v4i *>(w.tiles), w.scales,
                        (int)w.n_out, (int)w.n_tiles, (int)(w.kp / kChunkK), out, acc_out);
 }
@@ -180,6 +234,18 @@ template <int NI, bool FUSED, bool OPS = false>
 void dispatch_i8(CfgI8 c, ActIn in, size_t m, const float *sa_ptr, int sa_stride,
                  float sa_value, const QMatrixDev &w, float *out, int32_t *acc_out,
                  hipStream_t st) {
+    if constexpr (FUSED && NI == 1) {
+#define MRI_I8L(S_, D_, XR_)                                                               \
+    if (c.s == S_ && c.tpw == 1 && c.d == D_ && c.xr == XR_)                               \
+        return launch_i8<1, S_, 1, D_, XR_, true, OPS, true>(in, m, sa_ptr, sa_stride,     \
+                                                             sa_value, w, out, acc_out, st);
+        if (c.lazy) {
+            MRI_I8L(4, 4, 4) MRI_I8L(4, 4, 8) MRI_I8L(4, 4, 12)
+            MRI_I8L(4, 8, 4) MRI_I8L(4, 8, 8) MRI_I8L(4, 8, 12)
+            MRI_I8L(8, 8, 4) MRI_I8L(8, 8, 8) MRI_I8L(8, 8, 12)
+        }
+#undef MRI_I8L
+    }
 #define MRI_I8(S_, TPW_, D_, XR_)                                                          \
     if (c.s == S_ && c.tpw == TPW_ && c.d == D_ && c.xr == XR_)                            \
         return launch_i8<NI, S_, TPW_, D_, XR_, FUSED, OPS>(in, m, sa_ptr, sa_stride,      \
@@ -223,7 +289,8 @@ mri_status launch_gemv_int8(const float *x, const int8_t *act, size_t m,
                             float *scale_out, int32_t *acc_out, hipStream_t st,
                             const RowOps &ops) {
     if (w.n_tiles == 0 || m == 0) return MRI_OK;
-    const CfgI8 c = pick_i8(x != nullptr, w.n_tiles, m, w.k_in, w.kp);
+    const CfgI8 c = pick_i8(x != nullptr, w.n_tiles, m, w.k_in, w.kp,
+                            x && !act_q_out && (!ops.any() || w.n_tiles < 512));
     if (c.s == 0) return set_error(MRI_ERR_INVALID_ARGUMENT, "gemv: shape not supported");
     if (!row_ops_ok(x, ops))
         return set_error(MRI_ERR_INVALID_ARGUMENT, "gemv: row operations need the fused path");

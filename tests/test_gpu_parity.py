@@ -301,6 +301,34 @@ def test_matmul_int8_from_f32_bit_exact(m, n, k):
     assert_bits_equal(host(out), out0, "matmul_int8_from_f32 out")
 
 
+@pytest.mark.parametrize("n,k", [(11008, 4096), (4096, 4096), (4096, 11008), (8192, 1088),
+                                 (100, 96), (1000, 4160), (48, 32)])
+def test_matmul_int8_from_f32_lapwise_bit_exact(n, k):
+    """One row without the quantized-row output: below 1024 tiles the GEMV
+    quantizes the row lap by lap inside each wave (688 tiles with 4-chunk
+    laps, 256 with 8, 8 waves a tile at K = 11008, uneven segments and a
+    partial last lap at K = 1088 and 4160, K below one lap).  Outputs and
+    int32 sums bit for bit those of the oracle and of the call that also
+    returns the quantized row."""
+    say(f"matmul_int8_from_f32 lap-wise n={n} k={k}")
+    t = torch()
+    rng = np.random.default_rng(n + 7 * k)
+    wq, ws = synth_int8_weights(rng, n, k)
+    x = rng.standard_normal((1, k)).astype(F32)
+    out0, aq0, sa0, acc0 = O.matmul_int8_from_f32(x, wq, ws)
+    w = mri().QMatrix.from_host(wq, ws)
+    out, acc = empty((1, n), t.float32), empty((1, n), t.int32)
+    mri().matmul_int8_from_f32(dev(x), w, out, None, None, acc)
+    assert np.array_equal(host(acc), acc0)
+    assert_bits_equal(host(out), out0, "matmul_int8_from_f32 lap-wise out")
+    out2 = empty((1, n), t.float32)
+    mri().matmul_int8_from_f32(dev(x), w, out2)
+    assert_bits_equal(host(out2), out0, "matmul_int8_from_f32 lap-wise out (no acc)")
+    out3, aq, sa = empty((1, n), t.float32), empty((1, k), t.int8), empty(1, t.float32)
+    mri().matmul_int8_from_f32(dev(x), w, out3, aq, sa)
+    assert_bits_equal(host(out3), host(out), "up-front vs lap-wise")
+
+
 # ---- Q8_0 --------------------------------------------------------------------------
 
 Q8_SHAPES = [
