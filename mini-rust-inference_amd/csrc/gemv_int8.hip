@@ -6,8 +6,7 @@
 // wave 0 of the tile applies ((f32)acc * s_a) * s_w (int8.rs:93).  Each wave
 // keeps D chunk loads in flight in a ring of registers.
 //
-// LAZY (the fused row without a quantized-row output, below 1024 tiles, or
-// below 512 with the decode step's row operations): the
+// LAZY (the fused row without a quantized-row output, below 1024 tiles): the
 // prologue stages the f32 row in LDS and reduces max|x| without quantizing
 // it; each wave then quantizes one lap (its next D chunks, 64 D values, D/4
 // float4 a lane) into an LDS area of its own after the previous lap's MFMAs,
@@ -199,10 +198,12 @@ size_t lds_i8(int s, int tpw, size_t m, size_t kp, int d = 4, bool lazy = false)
 // split keeps enough waves.  The activation staging must fit XR pieces per
 // thread (4, 8 or 12 of 16 bytes).
 // lazy_ok: the fused row without a quantized-row output, which then takes
-// the lap-wise quantization below 1024 tiles.  Measured on MI355X (us per
-// call, same box): 4096 -> 11008 9.0 -> 8.85, 4096 -> 4096 5.25 -> 5.04,
-// 11008 -> 4096 10.4 -> 10.1; 2-8 waves with 4-16 chunks in flight at 688
-// tiles were slower than the configuration below (8.84-10.6 us).
+// the lap-wise quantization below 1024 tiles (with or without the decode
+// step's row operations).  Measured on MI355X (us per call, same box):
+// 4096 -> 11008 9.0 -> 8.85, 4096 -> 4096 5.25 -> 5.04, 11008 -> 4096
+// 10.4 -> 10.1; 2-8 waves with 4-16 chunks in flight at 688 tiles were
+// slower than the configuration below (8.84-10.6 us).  In the INT8 layer's
+// decode step (o, down and the 768-tile q/k/v): 83.7 -> 83.05 us per token.
 CfgI8 pick_i8(bool fused, size_t n_tiles, size_t m, size_t k, size_t kp, bool lazy_ok = false) {
     CfgI8 c;
     if (n_tiles >= 1024) { c.s = 1; c.tpw = 8; c.d = 8; }
@@ -290,7 +291,7 @@ mri_status launch_gemv_int8(const float *x, const int8_t *act, size_t m,
                             const RowOps &ops) {
     if (w.n_tiles == 0 || m == 0) return MRI_OK;
     const CfgI8 c = pick_i8(x != nullptr, w.n_tiles, m, w.k_in, w.kp,
-                            x && !act_q_out && (!ops.any() || w.n_tiles < 512));
+                            x && !act_q_out);
     if (c.s == 0) return set_error(MRI_ERR_INVALID_ARGUMENT, "gemv: shape not supported");
     if (!row_ops_ok(x, ops))
         return set_error(MRI_ERR_INVALID_ARGUMENT, "gemv: row operations need the fused path");
