@@ -38,6 +38,7 @@ namespace mri {
 namespace gemv {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
 
 constexpr int kWave = 64;
 constexpr int kMaxM = 4;
@@ -70,6 +71,44 @@ __device__ inline int round_clamp_i8(float y) {
     if (r != r) return 0;             // `NaN as i8` == 0
     r = fminf(fmaxf(r, -127.0f), 127.0f);
     return (int)r;
+}
+
+// The same map in six instructions: round(y), ties away from zero, is
+// trunc(y + copysign(0.5 - 2^-25, y)) for every f32 that is not NaN (the
+// sum rounds up to the next integer exactly when the fraction is >= 1/2;
+// checked over all 2^32 bit patterns); v_cvt_i32_f32 saturates and maps NaN
+// to 0, so the clamp to [-127, 127] is an integer med3.
+__device__ inline int cvt_i32_sat(float r) {
+    int v;
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(v) : "v"(r));
+    return v;
+}
+__device__ inline int quant_i8(float y) {
+    const float r = __builtin_truncf(y + __builtin_copysignf(0.49999997f, y));
+    return min(max(cvt_i32_sat(r), -127), 127);
+}
+// Four values times inv, quantized as quant_i8 and packed little-endian.
+__device__ inline int quant4_packed(float4 v, float inv) {
+    const unsigned q0 = (unsigned)quant_i8(v.x * inv), q1 = (unsigned)quant_i8(v.y * inv);
+    const unsigned q2 = (unsigned)quant_i8(v.z * inv), q3 = (unsigned)quant_i8(v.w * inv);
+    // v_perm_b32: selector bytes 0-3 pick bytes of the second operand, 4-7
+    // of the first, 0x0c gives zero
+    const unsigned lo = __builtin_amdgcn_perm(q1, q0, 0x0c0c0400u);
+    const unsigned hi = __builtin_amdgcn_perm(q3, q2, 0x04000c0cu);
+    return (int)(lo | hi);
+}
+
+// Masked row layout of a one-row Q8_0 MFMA operand (the kernels' chained
+// form): lap q of the row is a 512-byte area of 32 entries of 16 bytes;
+// entry (2s + h) + 8g holds the 8 bytes of lane group g of block 2s + h of
+// the lap's chunk s (elements 8g .. 8g + 7 of that block) in bytes 8h .. 8h
+// + 7 and zeros in the other half, so that lane (r = 2s + h, g) of the
+// chunk's MFMA reads row r of the A operand in one 16-byte load.
+// Byte offset of the data word of elements kk .. kk + 3 (kk % 4 == 0); the
+// zero word that goes with it is at offset ^ 8.
+__device__ inline int masked_off(int kk) {
+    const int e = kk & 63, s = (kk >> 6) & 3, h = e >> 5, g = (e >> 3) & 3;
+    return (kk >> 8) * 512 + 16 * (2 * s + h + 8 * g) + 8 * h + (e & 4);
 }
 
 // Calls f(std::integral_constant<int, I>) for I = 0 .. N-1 (compile-time
@@ -233,7 +272,9 @@ __device__ inline float wave_sum_f(float v) {
     return v;
 }
 
-template <int S, int XR, bool FUSED, bool OPS>
+// MASKED: the int8 rows (one row) are copied into the masked layout instead
+// (piece i, lane group i % 4 of chunk i / 4, goes to its two entries).
+template <int S, int XR, bool FUSED, bool OPS, bool MASKED = false>
 __device__ inline void act_begin(const ActIn &in, int n16, const v4i (&xr)[XR], int8_t *s_act,
                                  float *red) {
     const int t = threadIdx.x;
@@ -277,7 +318,15 @@ __device__ inline void act_begin(const ActIn &in, int n16, const v4i (&xr)[XR], 
 #pragma unroll
         for (int e = 0; e < XR; ++e) {
             const int i = t + S * kWave * e;
-            if (i < n16) dst[i] = xr[e];
+            if (i < n16) {
+                if constexpr (MASKED) {
+                    const int ent = (i >> 4) * 32 + 2 * ((i >> 2) & 3) + 8 * (i & 3);
+                    dst[ent] = v4i{xr[e].x, xr[e].y, 0, 0};
+                    dst[ent + 1] = v4i{0, 0, xr[e].z, xr[e].w};
+                } else {
+                    dst[i] = xr[e];
+                }
+            }
         }
     }
     // keep the uses above after the weight loads issued before them
@@ -285,8 +334,12 @@ __device__ inline void act_begin(const ActIn &in, int n16, const v4i (&xr)[XR], 
 }
 
 // wn: the norm weight pieces staged like xr (used when in.norm_w).
+// layout: kLayPlain (element kk at byte kk), kLayPerm (chunk-permuted,
+// q8_perm) or kLayMasked (masked_off, with the zero word beside each data
+// word).
+enum : int { kLayPlain = 0, kLayPerm = 1, kLayMasked = 2 };
 template <int S, int XR, bool FUSED, bool OPS>
-__device__ inline void act_end(const ActIn &in, bool perm, v4i (&xr)[XR], const v4i (&wn)[XR],
+__device__ inline void act_end(const ActIn &in, int layout, v4i (&xr)[XR], const v4i (&wn)[XR],
                                int8_t *s_act, float *red, float &scale, bool writer) {
     __syncthreads();
     if constexpr (FUSED) {
@@ -333,10 +386,13 @@ __device__ inline void act_end(const ActIn &in, bool perm, v4i (&xr)[XR], const 
                 const int q2 = round_clamp_i8(v.z * inv);
                 const int q3 = round_clamp_i8(v.w * inv);
                 const int kk = 4 * j;
-                const int pos = perm ? (kk & ~63) + q8_perm(kk & 63) : kk;
+                const int pos = layout == kLayMasked ? masked_off(kk)
+                                : layout == kLayPerm ? (kk & ~63) + q8_perm(kk & 63)
+                                                     : kk;
                 const int packed =
                     (q0 & 255) | ((q1 & 255) << 8) | ((q2 & 255) << 16) | (q3 << 24);
                 *reinterpret_cast<int *>(s_act + pos) = packed;
+                if (layout == kLayMasked) *reinterpret_cast<int *>(s_act + (pos ^ 8)) = 0;
                 if (writer && in.act_q_out)
                     *reinterpret_cast<int *>(in.act_q_out + kk) = packed;
             }

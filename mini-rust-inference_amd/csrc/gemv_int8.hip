@@ -46,7 +46,8 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_int8(
     const v4i *wp = tiles + (size_t)Tc * kWave + l;
 
     // LDS: [act M*kp, or with LAZY the f32 row (kp floats)][red NW floats]
-    // [partials TPW x (S-1) x 64 v4i][LAZY: one quantized lap (64 D bytes) per wave]
+    // [partials TPW x (S-1) x 64 v4i][LAZY: one quantized lap (64 D bytes) per
+    // wave, then 64 D bytes of zeros that the lanes of rows >= M read]
     int8_t *s_act = reinterpret_cast<int8_t *>(s_lds);
     float *red = reinterpret_cast<float *>(s_act + (size_t)(LAZY ? 4 : M) * kp);
     v4i *part = reinterpret_cast<v4i *>(red + 4 * NW) + (size_t)tw_ * (S - 1) * kWave;
@@ -55,7 +56,8 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_int8(
                     (size_t)wl * 64 * D;
 
     const bool aval = r < M;
-    const v4i *ap = LAZY ? reinterpret_cast<const v4i *>(s_lap) + g
+    int8_t *s_zero = s_lap + (size_t)(NW - wl) * 64 * D;  // LAZY
+    const v4i *ap = LAZY ? reinterpret_cast<const v4i *>(aval ? s_lap : s_zero) + g
                          : reinterpret_cast<const v4i *>(s_act + (size_t)(aval ? r : 0) * kp) + g;
     const v4i zero = {0, 0, 0, 0};
     v4i acc = zero;
@@ -81,13 +83,16 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_int8(
     if constexpr (FUSED && OPS) {
         if (in.up) act_swiglu<NW, XR>(in, xr, wn);
     }
+    if constexpr (LAZY) {  // the zero area (the prologue's barrier orders it)
+        if ((int)threadIdx.x < 4 * D) reinterpret_cast<v4i *>(s_zero)[threadIdx.x] = zero;
+    }
     act_begin<NW, XR, FUSED, OPS>(in, n16, xr, s_act, red);
     float inv = 0.0f;  // LAZY: 1 / scale of the row
     if constexpr (LAZY)
         inv = act_end_lazy<NW, XR, OPS>(in, xr, wn, reinterpret_cast<float *>(s_act), red,
                                         sa_value, blockIdx.x == 0);
     else
-        act_end<NW, XR, FUSED, OPS>(in, false, xr, wn, s_act, red, sa_value, blockIdx.x == 0);
+        act_end<NW, XR, FUSED, OPS>(in, kLayPlain, xr, wn, s_act, red, sa_value, blockIdx.x == 0);
     if constexpr (FUSED) sa_ptr = nullptr;
 
     // LAZY: quantize lap L (chunks c0 + L*D ..; lane l: values 256 e + 4 l of
@@ -100,18 +105,14 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_int8(
             const int kk = base + 256 * e + 4 * l;
             float4 v = float4{0.0f, 0.0f, 0.0f, 0.0f};
             if (kk < in.K) v = xf[kk >> 2];
-            const int packed = (round_clamp_i8(v.x * inv) & 255) |
-                               ((round_clamp_i8(v.y * inv) & 255) << 8) |
-                               ((round_clamp_i8(v.z * inv) & 255) << 16) |
-                               (round_clamp_i8(v.w * inv) << 24);
-            *reinterpret_cast<int *>(s_lap + 256 * e + 4 * l) = packed;
+            *reinterpret_cast<int *>(s_lap + 256 * e + 4 * l) = quant4_packed(v, inv);
         }
     };
     if constexpr (LAZY) {
         if (nc > 0) quant_lap(0);
     }
     auto mfma = [&](int s, int i) __attribute__((always_inline)) {
-        const v4i a = aval ? ap[(size_t)(LAZY ? s : c0 + i) * 4] : zero;
+        const v4i a = LAZY ? ap[s * 4] : aval ? ap[(size_t)(c0 + i) * 4] : zero;
         acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, wr[s], acc, 0, 0, 0);
     };
     // full laps with refills: chunk i is consumed from slot i % D, then the
@@ -189,7 +190,7 @@ struct CfgI8 {
 
 size_t lds_i8(int s, int tpw, size_t m, size_t kp, int d = 4, bool lazy = false) {
     return (lazy ? 4 : m) * kp + (size_t)s * tpw * 16 + (size_t)tpw * (s - 1) * kWave * 16 +
-           (lazy ? (size_t)s * tpw * 64 * d : 0);
+           (lazy ? (size_t)(s * tpw + 1) * 64 * d : 0);
 }
 
 // Configuration by the number of 16-row tiles (measured on MI355X): about

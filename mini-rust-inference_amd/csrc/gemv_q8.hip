@@ -18,6 +18,18 @@ namespace {
 // channel n = 16T + l%16.  MR (1, 2 or 4: rows of the instance) fixes how
 // many lane groups hold results.
 //
+// One row (MR = 1, the chained form): chunk s of a lap fills rows 2s and
+// 2s + 1 of its MFMA's A operand (blocks 2s, 2s + 1) and leaves the other
+// rows zero, so the lap's four MFMAs accumulate into one result: lane
+// (r, g < 2) holds blocks 4g .. 4g + 3 of the lap for channel r, and each
+// lane folds four terms per lap instead of eight terms of which three
+// quarters belong to zero rows.  The A operand comes from the masked row
+// layout (masked_off), where each lane's 16 bytes are one load with the
+// other block's half already zero; lanes without a row in a chunk read a
+// zero line.  The accumulator starts at kDotBias, so the block dots read
+// as f32 with one subtraction.  The two lane groups' sums are added after
+// the sweep.
+//
 // A workgroup holds TPW tiles of S waves each; its waves share the
 // activation staging.  A tile's K is swept in laps of one scale group
 // (4 chunks = 8 blocks) dealt out round-robin: in round R wave w takes lap
@@ -35,7 +47,7 @@ namespace {
 // LAZY (the plain fused row, 512-1023 tiles): the prologue stages the f32
 // row in LDS and reduces max|x| (one barrier) without quantizing it; each
 // wave then quantizes only the laps it consumes, one lap (4 values a lane,
-// the same round-half-away and clamp) into a 256-byte area of its own,
+// the same round-half-away and clamp) into a masked 512-byte area of its own,
 // after the previous lap's MFMAs and refills, while the next lap is in
 // flight.  Every workgroup re-quantizes the row it uses; quantizing it all
 // up front put that VALU work ahead of every wave's first lap.
@@ -63,7 +75,8 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     // [1,4096]x[4096,11008] on two boxes, 2 % at K = 992, same outputs);
     // with two laps in flight the compiler indexed
     // the pieces through scratch memory and the kernels ran 33-50 % slower,
-    // so those stage the row in LDS
+    // so those stage the row in LDS (a fully unrolled lap sequence, which
+    // indexes the pieces statically, ran 10.3 against 9.05 us)
     constexpr bool kRegRow = LAZY && !OPS && RL == 1 && XR <= 4;
     static_assert(!kRegRow || TPW == 1, "registers hold this wave's laps only with one tile");
     extern __shared__ v4i s_lds[];
@@ -82,17 +95,26 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     constexpr int SO = W4 ? 128 : 256;
     constexpr int NP = W4 ? 2 : 4;            // quant pieces per lap and lane
     const v4i *wp = laps + (size_t)Tc * G * LB + l;
-    const v4i *sp = laps + (size_t)Tc * G * LB + SO + r;
     const int n = T * 16 + r;
+    // CH: one row; the four MFMAs of a lap accumulate into one result
+    // (scale loads: the 4 f16 scales of blocks 4(g%2) .. + 3 of channel r)
+    constexpr bool CH = MR == 1;
+    using SR = std::conditional_t<CH, v2i, v4i>;
+    const SR *sp = reinterpret_cast<const SR *>(laps + (size_t)Tc * G * LB + SO + r) +
+                   (CH ? (g & 1) : 0);
+    constexpr size_t LBS = CH ? 2 * LB : LB;  // lap stride in SR units
 
-    // LDS: [act M*kp int8, or with LAZY the f32 row (kp floats)][red NW
-    // floats][wave sums TPW x (S-1) x LG x 16 x LR floats][LAZY: one
-    // quantized lap (256 bytes) per wave]
+    // LDS: [act: M*kp int8; CH: the masked row (2*kp bytes) and a 16-byte
+    // zero line; LAZY: the f32 row (kp floats)][red NW floats][wave sums TPW
+    // x (S-1) x LG x 16 x LR floats][LAZY: one masked lap (512 bytes) and a
+    // zero line per wave]
+    constexpr int kLapArea = 528;
     int8_t *s_act = reinterpret_cast<int8_t *>(s_lds);
-    float *red = reinterpret_cast<float *>(s_act + (size_t)(LAZY ? 4 : M) * kp);
+    float *red = reinterpret_cast<float *>(
+        s_act + (LAZY ? (size_t)4 * kp : CH ? (size_t)2 * kp + 16 : (size_t)M * kp));
     float *sums = red + 4 * NW;
     int8_t *s_lap = reinterpret_cast<int8_t *>(sums + (size_t)TPW * (S - 1) * LG * 16 * LR) +
-                    (size_t)wl * 256;
+                    (size_t)wl * kLapArea;
     auto sslot = [&](int ww) {  // sums of wave ww >= 1 of this tile, this lane
         return sums + ((((size_t)tw_ * (S - 1) + (ww - 1)) * LG + (g < LG ? g : 0)) * 16 + r) * LR;
     };
@@ -104,9 +126,15 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     const int mlo = (aval && !(r & 1)) ? -1 : 0;
     const int mhi = (aval && (r & 1)) ? -1 : 0;
     const v4i *ap = reinterpret_cast<const v4i *>(LAZY ? s_lap : s_act + (size_t)(aval ? arow : 0) * kp) + g;
+    // CH: lane (r, g), r < 8, feeds row r of chunk r/2's MFMA from entry
+    // r + 8g of the lap's masked area; every other (lane, MFMA) pair reads
+    // the zero line.
+    const int own_s = r < 8 ? r >> 1 : -1;
+    const int8_t *a_ent = (LAZY ? s_lap : s_act) + 16 * (r + 8 * g);
+    const int8_t *a_zero = LAZY ? s_lap + 512 : s_act + 2 * (size_t)kp;
 
     v4i wr[RL][4];
-    v4i sr[RL];
+    SR sr[RL];
     v4i xr[XR];
     const int n16 = FUSED ? in.K / 4 : M * kp / 16;
     const float *xrow = in.x;
@@ -138,7 +166,15 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
 #pragma unroll
         for (int s = 0; s < NP; ++s)
             wr[u][s] = __builtin_nontemporal_load(wp + (size_t)q * LB + s * 64);
-        sr[u] = sp[(size_t)q * LB];
+        sr[u] = sp[(size_t)q * LBS];
+    }
+    if constexpr (CH) {  // zero words of the masked areas, the zero line
+        if constexpr (LAZY) {
+            *reinterpret_cast<int *>(s_lap + (masked_off(4 * l) ^ 8)) = 0;
+            if (l < 4) reinterpret_cast<int *>(s_lap + 512)[l] = 0;
+        } else {
+            if (threadIdx.x < 4) reinterpret_cast<int *>(s_act + 2 * (size_t)kp)[threadIdx.x] = 0;
+        }
     }
     if constexpr (FUSED && OPS) {
         if (in.up) act_swiglu<NW, XR>(in, xr, wn);
@@ -152,8 +188,9 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
         inv = act_end_lazy<NW, XR, OPS, !kRegRow>(in, xr, wn, reinterpret_cast<float *>(s_act),
                                                   red, sa[0], blockIdx.x == 0);
     } else {
-        act_begin<NW, XR, FUSED, OPS>(in, n16, xr, s_act, red);
-        act_end<NW, XR, FUSED, OPS>(in, true, xr, wn, s_act, red, sa[0], blockIdx.x == 0);
+        act_begin<NW, XR, FUSED, OPS, CH>(in, n16, xr, s_act, red);
+        act_end<NW, XR, FUSED, OPS>(in, CH ? kLayMasked : kLayPerm, xr, wn, s_act, red, sa[0],
+                                    blockIdx.x == 0);
     }
     // LAZY: quantize lap q = L * S + w of the row (lane l: elements
     // 256q + 4l .. + 3, zero past K) into this wave's 256-byte area,
@@ -172,9 +209,9 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
         } else {
             if (kk < in.K) v = reinterpret_cast<const float4 *>(s_act)[kk >> 2];
         }
-        const int packed = (round_clamp_i8(v.x * inv) & 255) | ((round_clamp_i8(v.y * inv) & 255) << 8) |
-                           ((round_clamp_i8(v.z * inv) & 255) << 16) | (round_clamp_i8(v.w * inv) << 24);
-        *reinterpret_cast<int *>(s_lap + ((4 * l) & ~63) + q8_perm((4 * l) & 63)) = packed;
+        // the data word of elements 4l .. 4l + 3 of the lap (its zero word
+        // was written once)
+        *reinterpret_cast<int *>(s_lap + masked_off(4 * l)) = quant4_packed(v, inv);
     };
     if constexpr (LAZY) {
         if (nq > 0) quant_lap(0);
@@ -189,6 +226,60 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     auto lap = [&](int L, auto slot, bool refill, auto check) __attribute__((always_inline)) {
         constexpr int U = decltype(slot)::value;
         const int q = L * S + w;
+        if constexpr (CH) {
+            // rows 2s, 2s + 1 of MFMA s are blocks 2s, 2s + 1 of the lap and
+            // its other rows are zero, so one accumulator collects the lap:
+            // lane (r, g < 2) ends with blocks 4g .. 4g + 3 of channel r in
+            // registers 0-3, each as the bits of kDotBiasF + dot
+            const int8_t *ent = a_ent + (LAZY ? 0 : (size_t)512 * q);
+            v4i a[4];
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+                a[s] = *reinterpret_cast<const v4i *>(s == own_s ? ent : a_zero);
+            v4i c = v4i{kDotBias, kDotBias, kDotBias, kDotBias};
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                v4i bw;
+                if constexpr (W4) {
+                    const v4i pc = wr[U][s >> 1];
+                    const int w0 = (s & 1) ? pc.z : pc.x, w1 = (s & 1) ? pc.w : pc.y;
+                    constexpr int kHi = (int)0xF0F0F0F0u;
+                    bw = v4i{(w0 << 4) & kHi, w0 & kHi, (w1 << 4) & kHi, w1 & kHi};
+                } else {
+                    bw = wr[U][s];
+                }
+                c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[s], bw, c, 0, 0, 0);
+                if (refill && (!W4 || (s & 1))) {
+                    const int pi = W4 ? s >> 1 : s;
+                    wr[U][pi] = __builtin_nontemporal_load(wp + (size_t)(q + RL * S) * LB + pi * 64);
+                }
+            }
+            // t_b = ((f32)dot_b * s_a) * d_b (q8_direct.rs:281), in block order
+            // per lane (W4: the MFMA holds 16 * dot, and (f32)(16 dot) / 16 is
+            // exact)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                // (a copy first: __builtin_bit_cast of the element expression
+                // c[i] read element 0 for every i)
+                const int ci = c[i];
+                float dv = __builtin_bit_cast(float, ci) - kDotBiasF;
+                if constexpr (W4) dv = dv * 0.0625f;
+                const unsigned word = (unsigned)sr[U][i >> 1];
+                const float d = f16_bits_to_f32((i & 1) ? (word >> 16) : (word & 0xFFFFu));
+                float t = dv * sa[0];
+                t = t * d;
+                if (!decltype(check)::value || 8 * q + 4 * g + i < nb) fs[0] = fs[0] + t;
+            }
+            if constexpr (DEBUG) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int b = 8 * q + 4 * g + i;
+                    if (b < nb && g < 2 && n < N)
+                        block_dots[(size_t)n * nb + b] =
+                            W4 ? (c[i] - kDotBias) >> 4 : c[i] - kDotBias;
+                }
+            }
+        } else {
         v4i a[4];
 #pragma unroll
         for (int s = 0; s < 4; ++s) a[s] = ap[(size_t)((LAZY ? 0 : 4 * q) + s) * 4];
@@ -250,7 +341,8 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
                 }
             }
         }
-        if (refill) sr[U] = sp[(size_t)(q + RL * S) * LB];
+        }
+        if (refill) sr[U] = sp[(size_t)(q + RL * S) * LBS];
         if constexpr (LAZY) {
             if (L + 1 < nq) quant_lap(L + 1);  // while the next laps are in flight
         }
@@ -271,6 +363,8 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
             if (u < rem) lap(k * RL + u, u, false, T1{});
         });
     }
+    // CH: lane group 1 holds blocks 4-7 of every lap
+    if constexpr (CH) fs[0] = fs[0] + __shfl_xor(fs[0], 16);
     // the wave sums of the tile, added in wave order
     if constexpr (S > 1) {
         if (w != 0 && g < LG) {
@@ -468,8 +562,9 @@ size_t lds_q8(int s, int tpw, size_t m, size_t kp, size_t G, bool lazy = false) 
     (void)G;
     const size_t mr = (size_t)mr_of(m);
     const size_t lr = mr == 1 ? 1 : 2, lg = (mr + 1) / 2;
-    return (lazy ? 4 : m) * kp + (size_t)s * tpw * 16 + (size_t)tpw * (s - 1) * lg * 16 * lr * 4 +
-           (lazy ? (size_t)s * tpw * 256 : 0);
+    const size_t act = lazy ? 4 * kp : mr == 1 ? 2 * kp + 16 : m * kp;
+    return act + (size_t)s * tpw * 16 + (size_t)tpw * (s - 1) * lg * 16 * lr * 4 +
+           (lazy ? (size_t)s * tpw * 528 : 0);
 }
 
 // Activation pieces per thread of the instances with S waves per tile.
