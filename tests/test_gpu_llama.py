@@ -117,6 +117,28 @@ def test_llama_prefill_and_decode_logits(fmt):
         close(host(one), oracle.forward_decode(toks[p], p), TOL[fmt])
 
 
+def test_llama_decode_split_keys_head_dim_64():
+    """Decode past 128 keys at head_dim 64 with two query heads per KV head:
+    the decode attention then splits each head's keys over 64-key
+    workgroups (four key rows per wave load instruction at this head size)
+    and the last workgroup of a head combines them, including a partial
+    last chunk.  Teacher-forced decode steps at contexts 151-196 keys
+    against the oracle; Q4_0 weights quantize no activation, so the
+    tolerance is f32 rounding (a lost, doubled or misplaced key moves the
+    logits by far more)."""
+    t = torch()
+    oracle, gpu, rng = build("q4_0", seed=41, d=256, nh=4, nkv=2, max_seq=200, n_layers=1)
+    toks = rng.integers(0, 300, 196).tolist()
+    cache = gpu.kv_cache()
+    lg = empty((150, 300), t.float32)
+    gpu.forward_cached(toks[:150], 0, cache, lg)
+    close(host(lg), oracle.forward_cached(toks[:150], 0), TOL["q4_0"])
+    one = empty((300,), t.float32)
+    for p in range(150, 196):
+        gpu.forward_decode(toks[p], p, cache, one)
+        close(host(one), oracle.forward_decode(toks[p], p), TOL["q4_0"])
+
+
 @pytest.mark.parametrize("fmt", ["q8_0", "w4a8"])
 def test_llama_prefill_wide_ffn(fmt):
     """An FFN of 65568 (over 16384 float4 per row): the prefill rows'
