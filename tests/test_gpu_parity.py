@@ -329,6 +329,62 @@ def test_matmul_int8_from_f32_lapwise_bit_exact(n, k):
     assert_bits_equal(host(out3), host(out), "up-front vs lap-wise")
 
 
+def special_row(rng, k, top=127.0, nan=True, inf=False):
+    """A row whose values land on the quantizer's edge cases: with max|x| =
+    127 the scale is exactly 1, so every half-integer is a tie (rounded away
+    from zero), 0.49999997 is just below one, 126.5 and -127 sit at the
+    clamp; NaN elements quantize to 0 and leave the max alone; an infinite
+    element makes the scale infinite (every value then quantizes to 0)."""
+    vals = np.array([0.5, -0.5, 1.5, -1.5, 2.5, -2.5, 62.5, -62.5, 126.5, -126.5, 0.49999997,
+                     -0.49999997, 0.0, -0.0, 3.0, -127.0], F32)
+    x = vals[rng.integers(0, vals.size, k)] * F32(top / 127.0)
+    x[rng.integers(0, k)] = top
+    if nan:
+        x[rng.integers(0, k, 3)] = np.nan
+    if inf:
+        x[rng.integers(0, k)] = np.inf
+    return x.reshape(1, k)
+
+
+@pytest.mark.parametrize("n,k", [(11008, 4096), (4096, 4096), (32000, 4096), (8200, 992),
+                                 (48, 4096)])
+@pytest.mark.parametrize("case", ["ties", "ties_scaled", "inf"])
+def test_fused_row_quantizer_edge_values(n, k, case):
+    """The decode GEMVs quantize their f32 row themselves (lap by lap inside
+    each wave below 1024 tiles, up front above; Q8_0 into the masked operand
+    layout, INT8 into its lap area).  At ties, values just below one, the
+    clamp, NaN and infinite elements their quantized values must be
+    quantize_symmetric's (symmetric.rs:42-57): Q8_0 block dots and scale and
+    INT8 int32 sums bit for bit the oracle's."""
+    say(f"fused row quantizer n={n} k={k} {case}")
+    t = torch()
+    rng = np.random.default_rng(n + k + len(case))
+    x = special_row(rng, k, top=127.0 if case != "ties_scaled" else 3.75,
+                    inf=case == "inf")
+    raw = synth_q8_0(rng, n, k)
+    out0, bd0, sa0 = O.matmul_q8_0_direct(x, raw, n, k, want_block_dots=True)
+    w = mri().Q8Matrix.from_raw_bytes(raw, n, k)
+    out, bd, sa = empty((1, n), t.float32), empty((1, n, k // 32), t.int32), empty(1, t.float32)
+    mri().matmul_q8_0_direct(dev(x), w, out, bd, sa)
+    assert np.array_equal(bits(host(sa)), bits(sa0))
+    assert np.array_equal(host(bd), bd0)
+    if case == "inf":
+        assert np.isinf(sa0[0]) and not bd0.any()
+        assert np.array_equal(np.isnan(host(out)), np.isnan(out0))
+    else:
+        q8_check(host(out), out0, bd0, sa0, raw, n, k, "q8_0 out", exact=False)
+    wq, ws = synth_int8_weights(rng, n, k)
+    iout0, _, _, acc0 = O.matmul_int8_from_f32(x, wq, ws)
+    wi = mri().QMatrix.from_host(wq, ws)
+    iout, acc = empty((1, n), t.float32), empty((1, n), t.int32)
+    mri().matmul_int8_from_f32(dev(x), wi, iout, None, None, acc)
+    assert np.array_equal(host(acc), acc0)
+    if case == "inf":  # 0 * inf: NaN on both sides (the payload may differ)
+        assert np.array_equal(np.isnan(host(iout)), np.isnan(iout0))
+    else:
+        assert_bits_equal(host(iout), iout0, "int8 out")
+
+
 # ---- Q8_0 --------------------------------------------------------------------------
 
 Q8_SHAPES = [
