@@ -433,7 +433,7 @@ __global__ __launch_bounds__(256) void k_attn_decode_part(
     constexpr int R4 = HD / 4, KPI = kWave / R4, NI = 16 / KPI;
     static_assert(HD % 64 == 0 && HD <= 256, "head dim");
     __shared__ float s_s[64];
-    __shared__ float s_o[4][HD];
+    __shared__ __attribute__((aligned(16))) float s_o[4][HD];  // written as float4
     __shared__ int s_last;
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     const int sub = lane / R4, d4 = lane % R4;
