@@ -235,7 +235,7 @@ __global__ __launch_bounds__(256) void k_attention(
     constexpr int KT = 64;         // keys per tile
     constexpr int P4 = HD / 4;     // float4 per key row
     static_assert(QB % 4 == 0, "query block");
-    extern __shared__ float s_mem[];
+    extern __shared__ __attribute__((aligned(16))) float s_mem[];  // read and written as float4
     float *s_q = s_mem;                          // [QB][HD]
     float *s_t = s_q + QB * HD;                  // tile
     float *s_p = s_t + attn_tile_floats<HD>();   // [QB][lcap]
