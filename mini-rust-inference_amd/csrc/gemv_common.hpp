@@ -195,20 +195,40 @@ __device__ inline const float *row_of_keys(const ActIn &in) {
     return in.x + (size_t)tok * in.K;
 }
 
+// The destination of output channel n of the row operations, its old value
+// (for the residual add) and its RoPE factors, loaded when the kernel
+// starts, so that the epilogue waits for no load of its own (a dependent
+// round trip at the end of every decode-step projection otherwise).  n is
+// clamped: a lane past N loads an element it never stores.
+struct RowDst {
+    float *o;
+    float base = 0.0f, c = 1.0f, s = 0.0f;
+};
+__device__ inline RowDst row_dst(const ActIn &in, float *out, int n, int N) {
+    const int nc = min(n, N - 1);
+    RowDst d;
+    d.o = nc >= in.seg2 ? in.out2 + (nc - in.seg2)
+        : nc >= in.seg1 ? in.out1 + (nc - in.seg1)
+                        : out + nc;
+    if (in.accum) d.base = *d.o;
+    if (in.rope_n > 0) {
+        const int i = (nc % in.hd) >> 1;
+        d.c = in.rope_cos[i];
+        d.s = in.rope_sin[i];
+    }
+    return d;
+}
+
 // Epilogue of the row operations for output channel n of the row with value
 // v, where pv is the value of channel n ^ 1: RoPE below rope_n, as
 // rope_apply computes it (out[2i] = x0*c - x1*s, out[2i+1] = x1*c + x0*s),
 // then the store by output segment, or the residual accumulate.
-__device__ inline void row_store(const ActIn &in, float *out, int n, float v, float pv) {
+__device__ inline void row_store(const ActIn &in, const RowDst &d, int n, float v, float pv) {
     if (n < in.rope_n) {
-        const int i = (n % in.hd) >> 1;
-        const float a = v * in.rope_cos[i], b = pv * in.rope_sin[i];
+        const float a = v * d.c, b = pv * d.s;
         v = (n & 1) ? a + b : a - b;
     }
-    float *o = n >= in.seg2 ? in.out2 + (n - in.seg2)
-             : n >= in.seg1 ? in.out1 + (n - in.seg1)
-                            : out + n;
-    *o = in.accum ? *o + v : v;
+    *d.o = in.accum ? d.base + v : v;
 }
 
 // Greedy argmax keys in the epilogue of a one-row projection, called by the

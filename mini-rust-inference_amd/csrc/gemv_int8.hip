@@ -80,6 +80,15 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_int8(
 #pragma unroll
     for (int s = 0; s < D; ++s)
         wr[s] = __builtin_nontemporal_load(wp + (size_t)min(c0 + s, last) * pitch);
+    // the epilogue's weight scale and row-operation destination, loaded now
+    // (issued after the ring's loads, so the prologue does not wait for
+    // them), so that the epilogue waits for no load of its own
+    const int n = T * 16 + r;
+    const float sw = wscales[min(n, N - 1)];
+    RowDst dst{};
+    if constexpr (OPS) {
+        if (w == 0) dst = row_dst(in, out, n, N);
+    }
     if constexpr (FUSED && OPS) {
         if (in.up) act_swiglu<NW, XR>(in, xr, wn);
     }
@@ -154,22 +163,20 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_int8(
         for (int s = 1; s < S; ++s) acc += part[(s - 1) * kWave + l];
     }
 
-    const int n = T * 16 + r;
     if (!tile_ok) return;
     if constexpr (OPS) {  // one row: lanes 0-15 hold channels 16T .. 16T+15
         float v = (float)acc[0] * sa_value;
-        v = v * wscales[min(n, N - 1)];
+        v = v * sw;
         const float pv = __shfl_xor(v, 1);
         const bool mine = g == 0 && n < N;
         if (mine) {
             if (acc_out) acc_out[n] = acc[0];
-            row_store(in, out, n, v, pv);
+            row_store(in, dst, n, v, pv);
         }
         if (in.arg_keys) row_argmax_key(in.arg_keys, T, v, n, mine);
         return;
     }
     if (n >= N || g != 0) return;
-    const float sw = wscales[n];
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
         if (i < M) {

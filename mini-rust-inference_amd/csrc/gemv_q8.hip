@@ -168,6 +168,10 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
             wr[u][s] = __builtin_nontemporal_load(wp + (size_t)q * LB + s * 64);
         sr[u] = sp[(size_t)q * LBS];
     }
+    RowDst dst{};  // row operations: wave 0 stores the tile's outputs
+    if constexpr (OPS) {
+        if (w == 0) dst = row_dst(in, out, n, N);
+    }
     if constexpr (CH) {  // zero words of the masked areas, the zero line
         if constexpr (LAZY) {
             *reinterpret_cast<int *>(s_lap + (masked_off(4 * l) ^ 8)) = 0;
@@ -383,7 +387,7 @@ __global__ __launch_bounds__(S * TPW * kWave) void k_gemv_q8_0(
     if (w != 0 || !tile_ok) return;
     if constexpr (OPS) {  // one row: lanes 0-15 hold channels 16T .. 16T+15
         const float pv = __shfl_xor(fs[0], 1);
-        if (g == 0 && n < N) row_store(in, out, n, fs[0], pv);
+        if (g == 0 && n < N) row_store(in, dst, n, fs[0], pv);
         if (in.arg_keys) row_argmax_key(in.arg_keys, T, fs[0], n, g == 0 && n < N);
         return;
     }
