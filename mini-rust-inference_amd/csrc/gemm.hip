@@ -218,6 +218,30 @@ __global__ __launch_bounds__(WM * WN * kWave) void k_gemm_int8(
         const int piece = (2 * (f & 1) + (l >> 5)) * 16 + (l & 15);
         b_src[j] = tiles + ((size_t)T * kWave + piece) * 16;
     }
+    // The epilogue's row and channel scales.  In the large tiles they are
+    // loaded before any operand load: at the end they are a dependent memory
+    // round trip between the last MFMA and the stores (and the ring's waits
+    // count only the loads issued after the one they wait for, so these older
+    // ones change none).  Measured (us, one box): 512 x 11008 32.2 -> 32.0,
+    // 2048 x 11008 117.4 -> 116.5; in the 128 x 64 tiles, whose short K loop
+    // then starts 18 loads later, 2-3 % slower, so those load them at the end.
+    constexpr bool kEarlyScales = BM * BN >= 128 * 192;
+    float sw[TN], sa[TM][16];
+    auto load_scales = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+            sw[j] = wscales[min(16 * T0 + 32 * (wn * TN + j) + (l & 31), N - 1)];
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m =
+                    min(m0 + 32 * (wm * TM + i) + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3), M - 1);
+                sa[i][r] = sa_ptr ? sa_ptr[(size_t)m * sa_stride] : sa_value;
+            }
+    };
+    if constexpr (kEarlyScales) load_scales();
+
     const size_t a_pitch = (size_t)mg * 2 * 1024;   // bytes per K step
     const size_t b_pitch = (size_t)n_tiles * 1024;  // bytes per K slab
 
@@ -396,19 +420,10 @@ __global__ __launch_bounds__(WM * WN * kWave) void k_gemm_int8(
 
     // epilogue: lane l, register r of tile (i, j) holds row
     // m0 + 32*(wm*TM + i) + 8*(r/4) + 4*(l/32) + r%4 and column
-    // n = 16*T0 + 32*(wn*TN + j) + l%32.  The scales are loaded first: a
-    // global load issued after output stores would wait for those stores
-    // (one in-order counter covers both).
-    float sw[TN], sa[TM][16];
-#pragma unroll
-    for (int j = 0; j < TN; ++j) sw[j] = wscales[min(16 * T0 + 32 * (wn * TN + j) + (l & 31), N - 1)];
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int m = min(m0 + 32 * (wm * TM + i) + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3), M - 1);
-            sa[i][r] = sa_ptr ? sa_ptr[(size_t)m * sa_stride] : sa_value;
-        }
+    // n = 16*T0 + 32*(wn*TN + j) + l%32.  The scales are loaded before any
+    // store: a global load issued after output stores would wait for those
+    // stores (one in-order counter covers both).
+    if constexpr (!kEarlyScales) load_scales();
     if (acc_out) {  // with the int32 accumulators: element stores
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
