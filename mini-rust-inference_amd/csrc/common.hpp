@@ -250,10 +250,17 @@ struct RowOps {
     float eps = 0.0f;
     float *x_out = nullptr;         // receives a copy of x as read
     bool accum = false;             // out += the projection (a residual add)
-    // The row x is the gate half of a SwiGLU: the projection's input is
-    // x / (1 + exp(-x)) * up elementwise (ops/activation/swiglu.rs), computed
-    // as the separate SwiGLU kernel does (not with norm_w or x_out).
+    // The row x is the SiLU of the gate half of a SwiGLU (what silu_n below
+    // stores): the projection's input is x * up elementwise.  With x =
+    // g / (1 + exp(-g)) that is the SwiGLU g / (1 + exp(-g)) * u of
+    // ops/activation/swiglu.rs, rounded as the separate SwiGLU kernel rounds
+    // it (not with norm_w or x_out).
     const float *up = nullptr;
+    // Output channels [0, silu_n) are stored as v / (1 + exp(-v)), the SiLU
+    // (ops/activation/silu.rs:23-26) of a SwiGLU gate, once per channel in
+    // the producing projection instead of in every workgroup of the
+    // consuming one (not with accum or rope_n).
+    int silu_n = 0;
     // First half of the greedy argmax of the output row (sampling/mod.rs:
     // 144-151): each 16-channel tile T writes the largest key of its outputs
     // to arg_keys[T] (argmax_key: the order of the reference's max_by, the
@@ -280,7 +287,7 @@ struct RowOps {
     float *out1 = nullptr, *out2 = nullptr;
     bool any() const {
         return norm_w || x_out || accum || up || arg_keys || in_keys || rope_n > 0 || out1 ||
-               out2;
+               out2 || silu_n > 0;
     }
 };
 bool gemv_int8_supported(bool fused, size_t m, size_t n_tiles, size_t k, size_t kp);

@@ -148,7 +148,7 @@ struct ActIn {
     unsigned long long *arg_keys = nullptr;  // optional: per-tile argmax keys (RowOps)
     int accum = 0;
     const float *rope_cos = nullptr, *rope_sin = nullptr;
-    int rope_n = 0, hd = 2, seg1 = INT_MAX, seg2 = INT_MAX;
+    int rope_n = 0, hd = 2, seg1 = INT_MAX, seg2 = INT_MAX, silu_n = 0;
     float *out1 = nullptr, *out2 = nullptr;
     const unsigned long long *in_keys = nullptr;  // x is a table row picked by keys (RowOps)
     int n_in_keys = 0;
@@ -157,7 +157,8 @@ struct ActIn {
     ActIn(const float *x_, const int8_t *act_, int k, int8_t *aq, float *so, const RowOps &o)
         : x(x_), act(act_), K(k), act_q_out(aq), scale_out(so), norm_w(o.norm_w), eps(o.eps),
           x_out(o.x_out), up(o.up), arg_keys(o.arg_keys), accum(o.accum ? 1 : 0), rope_cos(o.rope_cos), rope_sin(o.rope_sin),
-          rope_n(o.rope_n), hd(o.hd), seg1(o.seg1), seg2(o.seg2), out1(o.out1), out2(o.out2),
+          rope_n(o.rope_n), hd(o.hd), seg1(o.seg1), seg2(o.seg2), silu_n(o.silu_n),
+          out1(o.out1), out2(o.out2),
           in_keys(o.in_keys), n_in_keys(o.n_in_keys), tok_out(o.tok_out) {}
 };
 
@@ -222,8 +223,10 @@ __device__ inline RowDst row_dst(const ActIn &in, float *out, int n, int N) {
 // Epilogue of the row operations for output channel n of the row with value
 // v, where pv is the value of channel n ^ 1: RoPE below rope_n, as
 // rope_apply computes it (out[2i] = x0*c - x1*s, out[2i+1] = x1*c + x0*s),
-// then the store by output segment, or the residual accumulate.
+// or the SiLU v / (1 + exp(-v)) below silu_n, then the store by output
+// segment, or the residual accumulate.
 __device__ inline void row_store(const ActIn &in, const RowDst &d, int n, float v, float pv) {
+    if (n < in.silu_n) v = v / (1.0f + expf(-v));
     if (n < in.rope_n) {
         const float a = v * d.c, b = pv * d.s;
         v = (n & 1) ? a + b : a - b;
@@ -256,8 +259,10 @@ __device__ inline void stage_load(const v4i *src, int n16, v4i (&xr)[XR]) {
 }
 
 // SwiGLU of the staged gate pieces with the up pieces staged in wn
-// (ops/activation/swiglu.rs): x = g / (1 + exp(-g)) * u, the expression of
-// the separate SwiGLU kernels, so the values are theirs.
+// (ops/activation/swiglu.rs): the gate row already holds g / (1 + exp(-g))
+// (stored so by the gate projection's epilogue, RowOps::silu_n), and x =
+// that times u, which is how the separate SwiGLU kernels evaluate
+// g / (1 + exp(-g)) * u, so the values are theirs.
 template <int S, int XR>
 __device__ inline void act_swiglu(const ActIn &in, v4i (&xr)[XR], const v4i (&wn)[XR]) {
     const int K4 = in.K / 4;
@@ -266,12 +271,7 @@ __device__ inline void act_swiglu(const ActIn &in, v4i (&xr)[XR], const v4i (&wn
         if ((int)threadIdx.x + S * kWave * e < K4) {
             const float4 g = __builtin_bit_cast(float4, xr[e]);
             const float4 u = __builtin_bit_cast(float4, wn[e]);
-            float4 y;
-            y.x = g.x / (1.0f + expf(-g.x)) * u.x;
-            y.y = g.y / (1.0f + expf(-g.y)) * u.y;
-            y.z = g.z / (1.0f + expf(-g.z)) * u.z;
-            y.w = g.w / (1.0f + expf(-g.w)) * u.w;
-            xr[e] = __builtin_bit_cast(v4i, y);
+            xr[e] = __builtin_bit_cast(v4i, float4{g.x * u.x, g.y * u.y, g.z * u.z, g.w * u.w});
         }
     }
 }

@@ -281,10 +281,11 @@ bool row_ops_ok(const float *x, const RowOps &o) {
     const bool segs = (o.seg1 == INT_MAX || o.out1) && (o.seg2 == INT_MAX || o.out2) &&
                       o.seg1 <= o.seg2 && o.seg1 >= 0;
     const bool glu = !o.up || (al(o.up) && !o.norm_w && !o.x_out);
+    const bool silu = o.silu_n == 0 || (o.silu_n > 0 && !o.accum && o.rope_n == 0);
     const bool arg = !o.arg_keys || (reinterpret_cast<uintptr_t>(o.arg_keys) & 7) == 0;
     const bool keys = !o.in_keys || ((reinterpret_cast<uintptr_t>(o.in_keys) & 7) == 0 &&
                                      o.n_in_keys > 0 && !o.up);
-    return x && al(o.norm_w) && al(o.x_out) && glu && arg && keys && rope && segs;
+    return x && al(o.norm_w) && al(o.x_out) && glu && silu && arg && keys && rope && segs;
 }
 
 bool gemv_fusable(size_t m, size_t k, const float *x) {

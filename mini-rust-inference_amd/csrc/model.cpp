@@ -357,10 +357,12 @@ mri_status block(mri_llama *m, size_t li, size_t rows, size_t start, mri_kv_cach
         copy_x = false;
         return o;
     };
-    auto in_proj = [&](const mri_weight_ref &w, const float *norm, float *out) {
+    // (silu_n: one row's leading output channels stored as their SiLU)
+    auto in_proj = [&](const mri_weight_ref &w, const float *norm, float *out, int silu_n = 0) {
         if (!fold) return m->fuse_norm ? proj_normed(m, w, rows, out, s)
                                        : proj(w, m->normed, rows, out, s);
-        const RowOps o = norm_ops(norm);
+        RowOps o = norm_ops(norm);
+        o.silu_n = silu_n;
         const float *src = xrow;
         if (o.in_keys) xrow = m->x;
         return row_proj(w, src, o, out, s);
@@ -377,7 +379,8 @@ mri_status block(mri_llama *m, size_t li, size_t rows, size_t start, mri_kv_cach
         return launch_add_rmsnorm(m->x, m->tmp, rows, g.dim, norm, g.eps, m->normed, s);
     };
     // projections whose output is added to the residual stream
-    // (up: in is a SwiGLU gate row, applied in the projection; one row only)
+    // (up: in is the SiLU of a SwiGLU gate row, multiplied by up in the
+    // projection; one row only)
     auto out_proj = [&](const mri_weight_ref &w, const float *in, const float *norm,
                         const float *up = nullptr) {
         if (fold) {
@@ -448,11 +451,11 @@ mri_status block(mri_llama *m, size_t li, size_t rows, size_t start, mri_kv_cach
                          m->attn_part, s));
     TRY(out_proj(L.w[3], m->attn, L.ffn_norm));
     xrow = m->x;
-    // gate rows, then up rows (one row: the SwiGLU runs in the down
-    // projection's prologue)
-    if (L.gu.ptr) TRY(in_proj(L.gu, L.ffn_norm, m->gu));
+    // gate rows, then up rows (one row: the gate projection stores the SiLU
+    // of its outputs, and the down projection's prologue multiplies by up)
+    if (L.gu.ptr) TRY(in_proj(L.gu, L.ffn_norm, m->gu, (int)g.ffn_dim));
     else {
-        TRY(in_proj(L.w[4], L.ffn_norm, m->gu));
+        TRY(in_proj(L.w[4], L.ffn_norm, m->gu, (int)g.ffn_dim));
         TRY(in_proj(L.w[5], L.ffn_norm, m->gu + rows * g.ffn_dim));
     }
     if (fold) return out_proj(L.w[6], m->gu, next_norm, m->gu + g.ffn_dim);
