@@ -547,12 +547,13 @@ __global__ __launch_bounds__(S * kWave) void k_gemv_w4a32(
 // 5.70) and 8 waves x 2 laps above (11008 -> 4096: 10.07-10.16 against
 // 10.62-10.78; 16 waves x 1 lap 10.05).  From 1024 tiles the up-front form
 // stays (2000 tiles, 4096 -> 32000: 22.3 against 21.6 with 4 x 1).  The
-// row-operation instances of the decode step take it below 512 tiles (the
-// o projection with its residual add, down with the SwiGLU prologue: 80.7-
-// 80.9 against 81.4 us per token); from 512 tiles (q/k/v, gate/up and
-// lm_head, with the RMSNorm prologue) it gave the same step time.
+// row-operation instances of the decode step take it at every tile count:
+// below 512 tiles (the o projection with its residual add, down with the
+// SwiGLU prologue) 80.7-80.9 against 81.4 us per token; with the one-row
+// chained form also from 512 tiles (q/k/v, gate/up and lm_head, with the
+// RMSNorm prologue): Q8_0 81.75-82.2 -> 81.1-81.2, W4A8 65.8-66.4 -> 62.3-
+// 62.4 us per token (768 tiles alone: no change).
 constexpr size_t kLazyMaxTiles = 1024;
-constexpr size_t kLazyMaxOpsTiles = 512;
 
 struct CfgQ8 {
     int s = 0, tpw = 1, rl = 1, xr = 0;  // s == 0: unsupported
@@ -582,7 +583,7 @@ inline int xr_large(int s) { return 48 / s; }
 CfgQ8 pick_q8(bool fused, size_t n_tiles, size_t m, size_t k, size_t kp, size_t G,
               bool ops = false) {
     CfgQ8 c;
-    if (fused && m == 1 && n_tiles < (ops ? kLazyMaxOpsTiles : kLazyMaxTiles)) {
+    if (fused && m == 1 && (ops || n_tiles < kLazyMaxTiles)) {
         CfgQ8 z;
         z.s = n_tiles >= 512 || G <= 16 ? 4 : 8;
         z.rl = n_tiles >= 512 ? 1 : 2;
