@@ -581,12 +581,15 @@ inline int xr_large(int s) { return 48 / s; }
 // from 512 tiles up; below, more waves per tile (8 at K <= 4096, 16 above)
 // with two laps in flight, so that the launch still has >= 2048 waves.
 CfgQ8 pick_q8(bool fused, size_t n_tiles, size_t m, size_t k, size_t kp, size_t G,
-              bool ops = false) {
+              bool ops = false, bool w4 = false) {
     CfgQ8 c;
     if (fused && m == 1 && (ops || n_tiles < kLazyMaxTiles)) {
         CfgQ8 z;
         z.s = n_tiles >= 512 || G <= 16 ? 4 : 8;
-        z.rl = n_tiles >= 512 ? 1 : 2;
+        // the 4-bit laps of the decode step's row operations: two in flight
+        // (half the bytes of a Q8_0 lap; W4A8 layer decode 62.1-62.6 -> 61.2-
+        // 61.3 us per token, where Q8_0 took 81.0 -> 81.4-81.9)
+        z.rl = n_tiles >= 512 && !(ops && w4) ? 1 : 2;
         z.lazy = true;
         const size_t nx = ceil_div(k / 4, (size_t)z.s * kWave);
         z.xr = nx <= (size_t)xr_small(z.s) ? xr_small(z.s) : nx <= (size_t)xr_large(z.s) ? xr_large(z.s) : 0;
@@ -742,7 +745,8 @@ mri_status launch_gemv_q8_0(const float *x, const int8_t *act, size_t m,
                             int32_t *block_dots, float *scales_out, hipStream_t st,
                             const RowOps &ops) {
     if (w.n_tiles == 0 || m == 0) return MRI_OK;
-    const CfgQ8 c = pick_q8(x != nullptr, w.n_tiles, m, w.k_in, w.kp, groups_of(w), ops.any());
+    const CfgQ8 c =
+        pick_q8(x != nullptr, w.n_tiles, m, w.k_in, w.kp, groups_of(w), ops.any(), w.w4);
     if (c.s == 0) return set_error(MRI_ERR_INVALID_ARGUMENT, "gemv: shape not supported");
     if (!row_ops_ok(x, ops))
         return set_error(MRI_ERR_INVALID_ARGUMENT, "gemv: row operations need the fused path");
