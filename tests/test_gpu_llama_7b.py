@@ -23,7 +23,7 @@ logit magnitude:
   measured at this geometry: at most 2e-5 on every prefill and decode row.
   This pins the layer's logic (heads, positions, RoPE, mask, the chunked
   decode attention and its combine) at the 7B sizes.
-- Q8_0 and per-channel INT8 (int8 activations): 4e-2.  A last-bit f32
+- Q8_0, W4A8 and per-channel INT8 (int8 activations): 4e-2.  A last-bit f32
   difference before a quantization moves one activation element by one
   step, and at this geometry that moves a row's logits by up to 2.6 %
   (measured: each row is either bit-identical to the oracle or 1-2.6 % off,
@@ -52,7 +52,7 @@ pytestmark = pytest.mark.gpu
 
 F32 = np.float32
 D, NH, HD, FFN, VOCAB = 4096, 32, 128, 11008, 32000
-TOL = {"q4_0": 1e-4, "q8_0": 4e-2, "int8": 4e-2}
+TOL = {"q4_0": 1e-4, "q8_0": 4e-2, "int8": 4e-2, "w4a8": 4e-2}
 POOL = ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 4))
 
 
@@ -100,6 +100,12 @@ class ParProj(O.Proj):
             def run(i):
                 a, b = cuts[i], cuts[i + 1]
                 out[:, a:b] = O.matmul_q8_0_direct(x, self.data[a * row:b * row], b - a, k)
+        elif self.fmt == "w4a8":
+            row = (k // 32) * 18
+
+            def run(i):
+                a, b = cuts[i], cuts[i + 1]
+                out[:, a:b] = O.matmul_q4_0_w4a8(x, self.data[a * row:b * row], b - a, k)
         else:
             row = (k // 32) * 18
 
@@ -116,7 +122,7 @@ def synth(fmt, rng, n, k):
     [-127, 127] (Q8_0: some -128, which the Q8_0 format allows), scales
     around 0.02 / 73; Q4_0: random nibbles (quants -8..7, standard deviation
     4.6), scales around 0.02 / 4.6."""
-    if fmt == "q4_0":
+    if fmt in ("q4_0", "w4a8"):
         raw = np.empty((n, k // 32, 18), np.uint8)
         raw[:, :, 2:] = rng.integers(0, 256, (n, k // 32, 16), dtype=np.uint8)
         d = rng.uniform(3.8e-3, 4.9e-3, (n, k // 32)).astype(np.float16).view(np.uint16)
@@ -144,6 +150,8 @@ def build_7b(fmt, seed, max_seq):
             return ParProj("int8", n, k, data, scales), Q.QMatrix.from_host(data, scales)
         if fmt == "q4_0":
             return ParProj("q4_0", n, k, data), (dev(data), n, k)
+        if fmt == "w4a8":
+            return ParProj("w4a8", n, k, data), Q.Q4Matrix.from_raw_bytes(data, n, k)
         return ParProj("q8_0", n, k, data), Q.Q8Matrix.from_raw_bytes(data, n, k)
 
     an = rng.uniform(0.8, 1.2, D).astype(F32)
@@ -166,14 +174,14 @@ def close(got, ref, what, tol):
     assert err <= tol * scale, f"{what}: max |gpu - ref| = {err:.3g} > {tol} * {scale:.3g}"
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "q8_0", "int8"])
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0", "int8", "w4a8"])
 def test_llama_7b_layer_teacher_forced(fmt):
     """Prefill 66 rows at position 0 and 64 rows at position 66, then three
     decode steps at positions 130-132 and a 4-step greedy run on a fresh
     cache, each compared with the oracle on the same tokens."""
     t = torch()
     say(f"7B layer {fmt}: building")
-    oracle, gpu, rng = build_7b(fmt, seed={"q8_0": 71, "int8": 72, "q4_0": 74}[fmt],
+    oracle, gpu, rng = build_7b(fmt, seed={"q8_0": 71, "int8": 72, "q4_0": 74, "w4a8": 77}[fmt],
                                 max_seq=160)
     tol = TOL[fmt]
     toks = rng.integers(0, VOCAB, 133).tolist()
