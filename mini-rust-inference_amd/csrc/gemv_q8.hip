@@ -547,13 +547,16 @@ __global__ __launch_bounds__(S * kWave) void k_gemv_w4a32(
 // 5.70) and 8 waves x 2 laps above (11008 -> 4096: 10.07-10.16 against
 // 10.62-10.78; 16 waves x 1 lap 10.05).  From 1024 tiles the up-front form
 // stays (2000 tiles, 4096 -> 32000: 22.3 against 21.6 with 4 x 1).  The
-// row-operation instances of the decode step take it at every tile count:
-// below 512 tiles (the o projection with its residual add, down with the
-// SwiGLU prologue) 80.7-80.9 against 81.4 us per token; with the one-row
-// chained form also from 512 tiles (q/k/v, gate/up and lm_head, with the
-// RMSNorm prologue): Q8_0 81.75-82.2 -> 81.1-81.2, W4A8 65.8-66.4 -> 62.3-
-// 62.4 us per token (768 tiles alone: no change).
+// row-operation instances of the decode step take it below 512 tiles (the
+// o projection with its residual add, down with the SwiGLU prologue: 80.7-
+// 80.9 against 81.4 us per token) and, with the one-row chained form, also
+// from 512 tiles (q/k/v and gate/up with the RMSNorm prologue, and the W4A8
+// lm_head): Q8_0 81.75-82.2 -> 81.1-81.2, W4A8 65.8-66.4 -> 62.3-62.4 us per
+// token.  The Q8_0 lm_head (2000 tiles) keeps the up-front form, like the
+// matmul entry points from 1024 tiles: lap-wise it took 24.2 against 23.3
+// us (rocprof), and the step 81.3 against 80.9-81.1.
 constexpr size_t kLazyMaxTiles = 1024;
+constexpr size_t kLazyMaxOpsTiles = 1536;  // Q8_0 row operations; W4A8: every count
 
 struct CfgQ8 {
     int s = 0, tpw = 1, rl = 1, xr = 0;  // s == 0: unsupported
@@ -583,7 +586,8 @@ inline int xr_large(int s) { return 48 / s; }
 CfgQ8 pick_q8(bool fused, size_t n_tiles, size_t m, size_t k, size_t kp, size_t G,
               bool ops = false, bool w4 = false) {
     CfgQ8 c;
-    if (fused && m == 1 && (ops || n_tiles < kLazyMaxTiles)) {
+    if (fused && m == 1 &&
+        n_tiles < (ops ? (w4 ? SIZE_MAX : kLazyMaxOpsTiles) : kLazyMaxTiles)) {
         CfgQ8 z;
         z.s = n_tiles >= 512 || G <= 16 ? 4 : 8;
         // the 4-bit laps of the decode step's row operations: two in flight
