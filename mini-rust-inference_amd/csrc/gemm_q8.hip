@@ -509,8 +509,12 @@ bool gemm_q8_supported(size_t m, const Q8MatrixDev &w) {
 
 // act: quantized rows [m][w.kp], chunk-permuted (launch_quantize_rows with
 // the Q8_0 layout); sa_rows: their scales.
-// Tiles of 128 rows x 64 channels, 8 waves of 32 x 32 (about 78 KiB of LDS:
-// two workgroups per CU, four waves per SIMD).  With the MFMA results in
+// Tiles of 128 rows x 64 channels, 8 waves of 32 x 32, two LDS stages
+// (about 52 KiB; the 126 VGPRs hold two workgroups per CU, four waves per
+// SIMD, either way).  Three stages took 1-2 % longer (M = 512, K = 4096:
+// N = 12288 86.5 against 88.2 us, N = 32000 204.5 against 208.1, N = 4096
+// 39.5 against 40.1; K = 11008 79.9 against 81.6; bit-identical).  With
+// the MFMA results in
 // VGPRs (see the build flags) 128 x 64 tiles beat 128 x 128 tiles of 8
 // waves at every N measured (M = 512, K = 4096: 164.5 against 176.4 us at
 // N = 22016, 223.5 against 234 at N = 32000); 8 waves of 32 x 32 rather
@@ -518,8 +522,8 @@ bool gemm_q8_supported(size_t m, const Q8MatrixDev &w) {
 // latency floor from 43 to 39 us (512 x 11008 -> 4096: 108 against 117).
 mri_status launch_gemm_q8_0(const int8_t *act, size_t m, const float *sa_rows,
                             const Q8MatrixDev &w, float *out, void *ws, hipStream_t s) {
-    if (w.w4) return launch_q8_inst<kQ8BM, kQ8BN, 4, 2, 3, true>(act, m, sa_rows, w, out, ws, s);
-    return launch_q8_inst<kQ8BM, kQ8BN, 4, 2, 3, false>(act, m, sa_rows, w, out, ws, s);
+    if (w.w4) return launch_q8_inst<kQ8BM, kQ8BN, 4, 2, 2, true>(act, m, sa_rows, w, out, ws, s);
+    return launch_q8_inst<kQ8BM, kQ8BN, 4, 2, 2, false>(act, m, sa_rows, w, out, ws, s);
 }
 
 // [tile counters (kGemmWsCounters ints, shared with the INT8 GEMM's)]
