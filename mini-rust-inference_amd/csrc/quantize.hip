@@ -214,11 +214,16 @@ inline int rows_nv(const float *x, size_t k, size_t ld, const int8_t *q_pad,
 // GLU rows (two loads per element) run 1024 threads per row: with 256 the
 // 512 rows of a prefill leave too few loads in flight (512 x 11008: 16.7 us
 // at 256 threads, 13.0 us at 1024, against 11.7 + 13.0 us for the SwiGLU
-// kernel followed by the separate pass).
-template <bool GLU>
+// kernel followed by the separate pass).  So do up to 32 rows, where the
+// launch is a handful of workgroups and its latency is the whole cost
+// (matmul_q8_0_direct at 2-32 x 4096 -> 11008: 0.02-0.15 us less per call,
+// the same bytes).
+template <bool GLU, int TH = GLU ? 1024 : kThreads>
 void launch_rows(const float *x, size_t m, size_t k, size_t ld, int perm, int8_t *q_pad,
                  int8_t *q_plain, float *scales, hipStream_t s) {
-    constexpr int TH = GLU ? 1024 : kThreads;
+    if constexpr (!GLU && TH == kThreads) {
+        if (m <= 32) return launch_rows<false, 1024>(x, m, k, ld, perm, q_pad, q_plain, scales, s);
+    }
     const dim3 grid((unsigned)m), block(TH);
     switch (rows_nv(x, k, ld, q_pad, q_plain, TH)) {
     case 4: hipLaunchKernelGGL((k_quantize_rows<4, GLU, TH>), grid, block, 0, s, x, k, ld, perm, q_pad, q_plain, scales); break;
