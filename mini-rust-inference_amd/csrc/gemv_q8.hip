@@ -675,7 +675,9 @@ void dispatch_q8_dbg(bool dbg, CfgQ8 c, ActIn in, size_t m, const float *sa_rows
 }
 
 // W4A32 on 4-bit lap blocks: rows in groups of up to four per launch,
-// four waves per tile from 512 tiles up, else 8 (K <= 4096) or 16.  LDS:
+// four waves per tile from 512 tiles up (one lap in flight: two took 8.51
+// against 8.07 us at 4096 -> 11008, 18.4 against 17.0 at 4096 -> 32000),
+// else 8 (K <= 4096) or 16.  LDS:
 // the MR f32 rows (at most kMaxLds) plus S - 1 waves' partial sums of MR x
 // 16 outputs (at most 3.75 KiB), so an instance may take more than 64 KiB
 // and declares its maximum once per device.
