@@ -355,19 +355,23 @@ __global__ __launch_bounds__(256) void k_attention(
 }
 
 // Decode form (one query row), split over the keys.  Workgroup (chunk c,
-// head h) takes keys [64c, 64c + 64) of the L = start_pos + 1 visible ones,
-// 16 per wave.  Each load instruction of a wave reads whole key (and value)
-// rows, HD/4 lanes of 16 bytes per row, so the 64 KiB of a chunk arrive as
-// contiguous 512-byte rows (with one lane per key, each instruction read 16
+// head h) takes keys [CK c, CK c + CK) of the L = start_pos + 1 visible ones,
+// CK = 16 NW, 16 per wave (NW = 8: 128 keys; in the 7B layer's decode step
+// at 512-640 keys, 64-key chunks of four waves took 0.2-0.7 us a token
+// longer, twice as many chunks to publish and combine, and 256-key chunks
+// of 16 waves 1.3-2.4 us longer).  Each load instruction
+// of a wave reads whole key (and value) rows, HD/4 lanes of 16 bytes per
+// row, so a chunk arrives as contiguous 512-byte rows (with one lane per
+// key, each instruction read 16
 // bytes of 64 different rows: 10.0 against 9.3 us a call at 512-640 keys,
 // 32 heads of 128); all of a thread's key and value loads are issued before
 // the first use.  The rest of a call is its tail: the partial stores, the
 // count and the combine, three memory round trips in sequence.  A key's dot is four products per
 // lane, then the HD/4 lanes added by a butterfly; then the chunk's max m_c,
 // weights e_j = exp(s_j - m_c) and their sum l_c (every wave computes them
-// from the 64 scores in LDS), and the chunk's weighted value sum o_c (per
-// lane in key order, then the lane groups and the four waves added in
-// order).  The chunk's (m_c, l_c, o_c) go to part ([heads][chunks][HD+2])
+// from the CK scores in LDS, CK / 64 a lane), and the chunk's weighted
+// value sum o_c (per lane in key order, then the lane groups and the NW
+// waves added in order).  The chunk's (m_c, l_c, o_c) go to part ([heads][chunks][HD+2])
 // through device-scope (sc1) stores, complete before the workgroup counts
 // itself on its head's counter (relaxed, device scope); the workgroup that
 // counts last for a head combines the chunks (attn_combine) and resets the
@@ -421,8 +425,8 @@ __device__ inline void attn_combine(const float *ph, int nch, int d, float *out)
     out[d] = o / l;
 }
 
-template <int HD>
-__global__ __launch_bounds__(256) void k_attn_decode_part(
+template <int HD, int NW>
+__global__ __launch_bounds__(NW * 64) void k_attn_decode_part(
     const float *__restrict__ q, const float *__restrict__ kc, const float *__restrict__ vc,
     int kvd, int L, int groups, float scale, float *__restrict__ part, int *__restrict__ cnt,
     float *__restrict__ out) {
@@ -431,14 +435,15 @@ __global__ __launch_bounds__(256) void k_attn_decode_part(
     // Wave wv holds keys 16 wv .. 16 wv + 15 of the chunk: key 16 wv + KPI i
     // + sub in load i, lane (sub, d4) with float4 d4 of the row.
     constexpr int R4 = HD / 4, KPI = kWave / R4, NI = 16 / KPI;
-    static_assert(HD % 64 == 0 && HD <= 256, "head dim");
-    __shared__ float s_s[64];
-    __shared__ __attribute__((aligned(16))) float s_o[4][HD];  // written as float4
+    constexpr int CK = 16 * NW, NS = CK / kWave;  // keys of a chunk, scores a lane
+    static_assert(HD % 64 == 0 && HD <= 256 && NW % 4 == 0, "head dim, waves");
+    __shared__ float s_s[CK];
+    __shared__ __attribute__((aligned(16))) float s_o[NW][HD];  // written as float4
     __shared__ int s_last;
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     const int sub = lane / R4, d4 = lane % R4;
     const int c = blockIdx.x, h = blockIdx.y, kh = h / groups, nch = gridDim.x;
-    const int j0 = 64 * c + 16 * wv + sub;
+    const int j0 = CK * c + 16 * wv + sub;
     float4 kr[NI], vr[NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
@@ -469,26 +474,44 @@ __global__ __launch_bounds__(256) void k_attn_decode_part(
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             const int j = j0 + KPI * i;
-            s_s[j - 64 * c] = j < L ? sc[i] * scale : -INFINITY;
+            s_s[j - CK * c] = j < L ? sc[i] * scale : -INFINITY;
         }
     }
     __syncthreads();
     // every wave: the chunk's max m_c, weights e_j = exp(s_j - m_c), sum l_c
-    const float sv = s_s[lane];
-    const float m = wave_max(sv);
-    const float e = 64 * c + lane < L ? expf(sv - m) : 0.0f;
-    const float lsum = wave_sum(e);
+    // (lane l holds keys l, l + 64, ..)
+    float sv[NS], e[NS];
+    float mm = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < NS; ++u) {
+        sv[u] = s_s[lane + kWave * u];
+        mm = fmaxf(mm, sv[u]);
+    }
+    const float m = wave_max(mm);
+    float es = 0.0f;
+#pragma unroll
+    for (int u = 0; u < NS; ++u) {
+        e[u] = CK * c + kWave * u + lane < L ? expf(sv[u] - m) : 0.0f;
+        es = es + e[u];
+    }
+    const float lsum = wave_sum(es);
     float *pc = part + ((size_t)h * nch + c) * (HD + 2);
     if (t == 0) {
         __hip_atomic_store(pc, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(pc + 1, lsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     // weighted values of this wave's keys, in key order per lane; the KPI
-    // lane groups, then the four waves, added in order
+    // lane groups, then the NW waves, added in order
     float4 o = float4{0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-        const float w = __shfl(e, 16 * wv + KPI * i + sub, kWave);
+        const int kx = 16 * wv + KPI * i + sub;  // key of the chunk
+        float w = __shfl(e[0], kx % kWave, kWave);
+#pragma unroll
+        for (int u = 1; u < NS; ++u) {
+            const float wu = __shfl(e[u], kx % kWave, kWave);
+            w = kx / kWave == u ? wu : w;
+        }
         float m0 = w * vr[i].x;
         o.x = o.x + m0;
         m0 = w * vr[i].y;
@@ -507,9 +530,12 @@ __global__ __launch_bounds__(256) void k_attn_decode_part(
     }
     if (sub == 0) reinterpret_cast<float4 *>(s_o[wv])[d4] = o;
     __syncthreads();
-    for (int d = t; d < HD; d += 256)
-        __hip_atomic_store(pc + 2 + d, ((s_o[0][d] + s_o[1][d]) + s_o[2][d]) + s_o[3][d],
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int d = t; d < HD; d += NW * kWave) {
+        float a = s_o[0][d];
+#pragma unroll
+        for (int u = 1; u < NW; ++u) a = a + s_o[u][d];
+        __hip_atomic_store(pc + 2 + d, a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's partials are at the device
     __syncthreads();
     if (t == 0)
@@ -1252,11 +1278,12 @@ mri_status attn_dispatch(const float *q, int qs, int qd, const float *kc, const 
         return MRI_OK;
     }
     if (seq_q == 1 && part && L <= 1024 * 64 && rows16) {  // the combine holds <= 1024 chunks
-        const int nch = (L + 63) / 64;
+        constexpr int NW = 8;  // waves of a chunk, 16 keys each
+        const int nch = (L + 16 * NW - 1) / (16 * NW);
         const float scale = 1.0f / sqrtf((float)HD);
         // [head counters, padded to 64 words][partials]
         int *cnt = reinterpret_cast<int *>(part);
-        hipLaunchKernelGGL(k_attn_decode_part<HD>, dim3(nch, n_heads), dim3(256), 0, s, q, kc,
+        hipLaunchKernelGGL((k_attn_decode_part<HD, NW>), dim3(nch, n_heads), dim3(NW * kWave), 0, s, q, kc,
                            vc, kvd, L, groups, scale, part + attn_cnt_words(n_heads), cnt, out);
         MRI_LAUNCHED("k_attn_decode_part");
         return MRI_OK;
